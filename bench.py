@@ -1,0 +1,319 @@
+"""Benchmark: BVH build + exact k-NN on one MI355X.
+
+Default workload: 1,048,576 uniform 3-D points,
+1,048,576 uniform queries, k = 16, fp32.  One step = build the BVH, Morton-
+order the queries, run the traversal — the whole hot path, inputs resident in
+HBM.  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
+                    [--cpu-sample Q] [--no-cpu-baseline]
+
+The synthetic workloads of every BASELINE config are defined here
+(``make_workload``) and shared with the parity tests.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+# ---------------------------------------------------------------------------
+# Workloads (seeds and shapes as fixed for the BASELINE configs; generated on
+# the CPU so GPU, oracle and CPU baseline see bit-identical inputs)
+# ---------------------------------------------------------------------------
+CONFIGS = {
+    "cfg1": "3D k-NN, 10,000 uniform points / 10,000 uniform queries, k=4",
+    "cfg2": "3D k-NN, 1,048,576 uniform points / 1,048,576 uniform queries, k=16",
+    "cfg3": "batched 3D k-NN, 32 x 65,536 Gaussian-mixture clouds, displaced self-queries, k=16",
+    "cfg4": "2D k-NN, 4,194,304 uniform points, jittered self-queries, k=8",
+    "cfg5": "ragged 3D k-NN, 64 torus clouds of 1,000-200,000 points, AABB-uniform queries, k=32",
+}
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator("cpu").manual_seed(seed)
+
+
+def make_workload(name: str, scale: float = 1.0) -> dict:
+    """Return CPU tensors for a BASELINE config.
+
+    ``scale`` < 1 shrinks the point/query counts (same distributions and
+    seeds) for quick parity runs; 1.0 is the configured size.
+    """
+    if name == "cfg1":
+        n = max(int(10_000 * scale), 16)
+        pts = torch.rand((n, 3), generator=_gen(1001))
+        q = torch.rand((n, 3), generator=_gen(1002))
+        return {"kind": "single", "points": pts, "queries": q, "k": 4}
+    if name == "cfg2":
+        n = max(int((1 << 20) * scale), 16)
+        pts = torch.rand((n, 3), generator=_gen(2001))
+        q = torch.rand((n, 3), generator=_gen(2002))
+        return {"kind": "single", "points": pts, "queries": q, "k": 16}
+    if name == "cfg3":
+        B, n = 32, max(int(65_536 * scale), 16)
+        centres = torch.rand((B, 8, 3), generator=_gen(3001))
+        comp = torch.randint(0, 8, (B, n), generator=_gen(3002))
+        base = torch.gather(centres, 1, comp.unsqueeze(-1).expand(-1, -1, 3))
+        pts = base + 0.02 * torch.randn((B, n, 3), generator=_gen(3003))
+        q = pts + 0.005 * torch.randn((B, n, 3), generator=_gen(3004))
+        return {"kind": "batched", "points": pts.contiguous(), "queries": q.contiguous(), "k": 16}
+    if name == "cfg4":
+        n = max(int((1 << 22) * scale), 16)
+        pts = torch.rand((n, 2), generator=_gen(4001))
+        q = pts + 0.01 * torch.randn((n, 2), generator=_gen(4002))
+        return {"kind": "single", "points": pts, "queries": q.contiguous(), "k": 8}
+    if name == "cfg5":
+        B = 64
+        sizes = torch.randint(1_000, 200_001, (B,), generator=_gen(5001))
+        sizes = [max(int(s * scale), 40) for s in sizes.tolist()]
+        total = sum(sizes)
+        # Angles uniform in [0, 2pi)^2 (not area-uniform on the torus).
+        ang = torch.rand((total, 2), generator=_gen(5002)) * (2.0 * math.pi)
+        theta, phi = ang[:, 0], ang[:, 1]
+        R, r = 0.35, 0.1
+        ring = R + r * torch.cos(phi)
+        pts = torch.stack((ring * torch.cos(theta), ring * torch.sin(theta), r * torch.sin(phi)), 1)
+        pts = pts + 0.5 + 0.002 * torch.randn((total, 3), generator=_gen(5003))
+        offsets = [0]
+        for s in sizes:
+            offsets.append(offsets[-1] + s)
+        u = torch.rand((total, 3), generator=_gen(5004))
+        q = torch.empty_like(pts)
+        for b in range(B):
+            p0, p1 = offsets[b], offsets[b + 1]
+            lo = pts[p0:p1].amin(0)
+            hi = pts[p0:p1].amax(0)
+            q[p0:p1] = lo + u[p0:p1] * (hi - lo)
+        off = torch.tensor(offsets, dtype=torch.int64)
+        return {"kind": "ragged", "points": pts.contiguous(), "queries": q.contiguous(),
+                "k": 32, "offsets": off, "query_offsets": off.clone()}
+    raise ValueError(f"unknown config {name!r}")
+
+
+# ---------------------------------------------------------------------------
+# Algorithmic bytes (fixed formulas)
+# ---------------------------------------------------------------------------
+def real_node_count(n: int) -> int:
+    L = (n - 1).bit_length()
+    return 2 * n - 1 + bin((1 << L) - n).count("1")
+
+
+def build_bytes(n: int, D: int) -> int:
+    return n * (12 * D + 80) + 8 * D * real_node_count(n)
+
+
+def qsort_bytes(q: int, D: int) -> int:
+    return q * (4 * D + 72)
+
+
+def knn_bytes(q: int, D: int, k: int) -> int:
+    return q * (4 * D + 4 + 12 * k)
+
+
+HBM_PEAK_GBS = 8000.0
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's brute-force test oracle (tests/test_knn.py:10-12)
+# with the (distance, index) tie rule, timed on a bounded sample of queries.
+# ---------------------------------------------------------------------------
+def cpu_baseline(points: torch.Tensor, queries: torch.Tensor, k: int, sample: int) -> dict:
+    from oracle.torch_bruteforce import knn_bruteforce
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = _gen(99)
+    sel = torch.randperm(queries.shape[0], generator=g)[:sample]
+    qs = queries[sel].contiguous()
+    knn_bruteforce(points, qs[:8], k)  # warm-up
+    t0 = time.perf_counter()
+    knn_bruteforce(points, qs, k)
+    dt = time.perf_counter() - t0
+    qps = sample / dt
+    cpu_model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": qps,
+        "unit": "queries/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{sample} of {queries.shape[0]} queries (seeded) against all "
+                   f"{points.shape[0]} points, torch brute force in chunks; "
+                   f"{dt:.2f} s measured; extrapolated full-query time "
+                   f"{queries.shape[0] / qps:.1f} s; CPU: {cpu_model}"),
+    }
+
+
+# ---------------------------------------------------------------------------
+# Bench
+# ---------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-sample", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md, not implemented", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+
+    import torchbvh_amd as tb
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config)
+    k = w["k"]
+    pts = w["points"].to(dev)
+    qs = w["queries"].to(dev)
+    D = pts.shape[-1]
+    kind = w["kind"]
+    if kind == "ragged":
+        off = w["offsets"].to(dev)
+        qoff = w["query_offsets"].to(dev)
+        total_q = qs.shape[0]
+        sizes = w["offsets"].diff().tolist()
+        b_bytes = sum(build_bytes(n, D) for n in sizes)
+    elif kind == "batched":
+        total_q = qs.shape[0] * qs.shape[1]
+        b_bytes = qs.shape[0] * build_bytes(pts.shape[1], D)
+    else:
+        total_q = qs.shape[0]
+        b_bytes = build_bytes(pts.shape[0], D)
+    s_bytes = qsort_bytes(total_q, D)
+    n_bytes = knn_bytes(total_q, D, k)
+
+    def step(events=None):
+        if events:
+            events[0].record()
+        if kind == "ragged":
+            bvh = tb.build_bvh(pts, batch_offsets=off)
+        else:
+            bvh = tb.build_bvh(pts)
+        if events:
+            events[1].record()
+        if kind == "ragged":
+            out = tb.query_knn(bvh, qs, k, query_offsets=qoff)
+        else:
+            out = tb.query_knn(bvh, qs, k)
+        if events:
+            events[2].record()
+        return bvh, out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    build_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    query_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+
+    # Split the query phase into ordering and traversal with events around the
+    # native calls on the current stream (the traversal is a single kernel).
+    from torchbvh_amd._native import _C
+
+    sort_ms = trav_ms = 0.0
+    if kind != "ragged":
+        bvh, _ = step()
+        data = bvh
+        qb = qs if kind == "batched" else qs.unsqueeze(0)
+        smin = data["scene_min"] if kind == "batched" else data["scene_min"].unsqueeze(0)
+        smax = data["scene_max"] if kind == "batched" else data["scene_max"].unsqueeze(0)
+        nodes = data["node_aabbs"] if kind == "batched" else data["node_aabbs"].unsqueeze(0)
+        sidx = data["sorted_indices"] if kind == "batched" else data["sorted_indices"].unsqueeze(0)
+        reps = max(args.steps, 5)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3 * reps)]
+        torch.cuda.synchronize()
+        for r in range(reps):
+            e[3 * r].record()
+            order = _C.morton_sort_queries_narrow(qb, smin, smax)
+            e[3 * r + 1].record()
+            _C.query_knn_batched_cached_bounds_ordered(
+                nodes, sidx, qb, order, data["num_leaves"], data["num_real_nodes"], D, k)
+            e[3 * r + 2].record()
+        torch.cuda.synchronize()
+        sort_ms = sum(e[3 * r].elapsed_time(e[3 * r + 1]) for r in range(reps)) / reps
+        trav_ms = sum(e[3 * r + 1].elapsed_time(e[3 * r + 2]) for r in range(reps)) / reps
+
+    value = total_q / (ms_per_step * 1e-3)
+    trav_gbs = n_bytes / (trav_ms * 1e-3) / 1e9 if trav_ms > 0 else None
+    line = {
+        "metric": "k-NN queries/sec + BVH build ms, 1M pts/1M queries k=16 3D fp32, 1 GPU",
+        "value": value,
+        "unit": "queries/s (end-to-end: build + query ordering + traversal per step)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch CPU generator, BASELINE config shapes)",
+        "config": {
+            "workload": CONFIGS[args.config],
+            "config_id": args.config,
+            "points": int(pts.numel() // D),
+            "queries": int(total_q),
+            "k": k,
+            "dim": D,
+        },
+        "build_ms": build_ms,
+        "query_ms": query_ms,
+        "query_sort_ms": sort_ms,
+        "traversal_ms": trav_ms,
+        "queries_per_s_excl_build": total_q / (query_ms * 1e-3) if query_ms > 0 else None,
+        "build_hbm_frac_algorithmic": (b_bytes / (build_ms * 1e-3) / 1e9) / HBM_PEAK_GBS,
+        "query_sort_hbm_frac_algorithmic": ((s_bytes / (sort_ms * 1e-3) / 1e9) / HBM_PEAK_GBS
+                                            if sort_ms > 0 else None),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "knn_kernel (traversal)",
+            "achieved": trav_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": (trav_gbs / HBM_PEAK_GBS) if trav_gbs else None,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        cpu_pts = w["points"] if kind != "batched" else w["points"][0]
+        cpu_q = w["queries"] if kind != "batched" else w["queries"][0]
+        if kind == "ragged":
+            cpu_pts = w["points"][: w["offsets"][1]]
+            cpu_q = w["queries"][: w["query_offsets"][1]]
+        line["cpu_baseline"] = cpu_baseline(cpu_pts, cpu_q, k, min(args.cpu_sample, cpu_q.shape[0]))
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,162 @@
+/*
+ * torchbvh_amd C ABI — BVH build and exact k-NN for 2-D/3-D fp32 point clouds
+ * on AMD Instinct MI355X (gfx950).
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as `void*`; a null stream means the legacy default stream).  The
+ * library never allocates device memory: callers query a workspace size, pass
+ * a device buffer of at least that many bytes, and own every output buffer.
+ * All launches are asynchronous on `stream`; no entry point synchronises the
+ * host.  Entry points are reentrant; calls that share one workspace buffer on
+ * overlapping streams race, exactly as two kernels writing one buffer would.
+ *
+ * Return value: TBVH_OK (0) on success, otherwise an error code, with a
+ * human-readable message available from tbvh_last_error() on the calling
+ * thread.
+ *
+ * Layouts (identical to the reference's handle payload):
+ *   points          [B, N, D] fp32 (batched) or [T, D] packed (ragged)
+ *   node_aabbs      [B, nr, 2D] fp32, row = (lo_0..lo_{D-1}, hi_0..hi_{D-1}),
+ *                   real nodes of the implicit tree in level order
+ *   sorted_indices  [B, N] int64, per-cloud (local) original point index of
+ *                   each Morton-ordered leaf
+ *   scene_min/max   [B, D] fp32
+ *   left/right_child_mem, mem_to_leaf   [nr] int32 (ragged: packed per cloud)
+ *   order           [B, M] int64 local query indices in Morton order
+ *   out_indices     [B, M, K] int64 local point indices, ascending by
+ *                   (squared distance, index)
+ *   out_distances   [B, M, K] fp32 squared distances
+ */
+#ifndef TORCHBVH_AMD_H
+#define TORCHBVH_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TBVH_OK = 0,
+    TBVH_ERR_INVALID_ARGUMENT = 1,
+    TBVH_ERR_WORKSPACE_TOO_SMALL = 2,
+    TBVH_ERR_HIP = 3,
+};
+
+/* ABI version of this header; bumped on any signature change. */
+#define TBVH_ABI_VERSION 1
+int tbvh_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* tbvh_last_error(void);
+
+/* ---- implicit-tree closed forms (host only; no GPU work) -------------------
+ * Replace implicit_tree.cuh:55-68 (`virtual_leaves`, `real_node_count`,
+ * `leaf_level`) for sizing outputs on the host.  n >= 1 and n <= INT32_MAX. */
+int     tbvh_leaf_level(int64_t n);
+int64_t tbvh_virtual_leaves(int64_t n);
+int64_t tbvh_real_node_count(int64_t n);
+
+/* ---- batched build ----------------------------------------------------------
+ * Replaces `build_bvh_batched_cooperative` (torchbvh/csrc/bindings.cpp:155-157,
+ * torchbvh/csrc/bvh_build.cu:679-721): per-cloud AABB, 30-bit (3-D) or 32-bit
+ * (2-D) Morton codes, stable key/value sort, implicit-tree node AABBs and the
+ * traversal arrays, for B clouds of N points.  Requires B >= 1, N >= 1,
+ * B*N <= INT32_MAX, D in {2,3}.  `left_child_mem`, `right_child_mem` and
+ * `mem_to_leaf` are [nr] (shared by all clouds, as in the reference). */
+int tbvh_build_workspace_size(int64_t B, int64_t N, int D, size_t* bytes);
+int tbvh_build(const float* points, int64_t B, int64_t N, int D,
+               float* node_aabbs, int64_t* sorted_indices,
+               float* scene_min, float* scene_max,
+               int32_t* left_child_mem, int32_t* right_child_mem,
+               int32_t* mem_to_leaf,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- ragged build -------------------------------------------------------------
+ * Replaces the per-segment Python loop of `_build_bvh_ragged`
+ * (torchbvh/_query.py:68-85), which calls the batched build once per cloud,
+ * with one segmented launch sequence.  `offsets` is a device int64 [B+1]
+ * array (0 = offsets[0] < offsets[1] < ... < offsets[B] = total).  Outputs
+ * are the per-cloud results concatenated: node_aabbs [sum nr_b, 2D],
+ * sorted_indices [total] (local indices), scene_min/max [B, D], the three
+ * traversal arrays [sum nr_b], and node_offsets [B+1] int64 (device) giving
+ * each cloud's first node row.  `total_nodes` = sum of real_node_count(n_b)
+ * (the caller sizes the outputs with it).  Offsets are validated by the
+ * caller; the library trusts them. */
+int tbvh_build_ragged_workspace_size(int64_t B, int64_t total, int D,
+                                     size_t* bytes);
+int tbvh_build_ragged(const float* points, const int64_t* offsets,
+                      int64_t B, int64_t total, int D,
+                      float* node_aabbs, int64_t* sorted_indices,
+                      float* scene_min, float* scene_max,
+                      int32_t* left_child_mem, int32_t* right_child_mem,
+                      int32_t* mem_to_leaf, int64_t* node_offsets,
+                      int64_t total_nodes,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- query ordering -----------------------------------------------------------
+ * Replaces `morton_sort_queries_narrow` (torchbvh/csrc/morton_sort.cu:212-287):
+ * Morton codes of the queries against the BVH's scene bounds, stable sort,
+ * int64 order [B, M].  M may be 0 (nothing is launched). */
+int tbvh_sort_queries_workspace_size(int64_t B, int64_t M, int D,
+                                     size_t* bytes);
+int tbvh_sort_queries(const float* queries, int64_t B, int64_t M, int D,
+                      const float* scene_min, const float* scene_max,
+                      int64_t* order,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Ragged form: queries [total_q, D] packed by `query_offsets` (device int64
+ * [B+1]); `order` [total_q] receives local query indices per cloud.  Replaces
+ * the per-segment calls made by `_query_knn_ragged` (torchbvh/_query.py:347-360). */
+int tbvh_sort_queries_ragged_workspace_size(int64_t B, int64_t total_q, int D,
+                                            size_t* bytes);
+int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets,
+                             int64_t B, int64_t total_q, int D,
+                             const float* scene_min, const float* scene_max,
+                             int64_t* order,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ---- diagnostic: Morton codes ------------------------------------------------------
+ * No counterpart in the reference's FFI (its codes stay inside
+ * `narrow_morton_sort_batched`, bvh_build.cu:551-600, and
+ * `morton_sort_queries_narrow_impl`, morton_sort.cu:212-262).  Exposes the
+ * library's Morton kernel so parity tests can compare codes bit for bit:
+ * codes [B*M] u32 of rows [B, M, D] against per-cloud bounds [B, D].  Uses the
+ * query-ordering workspace size. */
+int tbvh_morton_codes(const float* rows, int64_t B, int64_t M, int D,
+                      const float* scene_min, const float* scene_max,
+                      uint32_t* codes,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- exact k-NN ------------------------------------------------------------------
+ * Replaces `query_knn_batched_cached_bounds` and
+ * `query_knn_batched_cached_bounds_ordered` (torchbvh/csrc/knn_query.cu:419-446,
+ * dispatch and checks :350-417).  `order` may be NULL (queries are launched in
+ * input order).  k in {4, 8, 16, 32}; num_leaves >= k.  Results are the k
+ * smallest (squared distance, index) pairs in lexicographic order, so exact
+ * distance ties resolve to the lower point index. */
+int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices,
+             const float* queries, const int64_t* order,
+             int64_t B, int64_t M, int64_t num_leaves, int64_t num_real_nodes,
+             int D, int k,
+             int64_t* out_indices, float* out_distances, void* stream);
+
+/* Ragged form over the packed outputs of tbvh_build_ragged.  point_offsets,
+ * node_offsets and query_offsets are device int64 [B+1]; `order` (local query
+ * indices from tbvh_sort_queries_ragged) may be NULL.  Every cloud must hold
+ * at least k points (checked by the caller).  Output rows follow the packed
+ * query rows; indices are local to each cloud. */
+int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
+                    const int64_t* point_offsets, const int64_t* node_offsets,
+                    const float* queries, const int64_t* query_offsets,
+                    const int64_t* order,
+                    int64_t B, int64_t total_q, int D, int k,
+                    int64_t* out_indices, float* out_distances, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHBVH_AMD_H */

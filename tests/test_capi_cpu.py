@@ -1,0 +1,119 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+public header declares, its closed forms agree with the oracle, and argument
+errors are reported (status + message) before anything is launched."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import oracle
+from torchbvh_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "torchbvh_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tbvh_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_functions()
+    for required in ("tbvh_build", "tbvh_build_workspace_size", "tbvh_build_ragged",
+                     "tbvh_sort_queries", "tbvh_sort_queries_ragged", "tbvh_knn",
+                     "tbvh_knn_ragged", "tbvh_last_error", "tbvh_abi_version"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _native.load()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, f"not exported: {missing}"
+    assert L.tbvh_abi_version() == 1
+
+
+@pytest.mark.parametrize("n", list(range(1, 300)) + [10_000, 65_536, 1 << 20, 4_194_304, 200_000, 1 << 30])
+def test_closed_forms_match_oracle(n):
+    assert _native.leaf_level(n) == oracle.leaf_level(n)
+    assert _native.virtual_leaves(n) == oracle.virtual_leaves(n)
+    assert _native.real_node_count(n) == oracle.real_node_count(n)
+
+
+def test_closed_forms_reject_out_of_range():
+    assert _native.real_node_count(0) == -1
+    assert _native.real_node_count((1 << 30) + 1) == -1
+
+
+def _err(L) -> str:
+    return L.tbvh_last_error().decode()
+
+
+FAKE = ctypes.c_void_p(0x100000)  # never dereferenced: every call below fails validation
+
+
+def test_build_argument_errors():
+    L = _native.load()
+    size = ctypes.c_size_t()
+    assert L.tbvh_build_workspace_size(1, 10, 4, ctypes.byref(size)) == 1
+    assert "D must be 2 or 3" in _err(L)
+    assert L.tbvh_build_workspace_size(0, 10, 3, ctypes.byref(size)) == 1
+    assert L.tbvh_build_workspace_size(1 << 20, 1 << 12, 3, ctypes.byref(size)) == 1
+    assert "int32" in _err(L)
+    assert L.tbvh_build_workspace_size(2, 1000, 3, ctypes.byref(size)) == 0
+    assert size.value > 0 and _err(L) == ""
+    need = size.value
+    # Workspace too small: rejected before any launch.
+    args = [FAKE, 2, 1000, 3] + [FAKE] * 7
+    assert L.tbvh_build(*args, FAKE, need - 1, None) == 2
+    assert "workspace" in _err(L)
+    # Null output.
+    args = [FAKE, 2, 1000, 3, None] + [FAKE] * 6
+    assert L.tbvh_build(*args, FAKE, need, None) == 1
+    assert "null" in _err(L)
+    # Misaligned workspace.
+    args = [FAKE, 2, 1000, 3] + [FAKE] * 7
+    assert L.tbvh_build(*args, ctypes.c_void_p(0x100004), need, None) == 1
+    assert "aligned" in _err(L)
+
+
+def test_knn_argument_errors():
+    L = _native.load()
+    nr = _native.real_node_count(100)
+    base = [FAKE, FAKE, FAKE, None, 1, 10]
+    assert L.tbvh_knn(*base, 100, nr, 3, 5, FAKE, FAKE, None) == 1
+    assert "k must be 4, 8, 16, or 32" in _err(L)
+    assert L.tbvh_knn(*base, 100, nr, 4, 8, FAKE, FAKE, None) == 1
+    assert "D must be 2 or 3" in _err(L)
+    assert L.tbvh_knn(*base, 3, _native.real_node_count(3), 3, 4, FAKE, FAKE, None) == 1
+    assert "num_leaves must be >= k" in _err(L)
+    assert L.tbvh_knn(*base, 100, nr + 1, 3, 4, FAKE, FAKE, None) == 1
+    assert "num_real_nodes" in _err(L)
+    assert L.tbvh_knn(FAKE, None, FAKE, None, 1, 10, 100, nr, 3, 4, FAKE, FAKE, None) == 1
+    assert "null" in _err(L)
+    # M == 0 is a no-op success (nothing launched).
+    assert L.tbvh_knn(None, None, None, None, 1, 0, 100, nr, 3, 4, None, None, None) == 0
+
+
+def test_sort_and_ragged_argument_errors():
+    L = _native.load()
+    size = ctypes.c_size_t()
+    assert L.tbvh_sort_queries_workspace_size(1, -1, 3, ctypes.byref(size)) == 1
+    assert L.tbvh_sort_queries(None, 1, 0, 3, None, None, None, None, 0, None) == 0
+    assert L.tbvh_build_ragged_workspace_size(3, 2, 3, ctypes.byref(size)) == 1
+    assert L.tbvh_knn_ragged(*([FAKE] * 7), 2, 10, 3, 7, FAKE, FAKE, None) == 1
+    assert "k must be" in _err(L)
+    # total_nodes below any valid tree size is rejected.
+    assert L.tbvh_build_ragged(FAKE, FAKE, 2, 100, 3, *([FAKE] * 8), 10, FAKE, 1 << 20, None) == 1
+    assert "total_nodes" in _err(L)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.load()

@@ -1,0 +1,142 @@
+"""GPU build parity against the oracle: Morton codes, sort permutation,
+scene bounds, node AABBs and traversal arrays must be bit-exact.
+
+Point sets restate the reference's build tests (torchbvh
+tests/test_bvh_build.py:133-340) plus sizes around this library's tile and
+subtree boundaries (4096-key sort tiles, 256-leaf tree groups)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import torchbvh_amd as tb
+from parity import (
+    assert_same_f32,
+    assert_same_int,
+    boundary_cloud,
+    pathological_clouds,
+    single_child_cloud,
+)
+from torchbvh_amd._native import _C
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def dev(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def check_single_build(points: np.ndarray) -> None:
+    h = tb.build_bvh(dev(points))
+    ref = oracle.build(points)
+    for key in ("num_leaves", "num_real_nodes", "leaf_level", "virtual_leaves", "dim"):
+        assert h[key] == ref[key], key
+    assert "batch_size" not in h
+    for key in ("scene_min", "scene_max", "node_aabbs"):
+        assert tuple(h[key].shape) == ref[key].shape, key
+        assert_same_f32(h[key].cpu().numpy(), ref[key], key)
+    for key in ("sorted_indices", "left_child_mem", "right_child_mem", "mem_to_leaf"):
+        t = h[key]
+        assert t.dtype == (torch.int64 if key == "sorted_indices" else torch.int32), key
+        assert_same_int(t.cpu().numpy(), ref[key], key)
+
+
+@pytest.mark.parametrize("case", range(len(pathological_clouds())))
+def test_build_pathological_clouds(case):
+    check_single_build(pathological_clouds()[case])
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 31, 32, 33, 63, 64, 65])
+def test_build_boundary_sizes(n, dim):
+    check_single_build(boundary_cloud(n, dim))
+
+
+@pytest.mark.parametrize("n", [3, 5, 6, 9, 10, 17, 18])
+def test_build_single_child_nodes(n):
+    check_single_build(single_child_cloud(n))
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("n", [255, 256, 257, 4095, 4096, 4097, 8193, 65536, 65537, 100_003])
+def test_build_random_sizes_around_tiles(n, dim):
+    rng = np.random.default_rng(n * 10 + dim)
+    check_single_build(rng.random((n, dim), dtype=np.float32))
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_build_heavy_duplicates_keep_stable_order(dim):
+    rng = np.random.default_rng(77 + dim)
+    pts = rng.integers(0, 4, (20_000, dim)).astype(np.float32)  # few distinct codes
+    check_single_build(pts)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_batched_build_matches_per_cloud_oracle(dim):
+    rng = np.random.default_rng(500 + dim)
+    pts = rng.random((5, 3000, dim), dtype=np.float32)
+    pts[2] *= 1e4
+    pts[3] = 0.5  # fully degenerate cloud
+    h = tb.build_bvh(dev(pts))
+    assert isinstance(h, tb.BatchedBVHHandle) and h["batch_size"] == 5
+    ref = oracle.build_batched(pts)
+    for key in ("scene_min", "scene_max", "node_aabbs"):
+        assert_same_f32(h[key].cpu().numpy(), ref[key], key)
+    for key in ("sorted_indices", "left_child_mem", "right_child_mem", "mem_to_leaf"):
+        assert_same_int(h[key].cpu().numpy(), ref[key], key)
+
+
+def test_ragged_build_matches_per_cloud_oracle():
+    rng = np.random.default_rng(900)
+    counts = [1, 2, 4096, 4097, 300, 70_000, 17, 9000]
+    pts = np.concatenate([rng.random((c, 3), dtype=np.float32) * (b + 1) for b, c in enumerate(counts)])
+    offsets = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    h = tb.build_bvh(dev(pts), batch_offsets=dev(offsets))
+    assert isinstance(h, tb.RaggedBVHHandle)
+    assert h["batch_size"] == len(counts)
+    inner = h._handles
+    for b, c in enumerate(counts):
+        ref = oracle.build(pts[offsets[b]:offsets[b + 1]])
+        for key in ("scene_min", "scene_max", "node_aabbs"):
+            assert_same_f32(inner[b][key].cpu().numpy(), ref[key], f"cloud {b} {key}")
+        for key in ("sorted_indices", "left_child_mem", "right_child_mem", "mem_to_leaf"):
+            assert_same_int(inner[b][key].cpu().numpy(), ref[key], f"cloud {b} {key}")
+        for key in ("num_leaves", "num_real_nodes", "leaf_level", "virtual_leaves"):
+            assert inner[b][key] == ref[key]
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_morton_codes_bit_exact(dim):
+    rng = np.random.default_rng(31 + dim)
+    pts = (rng.standard_normal((3, 9000, dim)) * np.array([1.0, 1e3, 1e-3][:dim])).astype(np.float32)
+    lo = np.stack([oracle.bounds(p)[0] for p in pts])
+    hi = np.stack([oracle.bounds(p)[1] for p in pts])
+    hi[1, 0] = lo[1, 0]  # a zero-extent axis
+    codes = _C.morton_codes(dev(pts), dev(lo), dev(hi)).cpu().numpy()
+    for b in range(3):
+        assert_same_int(codes[b], oracle.morton_codes(pts[b], lo[b], hi[b]).astype(np.int64), f"codes {b}")
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("m", [1, 100, 4096, 4097, 50_000])
+def test_query_order_bit_exact(dim, m):
+    rng = np.random.default_rng(m + dim)
+    q = rng.random((2, m, dim), dtype=np.float32) * 1.2 - 0.1  # some outside the scene box
+    lo = np.zeros((2, dim), np.float32)
+    hi = np.ones((2, dim), np.float32)
+    order = _C.morton_sort_queries_narrow(dev(q), dev(lo), dev(hi)).cpu().numpy()
+    for b in range(2):
+        assert_same_int(order[b], oracle.query_order(q[b], lo[b], hi[b]), f"order {b}")
+
+
+def test_build_is_deterministic_across_calls():
+    rng = np.random.default_rng(5)
+    p = dev(rng.random((50_000, 3), dtype=np.float32))
+    a = tb.build_bvh(p)
+    b = tb.build_bvh(p)
+    assert torch.equal(a["node_aabbs"], b["node_aabbs"])
+    assert torch.equal(a["sorted_indices"], b["sorted_indices"])

@@ -1,0 +1,226 @@
+"""GPU k-NN parity against the oracle: indices identical and distances
+bit-exact (the contract's tolerance is 1e-6 relative; the kernel and the
+oracle evaluate the same fused chain, so equality is expected and tested).
+
+Cases restate the reference's k-NN tests (torchbvh tests/test_knn.py,
+tests/test_batched_knn.py, tests/test_ragged_knn.py) with index checks
+everywhere, since ties now resolve to the lower index."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import torchbvh_amd as tb
+from parity import (
+    assert_same_f32,
+    assert_same_int,
+    knn_pathological_clouds,
+    unit_direction_points,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+DIST_RTOL = 1e-6  # contractual tolerance; checked in addition to bit equality
+
+
+def dev(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def check_single(points: np.ndarray, queries: np.ndarray, k: int) -> None:
+    h = tb.build_bvh(dev(points))
+    ei, ed = oracle.knn(points, queries, k)
+    for sort in (True, False):
+        idx, dist = tb.query_knn(h, dev(queries), k, sort_queries=sort)
+        assert idx.dtype == torch.int64 and dist.dtype == torch.float32
+        assert tuple(idx.shape) == (queries.shape[0], k)
+        idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+        np.testing.assert_allclose(dist, ed, rtol=DIST_RTOL, atol=0)
+        assert_same_int(idx, ei, f"indices sort={sort}")
+        assert_same_f32(dist, ed, f"distances sort={sort}")
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
+def test_knn_uniform_random(dim, k):
+    rng = np.random.default_rng(1000 + dim * 10 + k)
+    check_single(rng.random((3000, dim), dtype=np.float32), rng.random((1500, dim), dtype=np.float32), k)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
+def test_knn_self_query(dim, k):
+    rng = np.random.default_rng(2000 + dim * 10 + k)
+    p = rng.random((777, dim), dtype=np.float32)
+    check_single(p, p, k)
+    idx, dist = tb.query_knn(tb.build_bvh(dev(p)), dev(p), k)
+    assert torch.all(dist[:, 0] == 0)
+    assert torch.equal(idx[:, 0].cpu(), torch.arange(777))
+
+
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
+def test_knn_minimum_cloud_sizes(k):
+    rng = np.random.default_rng(k)
+    for n in (k, k + 1, 2 * k - 1):
+        check_single(rng.random((n, 3), dtype=np.float32), rng.random((37, 3), dtype=np.float32), k)
+
+
+@pytest.mark.parametrize("k", [4, 8])
+def test_knn_displaced_curve(k):
+    base = np.linspace(-2.0, 2.0, 32, dtype=np.float32)
+    p = np.stack((base, np.sin(base), np.cos(base)), 1).astype(np.float32)
+    check_single(p, p + np.array([0.07, -0.11, 0.05], np.float32), k)
+
+
+@pytest.mark.parametrize("case", range(len(knn_pathological_clouds())))
+def test_knn_pathological_clouds(case):
+    p, k = knn_pathological_clouds()[case]
+    check_single(p, p[: min(7, p.shape[0])] + np.float32(0.125), k)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16])
+def test_knn_ties_take_lowest_indices(dim, k):
+    p = unit_direction_points(dim)
+    q = np.zeros((2, dim), np.float32)
+    check_single(p, q, k)
+    idx, dist = tb.query_knn(tb.build_bvh(dev(p)), dev(q), k)
+    assert torch.all(dist == 1.0)
+    assert torch.equal(idx.cpu(), torch.arange(k).repeat(2, 1))
+    dup = np.full((20, dim), 3.5, np.float32)
+    check_single(dup, np.full((3, dim), 3.5, np.float32), k)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
+def test_knn_robust_matrix(dim, k):
+    """tests/test_knn.py:327-356: random points, a tie block, duplicates and
+    outliers, with exact, displaced, origin and outlier queries."""
+    rng = np.random.default_rng(2400 + dim * 100 + k)
+    rand = (rng.random((96, dim), dtype=np.float32) * 2 - 1).astype(np.float32)
+    ties = np.zeros((k + 2, dim), np.float32)
+    dup = np.full((2, dim), 0.25, np.float32)
+    out = np.zeros((2, dim), np.float32)
+    out[0, 0], out[1, 0] = 50.0, -50.0
+    out[:, 1] = [30.0, -30.0]
+    p = np.concatenate((rand, ties, dup, out)).astype(np.float32)
+    disp = np.linspace(0.015, 0.045, dim, dtype=np.float32)
+    q = np.concatenate((p[:19], p[19:38] + disp, np.zeros((5, dim), np.float32), out + 0.1 * disp,
+                        rng.random((17, dim), dtype=np.float32) * 2 - 1)).astype(np.float32)
+    check_single(p, q, k)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_knn_clustered_duplicates_large(dim):
+    rng = np.random.default_rng(40 + dim)
+    centres = rng.random((8, dim)).astype(np.float32)
+    p = (centres[rng.integers(0, 8, 60_000)] + 0.02 * rng.standard_normal((60_000, dim))).astype(np.float32)
+    p[1000:1300] = p[3]
+    q = (p[:5000] + 0.005 * rng.standard_normal((5000, dim))).astype(np.float32)
+    check_single(p, q, 32)
+
+
+def test_knn_queries_outside_scene_box():
+    rng = np.random.default_rng(8)
+    p = rng.random((5000, 3), dtype=np.float32)
+    q = (rng.standard_normal((2000, 3)) * 5).astype(np.float32)
+    check_single(p, q, 16)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("n", [16, 17, 31, 300])
+@pytest.mark.parametrize("k", [4, 8, 16])
+def test_batched_knn_matches_oracle_and_single_loop(dim, n, k):
+    rng = np.random.default_rng(13100 + dim * 100 + n * 10 + k)
+    p = rng.random((3, n, dim), dtype=np.float32)
+    q = rng.random((3, 9, dim), dtype=np.float32)
+    h = tb.build_bvh(dev(p))
+    idx, dist, pos = tb.query_knn(h, dev(q), k, source_points=dev(p))
+    assert tuple(idx.shape) == (3, 9, k) and tuple(pos.shape) == (3, 9, k, dim)
+    for b in range(3):
+        ei, ed = oracle.knn(p[b], q[b], k)
+        assert_same_int(idx[b].cpu().numpy(), ei, f"batch {b} indices")
+        assert_same_f32(dist[b].cpu().numpy(), ed, f"batch {b} distances")
+        assert_same_f32(pos[b].cpu().numpy(), p[b][ei], f"batch {b} positions")
+        si, sd = tb.query_knn(tb.build_bvh(dev(p[b])), dev(q[b]), k)
+        assert torch.equal(si, idx[b]) and torch.equal(sd, dist[b])
+
+
+def test_batched_no_cross_sample_leakage():
+    rng = np.random.default_rng(13300)
+    p = np.stack([rng.random((200, 3), dtype=np.float32) + 100.0 * b for b in range(4)])
+    q = np.stack([p[b, :20] + 0.01 for b in range(4)]).astype(np.float32)
+    h = tb.build_bvh(dev(p))
+    idx, dist = tb.query_knn(h, dev(q), 8)
+    assert int(idx.min()) >= 0 and int(idx.max()) < 200
+    for b in range(4):
+        ei, ed = oracle.knn(p[b], q[b], 8)
+        assert_same_int(idx[b].cpu().numpy(), ei, "indices")
+
+
+def _offsets(counts):
+    return np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
+def test_ragged_knn_matches_oracle(dim, k):
+    rng = np.random.default_rng(14100 + dim * 10 + k)
+    counts = [k, k + 3, k + 9, 5000, 4097]
+    qcounts = [3, 6, 4, 1000, 777]
+    p = np.concatenate([rng.random((c, dim), dtype=np.float32) + 20.0 * b for b, c in enumerate(counts)])
+    q = np.concatenate([rng.random((c, dim), dtype=np.float32) + 20.0 * b for b, c in enumerate(qcounts)])
+    po, qo = _offsets(counts), _offsets(qcounts)
+    h = tb.build_bvh(dev(p), batch_offsets=dev(po))
+    idx, dist, pos = tb.query_knn(h, dev(q), k, query_offsets=dev(qo), source_points=dev(p))
+    ei, ed = oracle.knn_ragged(p, po, q, qo, k)
+    assert_same_int(idx.cpu().numpy(), ei, "indices")
+    assert_same_f32(dist.cpu().numpy(), ed, "distances")
+    rows = np.repeat(po[:-1], qcounts)
+    assert_same_f32(pos.cpu().numpy(), p[ei + rows[:, None]], "positions")
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16])
+def test_ragged_ties_take_lowest_local_indices(dim, k):
+    eye = np.eye(dim, dtype=np.float32)
+    dirs = np.concatenate([np.stack((eye[d], -eye[d])) for d in range(dim)])
+    counts = [k + 3, k + 7, k + 11]
+    qcounts = [2, 3, 1]
+    shifts = [np.full(dim, -40.0, np.float32), np.full(dim, 40.0, np.float32),
+              np.linspace(-25.0, 25.0, dim, dtype=np.float32)]
+    d0 = np.zeros(dim, np.float32)
+    d0[0] = 1.0
+    d2 = np.zeros(dim, np.float32)
+    d2[-1] = -1.0
+    reps = (counts[1] + dirs.shape[0] - 1) // dirs.shape[0]
+    samples = [np.tile(d0, (counts[0], 1)) + shifts[0],
+               np.tile(dirs, (reps, 1))[: counts[1]] + shifts[1],
+               np.tile(d2, (counts[2], 1)) + shifts[2]]
+    p = np.concatenate(samples).astype(np.float32)
+    q = np.concatenate([np.tile(s, (c, 1)) for s, c in zip(shifts, qcounts)]).astype(np.float32)
+    po, qo = _offsets(counts), _offsets(qcounts)
+    h = tb.build_bvh(dev(p), batch_offsets=dev(po))
+    idx, dist = tb.query_knn(h, dev(q), k, query_offsets=dev(qo))
+    ei, ed = oracle.knn_ragged(p, po, q, qo, k)
+    assert_same_int(idx.cpu().numpy(), ei, "indices")
+    assert_same_f32(dist.cpu().numpy(), ed, "distances")
+    assert torch.all(dist == 1.0)
+    assert torch.equal(idx.cpu(), torch.arange(k).repeat(6, 1))
+
+
+def test_ragged_indices_are_local():
+    rng = np.random.default_rng(14200)
+    counts = [8, 11, 14]
+    p = np.concatenate([rng.random((c, 3), dtype=np.float32) + 100.0 * b for b, c in enumerate(counts)])
+    po = _offsets(counts)
+    q = np.concatenate([p[po[b]:po[b] + 3] for b in range(3)])
+    h = tb.build_bvh(dev(p), batch_offsets=dev(po))
+    idx, dist = tb.query_knn(h, dev(q), 4, query_offsets=dev(_offsets([3, 3, 3])))
+    for b, c in enumerate(counts):
+        s = idx[3 * b:3 * b + 3]
+        assert int(s.min()) >= 0 and int(s.max()) < c
+    assert torch.all(dist[:, 0] == 0)

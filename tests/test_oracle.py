@@ -1,0 +1,342 @@
+"""Pin the C oracle (CPU only).
+
+Every oracle function is checked against something that does not restate it:
+brute-force constructions, exhaustive enumeration, exact rational arithmetic,
+numpy library routines, known answers, the invariants of the reference's own
+tests (torchbvh tests/test_bvh_build.py:65-130, tests/test_knn.py) and, for
+k-NN, two different algorithms (branch-and-bound vs brute force) that must
+agree exactly.
+"""
+
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle
+from parity import (
+    assert_same_f32,
+    assert_same_int,
+    boundary_cloud,
+    knn_pathological_clouds,
+    pathological_clouds,
+    single_child_cloud,
+    unit_direction_points,
+)
+
+
+# ---------------------------------------------------------------------------
+# Implicit tree closed forms vs a brute-force heap
+# ---------------------------------------------------------------------------
+def brute_tree(n: int):
+    """Build the heap explicitly: 2^L leaf slots, the first n real; an
+    internal node is real iff a child is; storage rows are ranks of real
+    nodes in heap order."""
+    L = 0
+    while (1 << L) < n:
+        L += 1
+    size = (1 << (L + 1)) - 1
+    real = np.zeros(size, bool)
+    first_leaf = (1 << L) - 1
+    real[first_leaf:first_leaf + n] = True
+    for i in range(first_leaf - 1, -1, -1):
+        real[i] = real[2 * i + 1] or real[2 * i + 2]
+    rank = np.cumsum(real) - 1
+    return L, real, rank
+
+
+@pytest.mark.parametrize("n", list(range(1, 700)) + [1000, 1023, 1024, 1025, 4097, 10000, 65535])
+def test_tree_closed_forms_match_brute_force_heap(n):
+    L, real, rank = brute_tree(n)
+    assert oracle.leaf_level(n) == L
+    assert oracle.virtual_leaves(n) == (1 << L) - n
+    assert oracle.real_node_count(n) == int(real.sum())
+    for i in range(real.size):
+        assert oracle.is_virtual(n, i) == (not real[i])
+        if real[i]:
+            assert oracle.memory_index(n, i) == rank[i]
+
+
+@pytest.mark.parametrize(
+    "n,nr,vl,L",
+    [(10_000, 20_005, 6_384, 14), (1 << 20, 2_097_151, 0, 20), (65_536, 131_071, 0, 16),
+     (1 << 22, 8_388_607, 0, 22), (200_000, None, 62_144, 18)],
+)
+def test_tree_facts_at_baseline_sizes(n, nr, vl, L):
+    if nr is None:
+        nr = int(brute_tree(n)[1].sum())
+    assert oracle.real_node_count(n) == nr
+    assert oracle.virtual_leaves(n) == vl
+    assert oracle.leaf_level(n) == L
+
+
+# ---------------------------------------------------------------------------
+# Morton codes
+# ---------------------------------------------------------------------------
+def interleave(values: list[int], bits: int) -> int:
+    out = 0
+    D = len(values)
+    for b in range(bits):
+        for d, v in enumerate(values):
+            out |= ((v >> b) & 1) << (D * b + d)
+    return out
+
+
+def test_spread_functions_exhaustive():
+    assert oracle.split3(1023) == 0x09249249
+    assert oracle.split2(0xFFFF) == 0x55555555
+    for v in range(1024):
+        assert oracle.split3(v) == sum(((v >> b) & 1) << (3 * b) for b in range(10))
+    vs = np.arange(65536)
+    expect = np.zeros_like(vs)
+    for b in range(16):
+        expect |= ((vs >> b) & 1) << (2 * b)
+    got = np.array([oracle.split2(int(v)) for v in vs])
+    assert np.array_equal(got, expect)
+
+
+def test_morton_known_answers_3d():
+    lo = np.zeros(3, np.float32)
+    hi = np.ones(3, np.float32)
+    pts = np.array([
+        [0, 0, 0], [1, 1, 1], [1, 0, 0], [0, 1, 0], [0, 0, 1],
+        [0.5, 0, 0], [0.25, 0.5, 0.75], [-5, 7, 0.5],
+    ], np.float32)
+    codes = oracle.morton_codes(pts, lo, hi)
+    s = 0x09249249
+    assert codes[0] == 0
+    assert codes[1] == (1 << 30) - 1
+    assert codes[2] == s and codes[3] == s << 1 and codes[4] == s << 2
+    assert codes[5] == 1 << 27  # x cell 512: bit 9 of x -> bit 27
+    assert codes[6] == interleave([256, 512, 768], 10)
+    assert codes[7] == interleave([0, 1023, 512], 10)  # clamped outside the box
+
+
+def test_morton_known_answers_2d_and_degenerate_axes():
+    lo = np.array([-1, 2], np.float32)
+    hi = np.array([3, 2], np.float32)  # axis 1 has zero extent -> cell 0
+    pts = np.array([[-1, 2], [3, 2], [1, 100], [2, -100]], np.float32)
+    codes = oracle.morton_codes(pts, lo, hi)
+    assert codes[0] == 0
+    assert codes[1] == 0x55555555  # x cell 65535, y cell 0
+    assert codes[2] == interleave([32768, 0], 16)
+    assert codes[3] == interleave([49152, 0], 16)
+    full = oracle.morton_codes(np.array([[3, 5]], np.float32), np.array([-1, 1], np.float32),
+                               np.array([3, 5], np.float32))
+    assert full[0] == 0xFFFFFFFF
+
+
+def test_morton_matches_numpy_ieee_quantisation():
+    rng = np.random.default_rng(5)
+    for D, bins, nbits in ((3, 1024, 10), (2, 65536, 16)):
+        pts = (rng.standard_normal((5000, D)) * 3).astype(np.float32)
+        lo, hi = oracle.bounds(pts)
+        u = np.clip((pts - lo) / (hi - lo), np.float32(0), np.float32(1)).astype(np.float32)
+        cells = np.minimum((u * np.float32(bins)).astype(np.uint32), bins - 1)
+        expect = [interleave([int(c) for c in row], nbits) for row in cells]
+        got = oracle.morton_codes(pts, lo, hi)
+        assert np.array_equal(got.astype(np.int64), np.array(expect, np.int64))
+
+
+def test_stable_argsort_matches_numpy_stable():
+    rng = np.random.default_rng(7)
+    for n, hi in ((1, 4), (2, 2), (1000, 8), (4097, 1 << 30), (70_000, 50)):
+        keys = rng.integers(0, hi, n, dtype=np.uint32)
+        assert_same_int(oracle.stable_argsort(keys), np.argsort(keys, kind="stable"), "argsort")
+
+
+def test_bounds_match_numpy_and_seed_semantics():
+    rng = np.random.default_rng(9)
+    p = rng.standard_normal((1000, 3)).astype(np.float32)
+    lo, hi = oracle.bounds(p)
+    assert_same_f32(lo, p.min(0), "lo")
+    assert_same_f32(hi, p.max(0), "hi")
+    # Seeds are +-1e30 (bvh_build.cu:466-467): coordinates beyond them clamp.
+    big = np.full((4, 2), 3e30, np.float32)
+    lo, hi = oracle.bounds(big)
+    assert np.all(lo == np.float32(1e30)) and np.all(hi == np.float32(3e30))
+
+
+# ---------------------------------------------------------------------------
+# Build: reference invariants + brute-force subtree boxes
+# ---------------------------------------------------------------------------
+def check_build(points: np.ndarray) -> dict:
+    n, D = points.shape
+    b = oracle.build(points)
+    L, real, rank = brute_tree(n)
+    nr = int(real.sum())
+    nodes = b["node_aabbs"]
+    assert nodes.shape == (nr, 2 * D)
+    assert b["num_real_nodes"] == nr and b["leaf_level"] == L
+    assert b["virtual_leaves"] == (1 << L) - n
+    # sorted_indices: the stable Morton order of the points.
+    lo, hi = points.min(0), points.max(0)
+    assert_same_f32(b["scene_min"], lo, "scene_min")
+    assert_same_f32(b["scene_max"], hi, "scene_max")
+    codes = oracle.morton_codes(points, lo, hi)
+    assert_same_int(b["sorted_indices"], np.argsort(codes, kind="stable"), "sorted_indices")
+    sp = points[b["sorted_indices"]]
+    first_leaf = (1 << L) - 1
+    for i in np.nonzero(real)[0]:
+        level = int(i + 1).bit_length() - 1
+        span = 1 << (L - level)
+        a = (i - ((1 << level) - 1)) * span
+        leaves = sp[a:min(a + span, n)]
+        box = nodes[rank[i]]
+        assert_same_f32(box[:D], leaves.min(0), f"node {i} lo")
+        assert_same_f32(box[D:], leaves.max(0), f"node {i} hi")
+        row = rank[i]
+        if i >= first_leaf:
+            assert b["left_child_mem"][row] == -1 and b["right_child_mem"][row] == -1
+            assert b["mem_to_leaf"][row] == i - first_leaf
+        else:
+            assert b["left_child_mem"][row] == rank[2 * i + 1]
+            assert b["right_child_mem"][row] == (rank[2 * i + 2] if real[2 * i + 2] else -1)
+            assert b["mem_to_leaf"][row] == -1
+    return b
+
+
+@pytest.mark.parametrize("case", range(len(pathological_clouds())))
+def test_build_pathological_clouds(case):
+    check_build(pathological_clouds()[case])
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 31, 32, 33, 63, 64, 65])
+def test_build_boundary_sizes(n, dim):
+    check_build(boundary_cloud(n, dim))
+
+
+@pytest.mark.parametrize("n", [3, 5, 6, 9, 10, 17, 18])
+def test_build_single_child_nodes(n):
+    check_build(single_child_cloud(n))
+
+
+@pytest.mark.parametrize("n,dim", [(1000, 3), (777, 2), (5000, 3)])
+def test_build_random(n, dim):
+    rng = np.random.default_rng(n + dim)
+    check_build(rng.random((n, dim), dtype=np.float32))
+
+
+def test_build_degenerate_extent_is_constant():
+    b = check_build(np.array([[7.0, -3.0]] * 3, np.float32))
+    assert np.all(b["node_aabbs"] == np.array([7.0, -3.0, 7.0, -3.0], np.float32))
+
+
+# ---------------------------------------------------------------------------
+# Distances: the fused chain, checked with exact rational arithmetic
+# ---------------------------------------------------------------------------
+def round_f32(x: Fraction) -> np.float32:
+    """Correctly round a rational to fp32 (nearest, ties to even)."""
+    if x == 0:
+        return np.float32(0)
+    c = np.float32(float(x))
+    cands = {c, np.nextafter(c, np.float32(np.inf)), np.nextafter(c, np.float32(-np.inf))}
+    best = min(cands, key=lambda v: (abs(Fraction(float(v)) - x),
+                                     int(np.array([v], np.float32).view(np.uint32)[0]) & 1))
+    return np.float32(best)
+
+
+def fused_chain(q, p) -> np.float32:
+    s = None
+    for d in range(len(q)):
+        delta = abs(Fraction(float(np.float32(q[d]) - np.float32(p[d]))))
+        s = round_f32(delta * delta) if s is None else round_f32(delta * delta + Fraction(float(s)))
+    return s
+
+
+def test_point_distance_is_correctly_rounded_fma_chain():
+    rng = np.random.default_rng(11)
+    for D in (2, 3):
+        for _ in range(1500):
+            scale = 10.0 ** rng.integers(-4, 5)
+            q = (rng.standard_normal(D) * scale).astype(np.float32)
+            p = (q + rng.standard_normal(D).astype(np.float32) * np.float32(scale * 1e-3)).astype(np.float32)
+            got = np.float32(oracle.point_distance(q, p))
+            assert_same_f32(got, fused_chain(q, p), f"dist {q} {p}")
+
+
+# ---------------------------------------------------------------------------
+# k-NN: branch-and-bound == brute force; brute force vs float64 truth
+# ---------------------------------------------------------------------------
+def check_knn(points, queries, k):
+    bi, bd = oracle.knn_brute(points, queries, k)
+    ti, td = oracle.knn(points, queries, k)
+    assert_same_int(ti, bi, "bvh vs brute indices")
+    assert_same_f32(td, bd, "bvh vs brute distances")
+    # Rows ascending lexicographically.
+    assert np.all((bd[:, :-1] < bd[:, 1:]) | ((bd[:, :-1] == bd[:, 1:]) & (bi[:, :-1] < bi[:, 1:])))
+    # Against float64 truth: the chosen set is optimal up to rounding.
+    p64 = points.astype(np.float64)
+    for r in range(queries.shape[0]):
+        d64 = ((queries[r].astype(np.float64) - p64) ** 2).sum(1)
+        kth = np.sort(d64)[k - 1]
+        chosen = d64[bi[r]]
+        assert np.all(chosen <= kth * (1 + 1e-6) + 1e-30)
+        np.testing.assert_allclose(bd[r], chosen, rtol=1e-6, atol=1e-30)
+    return bi, bd
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
+def test_knn_uniform(dim, k):
+    rng = np.random.default_rng(1000 + dim * 10 + k)
+    check_knn(rng.random((300, dim), dtype=np.float32), rng.random((60, dim), dtype=np.float32), k)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16])
+def test_knn_self_query(dim, k):
+    rng = np.random.default_rng(2000 + dim * 10 + k)
+    p = rng.random((48, dim), dtype=np.float32)
+    bi, bd = check_knn(p, p, k)
+    assert np.all(bd[:, 0] == 0) and np.array_equal(bi[:, 0], np.arange(48))
+
+
+@pytest.mark.parametrize("case", range(len(knn_pathological_clouds())))
+def test_knn_pathological(case):
+    p, k = knn_pathological_clouds()[case]
+    check_knn(p, p[: min(7, p.shape[0])] + np.float32(0.125), k)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 8, 16])
+def test_knn_ties_resolve_to_lowest_index(dim, k):
+    p = unit_direction_points(dim)
+    q = np.zeros((2, dim), np.float32)
+    bi, bd = check_knn(p, q, k)
+    assert np.all(bd == 1.0)
+    assert np.array_equal(bi, np.tile(np.arange(k), (2, 1)))
+    dup = np.full((20, dim), 3.5, np.float32)
+    bi, bd = check_knn(dup, np.full((3, dim), 3.5, np.float32), k)
+    assert np.all(bd == 0) and np.array_equal(bi, np.tile(np.arange(k), (3, 1)))
+
+
+def test_knn_clustered_and_duplicates_large():
+    rng = np.random.default_rng(3)
+    centres = rng.random((8, 3)).astype(np.float32)
+    p = (centres[rng.integers(0, 8, 20_000)] + 0.02 * rng.standard_normal((20_000, 3))).astype(np.float32)
+    p[100:200] = p[5]  # a block of exact duplicates
+    q = (p[:400] + 0.005 * rng.standard_normal((400, 3))).astype(np.float32)
+    bi, bd = oracle.knn_brute(p, q, 32)
+    ti, td = oracle.knn(p, q, 32)
+    assert_same_int(ti, bi, "indices")
+    assert_same_f32(td, bd, "distances")
+
+
+def test_torch_bruteforce_agrees_with_oracle_away_from_near_ties():
+    import torch
+
+    from oracle.torch_bruteforce import knn_bruteforce
+
+    rng = np.random.default_rng(21)
+    p = rng.random((4000, 3), dtype=np.float32)
+    q = rng.random((300, 3), dtype=np.float32)
+    ti, td = knn_bruteforce(torch.from_numpy(p), torch.from_numpy(q), 16)
+    oi, od = oracle.knn_brute(p, q, 16)
+    np.testing.assert_allclose(td.numpy(), od, rtol=1e-6, atol=0)
+    gaps = np.diff(od, axis=1)
+    safe = np.all(gaps > 1e-5 * od[:, 1:], axis=1)
+    assert np.array_equal(ti.numpy()[safe], oi[safe])

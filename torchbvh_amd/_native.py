@@ -1,0 +1,390 @@
+"""ctypes binding of the C-ABI library and torch-facing wrappers.
+
+``_C`` mirrors the reference's native module surface for this path
+(torchbvh/csrc/bindings.cpp:155-199): ``build_bvh_batched_cooperative``,
+``morton_sort_queries_narrow``, ``query_knn_batched_cached_bounds`` and
+``query_knn_batched_cached_bounds_ordered`` take and return torch tensors with
+the reference's shapes and dtypes, plus the ragged entry points this library
+adds (one launch sequence for all clouds).  Outputs and workspaces are
+allocated with torch on the input's device; every launch goes on the current
+stream of that device.  Native precondition failures raise ``RuntimeError``
+like the reference's ``TORCH_CHECK``.
+
+The library must be built (``python -m torchbvh_amd._build``); there is no
+fallback: without it every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+from ._build import LIB_PATH
+
+_lock = threading.Lock()
+_lib = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_szp = ctypes.POINTER(ctypes.c_size_t)
+
+
+def _declare(L) -> None:
+    L.tbvh_abi_version.restype = _int
+    L.tbvh_last_error.restype = ctypes.c_char_p
+    L.tbvh_leaf_level.argtypes = [_i64]
+    L.tbvh_leaf_level.restype = _int
+    L.tbvh_virtual_leaves.argtypes = [_i64]
+    L.tbvh_virtual_leaves.restype = _i64
+    L.tbvh_real_node_count.argtypes = [_i64]
+    L.tbvh_real_node_count.restype = _i64
+    L.tbvh_build_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_build.argtypes = [_vp, _i64, _i64, _int] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]
+    L.tbvh_build_ragged_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_build_ragged.argtypes = (
+        [_vp, _vp, _i64, _i64, _int] + [_vp] * 8 + [_i64, _vp, ctypes.c_size_t, _vp]
+    )
+    L.tbvh_sort_queries_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_sort_queries.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    L.tbvh_sort_queries_ragged_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_sort_queries_ragged.argtypes = (
+        [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    )
+    L.tbvh_morton_codes.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    L.tbvh_knn.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    L.tbvh_knn_ragged.argtypes = (
+        [_vp] * 7 + [_i64, _i64, _int, _int, _vp, _vp, _vp]
+    )
+    for name in (
+        "tbvh_build_workspace_size", "tbvh_build", "tbvh_build_ragged_workspace_size",
+        "tbvh_build_ragged", "tbvh_sort_queries_workspace_size", "tbvh_sort_queries",
+        "tbvh_sort_queries_ragged_workspace_size", "tbvh_sort_queries_ragged",
+        "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged",
+    ):
+        getattr(L, name).restype = _int
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def load():
+    """Load the native library (torch's HIP runtime is loaded first, so the
+    library binds to the same runtime instance as torch)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"torchbvh_amd: native library {LIB_PATH} is not built; "
+                    "run `python -m torchbvh_amd._build` (hipcc, gfx950)"
+                )
+            L = ctypes.CDLL(str(LIB_PATH))
+            _declare(L)
+            _lib = L
+    return _lib
+
+
+def _last_error() -> str:
+    msg = load().tbvh_last_error()
+    return msg.decode() if msg else "unknown error"
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise RuntimeError(_last_error())
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _size(fn, *args) -> int:
+    out = ctypes.c_size_t(0)
+    _check(fn(*args, ctypes.byref(out)))
+    return out.value
+
+
+def _require(cond: bool, op: str, message: str) -> None:
+    if not cond:
+        raise RuntimeError(f"{op}: {message}")
+
+
+def _require_device_f32(op: str, t: torch.Tensor, name: str) -> None:
+    _require(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32, op,
+             f"{name} must be contiguous CUDA float32")
+
+
+def _require_device_i64(op: str, t: torch.Tensor, name: str) -> None:
+    _require(t.is_cuda and t.is_contiguous() and t.dtype == torch.int64, op,
+             f"{name} must be contiguous CUDA int64")
+
+
+# ---------------------------------------------------------------------------
+# Closed forms
+# ---------------------------------------------------------------------------
+def leaf_level(n: int) -> int:
+    return int(load().tbvh_leaf_level(n))
+
+
+def virtual_leaves(n: int) -> int:
+    return int(load().tbvh_virtual_leaves(n))
+
+
+def real_node_count(n: int) -> int:
+    return int(load().tbvh_real_node_count(n))
+
+
+# ---------------------------------------------------------------------------
+# Native operations (reference `_C` surface)
+# ---------------------------------------------------------------------------
+class _NativeOps:
+    """Torch-level wrappers over the C ABI, named as the reference's `_C`."""
+
+    @staticmethod
+    def build_bvh_batched_cooperative(points: torch.Tensor) -> dict:
+        op = "build_bvh_batched_cooperative"
+        _require_device_f32(op, points, "points")
+        _require(points.dim() == 3 and points.size(0) >= 1 and points.size(1) >= 1
+                 and points.size(2) in (2, 3), op, "points must have shape (B, N, 2|3)")
+        L = load()
+        B, N, D = (int(s) for s in points.shape)
+        dev = points.device
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_build_workspace_size, B, N, D)
+            nr = real_node_count(N)
+            node_aabbs = torch.empty((B, nr, 2 * D), dtype=torch.float32, device=dev)
+            sorted_indices = torch.empty((B, N), dtype=torch.int64, device=dev)
+            scene_min = torch.empty((B, D), dtype=torch.float32, device=dev)
+            scene_max = torch.empty((B, D), dtype=torch.float32, device=dev)
+            left = torch.empty(nr, dtype=torch.int32, device=dev)
+            right = torch.empty(nr, dtype=torch.int32, device=dev)
+            leaf = torch.empty(nr, dtype=torch.int32, device=dev)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_build(
+                _ptr(points), B, N, D, _ptr(node_aabbs), _ptr(sorted_indices),
+                _ptr(scene_min), _ptr(scene_max), _ptr(left), _ptr(right), _ptr(leaf),
+                _ptr(ws), ws.numel(), _stream(dev)))
+        return {
+            "node_aabbs": node_aabbs,
+            "sorted_indices": sorted_indices,
+            "scene_min": scene_min,
+            "scene_max": scene_max,
+            "batch_size": B,
+            "num_leaves": N,
+            "num_real_nodes": nr,
+            "leaf_level": leaf_level(N),
+            "virtual_leaves": virtual_leaves(N),
+            "dim": D,
+            "left_child_mem": left,
+            "right_child_mem": right,
+            "mem_to_leaf": leaf,
+        }
+
+    @staticmethod
+    def build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor,
+                         counts: list[int]) -> dict:
+        """Segmented build of packed clouds; `counts` are the host-side cloud
+        sizes (already validated).  Returns packed tensors and per-cloud node
+        offsets."""
+        op = "build_bvh_ragged"
+        _require_device_f32(op, points, "points")
+        _require_device_i64(op, batch_offsets, "batch_offsets")
+        L = load()
+        T, D = (int(s) for s in points.shape)
+        B = len(counts)
+        dev = points.device
+        node_counts = [real_node_count(c) for c in counts]
+        total_nodes = sum(node_counts)
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_build_ragged_workspace_size, B, T, D)
+            node_aabbs = torch.empty((total_nodes, 2 * D), dtype=torch.float32, device=dev)
+            sorted_indices = torch.empty(T, dtype=torch.int64, device=dev)
+            scene_min = torch.empty((B, D), dtype=torch.float32, device=dev)
+            scene_max = torch.empty((B, D), dtype=torch.float32, device=dev)
+            left = torch.empty(total_nodes, dtype=torch.int32, device=dev)
+            right = torch.empty(total_nodes, dtype=torch.int32, device=dev)
+            leaf = torch.empty(total_nodes, dtype=torch.int32, device=dev)
+            node_offsets = torch.empty(B + 1, dtype=torch.int64, device=dev)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_build_ragged(
+                _ptr(points), _ptr(batch_offsets), B, T, D, _ptr(node_aabbs),
+                _ptr(sorted_indices), _ptr(scene_min), _ptr(scene_max), _ptr(left),
+                _ptr(right), _ptr(leaf), _ptr(node_offsets), total_nodes,
+                _ptr(ws), ws.numel(), _stream(dev)))
+        host_node_offsets = [0]
+        for c in node_counts:
+            host_node_offsets.append(host_node_offsets[-1] + c)
+        return {
+            "node_aabbs": node_aabbs,
+            "sorted_indices": sorted_indices,
+            "scene_min": scene_min,
+            "scene_max": scene_max,
+            "left_child_mem": left,
+            "right_child_mem": right,
+            "mem_to_leaf": leaf,
+            "node_offsets": node_offsets,
+            "host_node_offsets": host_node_offsets,
+        }
+
+    @staticmethod
+    def morton_sort_queries_narrow(queries: torch.Tensor, scene_min: torch.Tensor,
+                                   scene_max: torch.Tensor) -> torch.Tensor:
+        op = "morton_sort_queries_narrow"
+        _require_device_f32(op, queries, "queries")
+        _require(scene_min.is_cuda and scene_max.is_cuda and scene_min.is_contiguous()
+                 and scene_max.is_contiguous(), op, "bounds must be contiguous CUDA tensors")
+        _require(queries.dim() == 3 and queries.size(2) in (2, 3), op,
+                 "queries must have shape (B, M, 2|3)")
+        _require(scene_min.shape == scene_max.shape and scene_min.dim() == 2
+                 and scene_min.size(0) == queries.size(0)
+                 and scene_min.size(1) == queries.size(2), op, "bounds shape mismatch")
+        _require(scene_min.dtype == torch.float32 and scene_max.dtype == torch.float32, op,
+                 "bounds must be float32")
+        L = load()
+        B, M, D = (int(s) for s in queries.shape)
+        dev = queries.device
+        order = torch.empty((B, M), dtype=torch.int64, device=dev)
+        if M == 0:
+            return order
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_sort_queries_workspace_size, B, M, D)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_sort_queries(
+                _ptr(queries), B, M, D, _ptr(scene_min), _ptr(scene_max), _ptr(order),
+                _ptr(ws), ws.numel(), _stream(dev)))
+        return order
+
+    @staticmethod
+    def morton_sort_queries_ragged(queries: torch.Tensor, query_offsets: torch.Tensor,
+                                   scene_min: torch.Tensor, scene_max: torch.Tensor,
+                                   batch_size: int) -> torch.Tensor:
+        op = "morton_sort_queries_ragged"
+        _require_device_f32(op, queries, "queries")
+        _require_device_i64(op, query_offsets, "query_offsets")
+        L = load()
+        T, D = (int(s) for s in queries.shape)
+        dev = queries.device
+        order = torch.empty(T, dtype=torch.int64, device=dev)
+        if T == 0:
+            return order
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_sort_queries_ragged_workspace_size, batch_size, T, D)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_sort_queries_ragged(
+                _ptr(queries), _ptr(query_offsets), batch_size, T, D, _ptr(scene_min),
+                _ptr(scene_max), _ptr(order), _ptr(ws), ws.numel(), _stream(dev)))
+        return order
+
+    @staticmethod
+    def morton_codes(rows: torch.Tensor, scene_min: torch.Tensor,
+                     scene_max: torch.Tensor) -> torch.Tensor:
+        """Diagnostic: the Morton kernel's u32 codes (as int64) of [B, M, D]
+        rows against per-cloud bounds [B, D]."""
+        op = "morton_codes"
+        _require_device_f32(op, rows, "rows")
+        _require(rows.dim() == 3 and rows.size(2) in (2, 3), op, "rows must have shape (B, M, 2|3)")
+        _require_device_f32(op, scene_min, "scene_min")
+        _require_device_f32(op, scene_max, "scene_max")
+        L = load()
+        B, M, D = (int(s) for s in rows.shape)
+        dev = rows.device
+        codes = torch.empty((B, M), dtype=torch.int32, device=dev)
+        if M == 0:
+            return codes.to(torch.int64)
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_sort_queries_workspace_size, B, M, D)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_morton_codes(
+                _ptr(rows), B, M, D, _ptr(scene_min), _ptr(scene_max), _ptr(codes),
+                _ptr(ws), ws.numel(), _stream(dev)))
+        return codes.to(torch.int64) & 0xFFFFFFFF
+
+    @staticmethod
+    def _knn(op, node_aabbs, sorted_indices, query_points, query_order, num_leaves,
+             num_real_nodes, dim, k):
+        _require(dim in (2, 3), op, "D must be 2 or 3")
+        _require_device_f32(op, query_points, "query_points")
+        _require(query_points.dim() == 3 and query_points.size(2) == dim, op,
+                 "query_points must have shape (B, M, D)")
+        _require_device_f32(op, node_aabbs, "node_aabbs")
+        _require(node_aabbs.dim() == 3 and node_aabbs.size(0) == query_points.size(0)
+                 and node_aabbs.size(1) == num_real_nodes and node_aabbs.size(2) == 2 * dim,
+                 op, "node_aabbs has incompatible shape")
+        _require_device_i64(op, sorted_indices, "sorted_indices")
+        _require(sorted_indices.dim() == 2 and sorted_indices.size(0) == query_points.size(0)
+                 and sorted_indices.size(1) == num_leaves, op,
+                 "sorted_indices has incompatible shape")
+        if query_order is not None:
+            _require_device_i64(op, query_order, "query_order")
+            _require(query_order.dim() == 2 and query_order.shape == query_points.shape[:2],
+                     op, "query_order must have shape (B, M)")
+        _require(num_leaves >= k, op, "num_leaves must be >= k")
+        dev = query_points.device
+        for t in (node_aabbs, sorted_indices) + ((query_order,) if query_order is not None else ()):
+            _require(t.device == dev, op, "all inputs must share a device")
+        B, M = int(query_points.size(0)), int(query_points.size(1))
+        indices = torch.empty((B, M, k), dtype=torch.int64, device=dev)
+        distances = torch.empty((B, M, k), dtype=torch.float32, device=dev)
+        if M == 0:
+            return indices, distances
+        L = load()
+        with torch.cuda.device(dev):
+            _check(L.tbvh_knn(
+                _ptr(node_aabbs), _ptr(sorted_indices), _ptr(query_points), _ptr(query_order),
+                B, M, int(num_leaves), int(num_real_nodes), int(dim), int(k),
+                _ptr(indices), _ptr(distances), _stream(dev)))
+        return indices, distances
+
+    @classmethod
+    def query_knn_batched_cached_bounds(cls, node_aabbs, sorted_indices, query_points,
+                                        num_leaves, num_real_nodes, dim, k):
+        return cls._knn("query_knn_batched_cached_bounds", node_aabbs, sorted_indices,
+                        query_points, None, num_leaves, num_real_nodes, dim, k)
+
+    @classmethod
+    def query_knn_batched_cached_bounds_ordered(cls, node_aabbs, sorted_indices, query_points,
+                                                query_order, num_leaves, num_real_nodes, dim, k):
+        return cls._knn("query_knn_batched_cached_bounds_ordered", node_aabbs, sorted_indices,
+                        query_points, query_order, num_leaves, num_real_nodes, dim, k)
+
+    @staticmethod
+    def query_knn_ragged(node_aabbs, sorted_indices, point_offsets, node_offsets, query_points,
+                         query_offsets, query_order, batch_size, dim, k):
+        op = "query_knn_ragged"
+        _require_device_f32(op, query_points, "query_points")
+        _require_device_f32(op, node_aabbs, "node_aabbs")
+        _require_device_i64(op, sorted_indices, "sorted_indices")
+        for name, t in (("point_offsets", point_offsets), ("node_offsets", node_offsets),
+                        ("query_offsets", query_offsets)):
+            _require_device_i64(op, t, name)
+        T = int(query_points.size(0))
+        dev = query_points.device
+        indices = torch.empty((T, k), dtype=torch.int64, device=dev)
+        distances = torch.empty((T, k), dtype=torch.float32, device=dev)
+        if T == 0:
+            return indices, distances
+        L = load()
+        with torch.cuda.device(dev):
+            _check(L.tbvh_knn_ragged(
+                _ptr(node_aabbs), _ptr(sorted_indices), _ptr(point_offsets), _ptr(node_offsets),
+                _ptr(query_points), _ptr(query_offsets), _ptr(query_order), int(batch_size), T,
+                int(dim), int(k), _ptr(indices), _ptr(distances), _stream(dev)))
+        return indices, distances
+
+
+_C = _NativeOps()

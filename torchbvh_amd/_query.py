@@ -1,0 +1,352 @@
+"""Build and k-NN query entry points: validation, dispatch and handle payloads.
+
+Public behaviour (signatures, dispatch, messages, payloads) follows
+torchbvh/_query.py:29-405.  Ragged inputs differ in mechanism only: the
+reference loops over clouds in Python with one native build/query per cloud
+(:68-85, :299-366); here one segmented native build and one segmented
+sort + k-NN launch sequence serve every cloud, and the per-cloud handles are
+views into the packed result.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping
+
+import torch
+
+from ._constants import SUPPORTED_DIMS
+from ._handles import (
+    BVHHandle,
+    BatchedBVHHandle,
+    RaggedBVHHandle,
+    _batched_bvh_data,
+    _bvh_data,
+    _ragged_bvh_data,
+)
+from ._native import _C
+from ._validation import (
+    _as_contiguous,
+    _as_contiguous_int64,
+    _validate_cuda_float32,
+    _validate_offsets,
+    _validate_ragged_points,
+    _validate_supported_k,
+)
+
+_INT32_MAX = 2**31 - 1
+
+
+def _validate_narrow_build_extent(prefix: str, points: torch.Tensor) -> None:
+    total = int(points.size(0)) if points.dim() == 2 else int(points.size(0)) * int(points.size(1))
+    if total > _INT32_MAX:
+        raise ValueError(f"{prefix}: total point count must fit in signed int32")
+
+
+# ---------------------------------------------------------------------------
+# Builders
+# ---------------------------------------------------------------------------
+def _build_bvh_single(points: torch.Tensor) -> BVHHandle:
+    if points.dim() != 2:
+        raise ValueError("build_bvh: points must have shape (N, D)")
+    if points.size(1) not in SUPPORTED_DIMS:
+        raise ValueError("build_bvh: D must be 2 or 3")
+    _validate_cuda_float32("build_bvh", points, "points")
+    points = _as_contiguous(points)
+    _validate_narrow_build_extent("build_bvh", points)
+    data = _C.build_bvh_batched_cooperative(points.unsqueeze(0))
+    # A single handle carries the payload without the batch dimension.
+    del data["batch_size"]
+    for key in ("node_aabbs", "sorted_indices", "scene_min", "scene_max"):
+        data[key] = data[key].squeeze(0)
+    return BVHHandle(data)
+
+
+def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
+    if points.dim() != 3:
+        raise ValueError("build_bvh: batched points must have shape (B, N, D)")
+    if points.size(2) not in SUPPORTED_DIMS:
+        raise ValueError("build_bvh: D must be 2 or 3")
+    _validate_cuda_float32("build_bvh", points, "points")
+    points = _as_contiguous(points)
+    _validate_narrow_build_extent("build_bvh", points)
+    return BatchedBVHHandle(_C.build_bvh_batched_cooperative(points))
+
+
+def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> RaggedBVHHandle:
+    points = _as_contiguous(points)
+    batch_offsets = _as_contiguous_int64(batch_offsets)
+    offsets = _validate_ragged_points("build_bvh", points, batch_offsets)
+    _validate_narrow_build_extent("build_bvh", points)
+    counts = [b - a for a, b in zip(offsets, offsets[1:])]
+    packed = _C.build_bvh_ragged(points, batch_offsets, counts)
+    dim = int(points.size(1))
+    node_offsets = packed["host_node_offsets"]
+    handles = []
+    for b, n in enumerate(counts):
+        n0, n1 = node_offsets[b], node_offsets[b + 1]
+        p0, p1 = offsets[b], offsets[b + 1]
+        handles.append(
+            BVHHandle(
+                {
+                    "node_aabbs": packed["node_aabbs"][n0:n1],
+                    "sorted_indices": packed["sorted_indices"][p0:p1],
+                    "scene_min": packed["scene_min"][b],
+                    "scene_max": packed["scene_max"][b],
+                    "num_leaves": n,
+                    "num_real_nodes": n1 - n0,
+                    "leaf_level": (n - 1).bit_length(),
+                    "virtual_leaves": (1 << (n - 1).bit_length()) - n,
+                    "dim": dim,
+                    "left_child_mem": packed["left_child_mem"][n0:n1],
+                    "right_child_mem": packed["right_child_mem"][n0:n1],
+                    "mem_to_leaf": packed["mem_to_leaf"][n0:n1],
+                }
+            )
+        )
+    return RaggedBVHHandle(
+        {
+            "batch_offsets": batch_offsets.clone(),
+            "num_leaves_per_sample": torch.diff(batch_offsets).clone(),
+            "batch_size": len(counts),
+            "dim": dim,
+        },
+        handles,
+        aux={
+            "packed": packed,
+            "host_offsets": offsets,
+        },
+    )
+
+
+def build_bvh(
+    points: torch.Tensor,
+    *,
+    batch_offsets: torch.Tensor | None = None,
+) -> BVHHandle | BatchedBVHHandle | RaggedBVHHandle:
+    """Build a BVH; dispatches on the points' shape and ``batch_offsets``.
+
+    - ``(N, D)`` → ``BVHHandle``
+    - ``(B, N, D)`` → ``BatchedBVHHandle`` (independent trees per cloud)
+    - ``(total_N, D)`` with ``batch_offsets`` ``(B + 1,)`` → ``RaggedBVHHandle``
+
+    Ragged neighbour indices are local to each cloud.
+    """
+    if batch_offsets is not None:
+        if points.dim() != 2:
+            raise ValueError("build_bvh: ragged mode requires 2-D points (total_N, D)")
+        return _build_bvh_ragged(points, batch_offsets)
+    if points.dim() == 3:
+        return _build_bvh_batched(points)
+    if points.dim() == 2:
+        return _build_bvh_single(points)
+    raise ValueError("build_bvh: points must have shape (N, D) or (B, N, D)")
+
+
+# ---------------------------------------------------------------------------
+# Queries
+# ---------------------------------------------------------------------------
+def _query_knn_single(
+    bvh: BVHHandle,
+    query_points: torch.Tensor,
+    k: int,
+    *,
+    source_points: torch.Tensor | None = None,
+    sort_queries: bool = True,
+):
+    _validate_supported_k("query_knn", k)
+    data = _bvh_data(bvh, "query_knn")
+    if query_points.dim() != 2:
+        raise ValueError("query_knn: query_points must have shape (M, D)")
+    if query_points.size(1) != data["dim"]:
+        raise ValueError("query_knn: query_points second dimension must match BVH dim")
+    _validate_cuda_float32("query_knn", query_points, "query_points")
+    if query_points.device != data["sorted_indices"].device:
+        raise ValueError("query_knn: query_points must be on the same device as the BVH")
+    queries = _as_contiguous(query_points).unsqueeze(0)
+    node_aabbs = data["node_aabbs"].unsqueeze(0)
+    sorted_indices = data["sorted_indices"].unsqueeze(0)
+    if sort_queries:
+        order = _C.morton_sort_queries_narrow(
+            queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0)
+        )
+        indices, distances = _C.query_knn_batched_cached_bounds_ordered(
+            node_aabbs, sorted_indices, queries, order.contiguous(),
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+        )
+    else:
+        indices, distances = _C.query_knn_batched_cached_bounds(
+            node_aabbs, sorted_indices, queries,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+        )
+    indices = indices.squeeze(0)
+    distances = distances.squeeze(0)
+    if source_points is None:
+        return indices, distances
+    _validate_single_source_points("query_knn", data, source_points)
+    return indices, distances, _as_contiguous(source_points)[indices]
+
+
+def _validate_single_source_points(prefix: str, data: Mapping, source_points: torch.Tensor) -> None:
+    if source_points.dim() != 2:
+        raise ValueError(f"{prefix}: source_points must have shape (N, D)")
+    if source_points.size(0) != data["num_leaves"]:
+        raise ValueError(f"{prefix}: source_points first dimension must match BVH num_leaves")
+    if source_points.size(1) != data["dim"]:
+        raise ValueError(f"{prefix}: source_points second dimension must match BVH dim")
+    _validate_cuda_float32(prefix, source_points, "source_points")
+    if source_points.device != data["sorted_indices"].device:
+        raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
+
+
+def _validate_batched_source_points(prefix: str, data: Mapping, source_points: torch.Tensor) -> None:
+    if source_points.dim() != 3:
+        raise ValueError(f"{prefix}: source_points must have shape (B, N, D)")
+    if source_points.size(0) != data["batch_size"]:
+        raise ValueError(f"{prefix}: source_points batch size must match BVH batch_size")
+    if source_points.size(1) != data["num_leaves"]:
+        raise ValueError(f"{prefix}: source_points second dimension must match BVH num_leaves")
+    if source_points.size(2) != data["dim"]:
+        raise ValueError(f"{prefix}: source_points last dimension must match BVH dim")
+    _validate_cuda_float32(prefix, source_points, "source_points")
+    if source_points.device != data["sorted_indices"].device:
+        raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
+
+
+def _gather_batched_neighbor_positions(source_points, indices) -> torch.Tensor:
+    B, M, K = indices.shape
+    D = source_points.size(2)
+    flat = indices.reshape(B, M * K, 1).expand(-1, -1, D)
+    return torch.gather(source_points, 1, flat).reshape(B, M, K, D)
+
+
+def _query_knn_batched(
+    bvh: BatchedBVHHandle,
+    query_points: torch.Tensor,
+    k: int,
+    *,
+    source_points: torch.Tensor | None = None,
+    sort_queries: bool = True,
+):
+    _validate_supported_k("query_knn", k)
+    data = _batched_bvh_data(bvh, "query_knn")
+    if query_points.dim() != 3:
+        raise ValueError("query_knn: batched query_points must have shape (B, M, D)")
+    if query_points.size(0) != data["batch_size"]:
+        raise ValueError("query_knn: query_points batch size must match BVH batch_size")
+    if query_points.size(2) != data["dim"]:
+        raise ValueError("query_knn: query_points last dimension must match BVH dim")
+    _validate_cuda_float32("query_knn", query_points, "query_points")
+    if query_points.device != data["sorted_indices"].device:
+        raise ValueError("query_knn: query_points must be on the same device as the BVH")
+    queries = _as_contiguous(query_points)
+    if sort_queries:
+        order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"])
+        indices, distances = _C.query_knn_batched_cached_bounds_ordered(
+            data["node_aabbs"], data["sorted_indices"], queries, order.contiguous(),
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+        )
+    else:
+        indices, distances = _C.query_knn_batched_cached_bounds(
+            data["node_aabbs"], data["sorted_indices"], queries,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+        )
+    if source_points is None:
+        return indices, distances
+    _validate_batched_source_points("query_knn", data, source_points)
+    positions = _gather_batched_neighbor_positions(_as_contiguous(source_points), indices)
+    return indices, distances, positions
+
+
+def _validate_ragged_source_points(prefix, data, source_points, *, total_rows, device) -> None:
+    if source_points.dim() != 2:
+        raise ValueError(f"{prefix}: ragged source_points must have shape (total_N, D)")
+    if source_points.size(0) != total_rows:
+        raise ValueError(f"{prefix}: source_points first dimension must match BVH total_N")
+    if source_points.size(1) != data["dim"]:
+        raise ValueError(f"{prefix}: source_points second dimension must match BVH dim")
+    _validate_cuda_float32(prefix, source_points, "source_points")
+    if source_points.device != device:
+        raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
+
+
+def _query_knn_ragged(
+    bvh: RaggedBVHHandle,
+    query_points: torch.Tensor,
+    query_offsets: torch.Tensor,
+    k: int,
+    *,
+    source_points: torch.Tensor | None = None,
+):
+    _validate_supported_k("query_knn", k)
+    data, _handles = _ragged_bvh_data(bvh, "query_knn")
+    if query_points.dim() != 2:
+        raise ValueError("query_knn: ragged query_points must have shape (total_M, D)")
+    if query_points.size(1) != data["dim"]:
+        raise ValueError("query_knn: query_points second dimension must match BVH dim")
+    _validate_cuda_float32("query_knn", query_points, "query_points")
+    if query_points.device != data["batch_offsets"].device:
+        raise ValueError("query_knn: query_points must be on the same device as the BVH")
+    queries = _as_contiguous(query_points)
+    query_offsets = _as_contiguous_int64(query_offsets)
+    q_offsets = _validate_offsets(
+        "query_knn", query_offsets, total_rows=int(queries.size(0)), device=queries.device
+    )
+    if len(q_offsets) - 1 != data["batch_size"]:
+        raise ValueError("query_knn: query_offsets batch size must match BVH batch_size")
+    p_offsets = bvh._aux["host_offsets"]
+    if any(b - a < k for a, b in zip(p_offsets, p_offsets[1:])):
+        raise ValueError("query_knn: each source sample must contain at least k points")
+    if source_points is not None:
+        _validate_ragged_source_points(
+            "query_knn", data, source_points, total_rows=p_offsets[-1], device=queries.device
+        )
+        source_points = _as_contiguous(source_points)
+
+    packed = bvh._aux["packed"]
+    order = _C.morton_sort_queries_ragged(
+        queries, query_offsets, packed["scene_min"], packed["scene_max"], data["batch_size"]
+    )
+    indices, distances = _C.query_knn_ragged(
+        packed["node_aabbs"], packed["sorted_indices"], data["batch_offsets"],
+        packed["node_offsets"], queries, query_offsets, order, data["batch_size"],
+        data["dim"], k,
+    )
+    if source_points is None:
+        return indices, distances
+    counts = torch.tensor(
+        [b - a for a, b in zip(q_offsets, q_offsets[1:])], device=queries.device
+    )
+    starts = data["batch_offsets"][:-1].repeat_interleave(counts)
+    positions = source_points[indices + starts[:, None]]
+    return indices, distances, positions
+
+
+def query_knn(
+    bvh: BVHHandle | BatchedBVHHandle | RaggedBVHHandle,
+    query_points: torch.Tensor,
+    k: int,
+    *,
+    query_offsets: torch.Tensor | None = None,
+    source_points: torch.Tensor | None = None,
+    sort_queries: bool = True,
+):
+    """Exact k nearest neighbours; dispatches on the handle type.
+
+    Returns ``(indices int64, squared_distances fp32)`` with rows ascending by
+    (distance, index), or ``(indices, squared_distances, neighbor_positions)``
+    when ``source_points`` is given.  Shapes: ``(M, k)`` single, ``(B, M, k)``
+    batched, packed ``(total_M, k)`` ragged (``query_offsets`` required).
+    """
+    if isinstance(bvh, RaggedBVHHandle):
+        if query_offsets is None:
+            raise ValueError("query_knn: query_offsets is required when querying a ragged BVH")
+        return _query_knn_ragged(bvh, query_points, query_offsets, k, source_points=source_points)
+    if query_offsets is not None:
+        raise TypeError("query_knn: query_offsets requires a RaggedBVHHandle")
+    if isinstance(bvh, BatchedBVHHandle):
+        return _query_knn_batched(
+            bvh, query_points, k, source_points=source_points, sort_queries=sort_queries
+        )
+    return _query_knn_single(
+        bvh, query_points, k, source_points=source_points, sort_queries=sort_queries
+    )

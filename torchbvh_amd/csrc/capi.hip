@@ -1,0 +1,397 @@
+// C ABI entry points (declared in include/torchbvh_amd.h): argument checks,
+// workspace carving and launch sequencing.  No entry point allocates device
+// memory or synchronises the host.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/torchbvh_amd.h"
+#include "tbvh_internal.hpp"
+
+using namespace tbvh;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return TBVH_OK;
+}
+
+int hip_fail(const char* op, hipError_t e) {
+    return fail(TBVH_ERR_HIP, "%s: HIP error %d (%s)", op, static_cast<int>(e), hipGetErrorString(e));
+}
+
+#define TBVH_TRY(op, expr)                       \
+    do {                                         \
+        const hipError_t e_ = (expr);            \
+        if (e_ != hipSuccess) return hip_fail(op, e_); \
+    } while (0)
+
+// Largest cloud the implicit-tree index math supports (heap indices of the
+// 2^(L+1) - 1 slots must fit in int32).
+constexpr int64_t kMaxCloud = int64_t(1) << 30;
+constexpr int64_t kMaxRows = 2147483647;  // INT32_MAX
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Workspace carve-out shared by build and query sort.
+struct Layout {
+    size_t segs = 0, partials = 0, keys_a = 0, keys_b = 0, vals_a = 0, vals_b = 0;
+    size_t hist = 0, dpre = 0, total = 0;
+};
+
+Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials) {
+    Layout l;
+    const int64_t tiles = tiles_bound(rows, S);
+    size_t at = 0;
+    l.segs = at; at = align_up(at + static_cast<size_t>(S) * sizeof(Segment));
+    l.partials = at; at = align_up(at + (with_partials ? static_cast<size_t>(tiles) * 2 * D * sizeof(float) : 0));
+    l.keys_a = at; at = align_up(at + static_cast<size_t>(rows) * 4);
+    l.keys_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
+    l.vals_a = at; at = align_up(at + static_cast<size_t>(rows) * 4);
+    l.vals_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
+    l.hist = at; at = align_up(at + static_cast<size_t>(tiles) * kRadix * 4);
+    l.dpre = at; at = align_up(at + static_cast<size_t>(tiles) * kRadix * 4);
+    l.total = at;
+    return l;
+}
+
+template <typename T>
+T* carve(void* ws, size_t off) {
+    return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+SortBuffers sort_buffers(void* ws, const Layout& l) {
+    SortBuffers b;
+    b.keys_a = carve<uint32_t>(ws, l.keys_a);
+    b.keys_b = carve<uint32_t>(ws, l.keys_b);
+    b.vals_a = carve<uint32_t>(ws, l.vals_a);
+    b.vals_b = carve<uint32_t>(ws, l.vals_b);
+    b.hist = carve<uint32_t>(ws, l.hist);
+    b.dpre = carve<uint32_t>(ws, l.dpre);
+    return b;
+}
+
+int check_dim(const char* op, int D) {
+    if (D != 2 && D != 3) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: D must be 2 or 3, got %d", op, D);
+    return TBVH_OK;
+}
+
+int check_batched_extent(const char* op, int64_t B, int64_t N) {
+    if (B < 1 || N < 1) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: B and N must be >= 1", op);
+    if (N > kMaxCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: a cloud may hold at most 2^30 points", op);
+    if (B > kMaxRows / N) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    return TBVH_OK;
+}
+
+int check_workspace(const char* op, void* ws, size_t have, size_t need) {
+    if (have < need) {
+        return fail(TBVH_ERR_WORKSPACE_TOO_SMALL, "%s: workspace holds %zu bytes, %zu required", op, have, need);
+    }
+    if (need > 0 && ws == nullptr) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: workspace is null", op);
+    if (reinterpret_cast<uintptr_t>(ws) % kAlign != 0) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: workspace must be %zu-byte aligned", op, kAlign);
+    }
+    return TBVH_OK;
+}
+
+bool supported_k(int k) { return k == 4 || k == 8 || k == 16 || k == 32; }
+
+}  // namespace
+
+extern "C" {
+
+int tbvh_abi_version(void) { return TBVH_ABI_VERSION; }
+
+const char* tbvh_last_error(void) { return g_last_error.c_str(); }
+
+int tbvh_leaf_level(int64_t n) {
+    if (n < 1 || n > kMaxCloud) return -1;
+    return tree::leaf_level(static_cast<int>(n));
+}
+
+int64_t tbvh_virtual_leaves(int64_t n) {
+    if (n < 1 || n > kMaxCloud) return -1;
+    return tree::virtual_leaves(static_cast<int>(n));
+}
+
+int64_t tbvh_real_node_count(int64_t n) {
+    if (n < 1 || n > kMaxCloud) return -1;
+    return tree::real_node_count(static_cast<int>(n));
+}
+
+// ---------------------------------------------------------------------------
+// Build
+// ---------------------------------------------------------------------------
+int tbvh_build_workspace_size(int64_t B, int64_t N, int D, size_t* bytes) {
+    const char* op = "tbvh_build_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    *bytes = make_layout(B, B * N, D, true).total;
+    return ok();
+}
+
+int tbvh_build(const float* points, int64_t B, int64_t N, int D, float* node_aabbs,
+               int64_t* sorted_indices, float* scene_min, float* scene_max,
+               int32_t* left_child_mem, int32_t* right_child_mem, int32_t* mem_to_leaf,
+               void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_build";
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    if (!points || !node_aabbs || !sorted_indices || !scene_min || !scene_max ||
+        !left_child_mem || !right_child_mem || !mem_to_leaf) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const int64_t rows = B * N;
+    const Layout l = make_layout(B, rows, D, true);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, l.segs);
+    const int64_t tiles = tiles_bound(rows, B);
+    const SortBuffers sb = sort_buffers(workspace, l);
+    const int nr = tree::real_node_count(static_cast<int>(N));
+
+    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
+    TBVH_TRY(op, launch_bounds(points, D, segs, B, tiles, carve<float>(workspace, l.partials),
+                               scene_min, scene_max, stream));
+    TBVH_TRY(op, launch_morton(points, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
+                               sb.hist, sb.dpre, stream));
+    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, sorted_indices, stream));
+    TBVH_TRY(op, launch_tree(points, D, segs, B, rows, N, sorted_indices, node_aabbs, stream));
+    TBVH_TRY(op, launch_traversal_arrays(segs, 1, nr, left_child_mem, right_child_mem, mem_to_leaf,
+                                         stream));
+    return ok();
+}
+
+int tbvh_build_ragged_workspace_size(int64_t B, int64_t total, int D, size_t* bytes) {
+    const char* op = "tbvh_build_ragged_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || total < B) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total >= B", op);
+    if (total > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    *bytes = make_layout(B, total, D, true).total;
+    return ok();
+}
+
+int tbvh_build_ragged(const float* points, const int64_t* offsets, int64_t B, int64_t total, int D,
+                      float* node_aabbs, int64_t* sorted_indices, float* scene_min,
+                      float* scene_max, int32_t* left_child_mem, int32_t* right_child_mem,
+                      int32_t* mem_to_leaf, int64_t* node_offsets, int64_t total_nodes,
+                      void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_build_ragged";
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || total < B) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total >= B", op);
+    if (total > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    if (total_nodes < 2 * total - B) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total_nodes is smaller than any tree over %lld points",
+                    op, static_cast<long long>(total));
+    }
+    if (!points || !offsets || !node_aabbs || !sorted_indices || !scene_min || !scene_max ||
+        !left_child_mem || !right_child_mem || !mem_to_leaf || !node_offsets) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const Layout l = make_layout(B, total, D, true);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, l.segs);
+    const int64_t tiles = tiles_bound(total, B);
+    const SortBuffers sb = sort_buffers(workspace, l);
+    const int64_t max_n = total < kMaxCloud ? total : kMaxCloud;
+
+    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, node_offsets, stream));
+    TBVH_TRY(op, launch_bounds(points, D, segs, B, tiles, carve<float>(workspace, l.partials),
+                               scene_min, scene_max, stream));
+    TBVH_TRY(op, launch_morton(points, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
+                               sb.hist, sb.dpre, stream));
+    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, sorted_indices, stream));
+    TBVH_TRY(op, launch_tree(points, D, segs, B, total, max_n, sorted_indices, node_aabbs, stream));
+    TBVH_TRY(op, launch_traversal_arrays(segs, B, total_nodes, left_child_mem, right_child_mem,
+                                         mem_to_leaf, stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Query ordering
+// ---------------------------------------------------------------------------
+int tbvh_sort_queries_workspace_size(int64_t B, int64_t M, int D, size_t* bytes) {
+    const char* op = "tbvh_sort_queries_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    *bytes = make_layout(B, B * M, D, false).total;
+    return ok();
+}
+
+int tbvh_sort_queries(const float* queries, int64_t B, int64_t M, int D, const float* scene_min,
+                      const float* scene_max, int64_t* order, void* workspace,
+                      size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_sort_queries";
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (M == 0) return ok();
+    if (M > kMaxCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: at most 2^30 queries per cloud", op);
+    if (!queries || !scene_min || !scene_max || !order) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const int64_t rows = B * M;
+    const Layout l = make_layout(B, rows, D, false);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, l.segs);
+    const int64_t tiles = tiles_bound(rows, B);
+    const SortBuffers sb = sort_buffers(workspace, l);
+    TBVH_TRY(op, launch_plan_uniform(segs, B, M, false, stream));
+    TBVH_TRY(op, launch_morton(queries, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
+                               sb.hist, sb.dpre, stream));
+    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, order, stream));
+    return ok();
+}
+
+int tbvh_morton_codes(const float* rows, int64_t B, int64_t M, int D, const float* scene_min,
+                      const float* scene_max, uint32_t* codes, void* workspace,
+                      size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_morton_codes";
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total row count must fit in signed int32", op);
+    if (M == 0) return ok();
+    if (M > kMaxCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: at most 2^30 rows per cloud", op);
+    if (!rows || !scene_min || !scene_max || !codes) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const int64_t n = B * M;
+    const Layout l = make_layout(B, n, D, false);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, l.segs);
+    const SortBuffers sb = sort_buffers(workspace, l);
+    TBVH_TRY(op, launch_plan_uniform(segs, B, M, false, stream));
+    TBVH_TRY(op, launch_morton(rows, D, segs, B, tiles_bound(n, B), scene_min, scene_max, codes,
+                               sb.hist, sb.dpre, stream));
+    return ok();
+}
+
+int tbvh_sort_queries_ragged_workspace_size(int64_t B, int64_t total_q, int D, size_t* bytes) {
+    const char* op = "tbvh_sort_queries_ragged_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
+    if (total_q > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    *bytes = make_layout(B, total_q, D, false).total;
+    return ok();
+}
+
+int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets, int64_t B,
+                             int64_t total_q, int D, const float* scene_min,
+                             const float* scene_max, int64_t* order, void* workspace,
+                             size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_sort_queries_ragged";
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
+    if (total_q > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (total_q == 0) return ok();
+    if (!queries || !query_offsets || !scene_min || !scene_max || !order) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const Layout l = make_layout(B, total_q, D, false);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, l.segs);
+    const int64_t tiles = tiles_bound(total_q, B);
+    const SortBuffers sb = sort_buffers(workspace, l);
+    TBVH_TRY(op, launch_plan_offsets(segs, query_offsets, B, false, nullptr, stream));
+    TBVH_TRY(op, launch_morton(queries, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
+                               sb.hist, sb.dpre, stream));
+    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, order, stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// k-NN
+// ---------------------------------------------------------------------------
+int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices, const float* queries,
+             const int64_t* order, int64_t B, int64_t M, int64_t num_leaves,
+             int64_t num_real_nodes, int D, int k, int64_t* out_indices, float* out_distances,
+             void* stream_ptr) {
+    const char* op = "tbvh_knn";
+    if (int r = check_dim(op, D)) return r;
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (num_leaves < 1 || num_leaves > kMaxCloud) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_leaves must be in [1, 2^30]", op);
+    }
+    if (num_leaves < k) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_leaves must be >= k", op);
+    if (num_real_nodes != tree::real_node_count(static_cast<int>(num_leaves))) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_real_nodes does not match num_leaves", op);
+    }
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (B > kMaxRows / num_leaves) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    if (M == 0) return ok();
+    if (!node_aabbs || !sorted_indices || !queries || !out_indices || !out_distances) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    KnnArgs a{};
+    a.node_aabbs = node_aabbs;
+    a.sorted_indices = sorted_indices;
+    a.queries = queries;
+    a.order = order;
+    a.B = B;
+    a.M = M;
+    a.total_q = B * M;
+    a.num_leaves = static_cast<int32_t>(num_leaves);
+    a.num_real_nodes = static_cast<int32_t>(num_real_nodes);
+    a.out_indices = out_indices;
+    a.out_distances = out_distances;
+    TBVH_TRY(op, launch_knn(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
+                    const int64_t* point_offsets, const int64_t* node_offsets,
+                    const float* queries, const int64_t* query_offsets, const int64_t* order,
+                    int64_t B, int64_t total_q, int D, int k, int64_t* out_indices,
+                    float* out_distances, void* stream_ptr) {
+    const char* op = "tbvh_knn_ragged";
+    if (int r = check_dim(op, D)) return r;
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
+    if (total_q > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (total_q == 0) return ok();
+    if (!node_aabbs || !sorted_indices || !point_offsets || !node_offsets || !queries ||
+        !query_offsets || !out_indices || !out_distances) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    KnnArgs a{};
+    a.node_aabbs = node_aabbs;
+    a.sorted_indices = sorted_indices;
+    a.queries = queries;
+    a.order = order;
+    a.point_offsets = point_offsets;
+    a.node_offsets = node_offsets;
+    a.query_offsets = query_offsets;
+    a.B = B;
+    a.total_q = total_q;
+    a.out_indices = out_indices;
+    a.out_distances = out_distances;
+    TBVH_TRY(op, launch_knn(a, D, k, true, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+}  // extern "C"

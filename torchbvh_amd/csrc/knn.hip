@@ -1,0 +1,184 @@
+// Exact k-NN by branch-and-bound over the implicit BVH.
+//
+// Follows the reference traversal (torchbvh/csrc/knn_query.cu:47-154): one
+// query per lane, launched in Morton order when an order is given; root box
+// distance first; at an internal node both real children's box distances are
+// evaluated, the far child is deferred on a stack with its distance cached if
+// it can still hold a candidate, and the near child is entered; nodes are
+// visited while their box distance is <= the current k-th distance.
+//
+// The candidate list is where this kernel deliberately differs: entries are
+// 64-bit keys (float bits of the squared distance << 32 | point index) kept
+// in ascending order in registers.  Squared distances are >= 0, so their bit
+// patterns order like the floats and one unsigned compare orders candidates
+// lexicographically by (distance, index).  The result is therefore the k
+// smallest (distance, index) pairs, independent of traversal order: exact
+// ties resolve to the lower point index.  Empty slots hold (FLT_MAX, -1),
+// the reference's initial values (knn_query.cu:13, :83-85).
+//
+// Distances: delta_d = max(lo - q, max(0, q - hi)) per axis (geometry.cuh:3-18)
+// accumulated as fma(d2, d2, fma(d1, d1, d0 * d0)), the contraction the
+// reference's `dist += delta * delta` loop compiles to.  On a leaf's
+// degenerate box this is the exact point distance with delta = |q - p|.
+#include <float.h>
+
+#include "tbvh_internal.hpp"
+
+namespace tbvh {
+namespace {
+
+constexpr float kFar = FLT_MAX;
+constexpr int kStackDepth = 32;
+
+template <int D>
+__device__ __forceinline__ float box_distance(const float* q, const float* box) {
+    float s = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const float delta = fmaxf(box[d] - q[d], fmaxf(0.0f, q[d] - box[D + d]));
+        s = d == 0 ? delta * delta : __builtin_fmaf(delta, delta, s);
+    }
+    return s;
+}
+
+__device__ __forceinline__ uint64_t candidate_key(float dist, uint32_t idx) {
+    return (static_cast<uint64_t>(__float_as_uint(dist)) << 32) | idx;
+}
+
+// Insert `key` into the ascending list `best`, dropping the largest entry.
+template <int K>
+__device__ __forceinline__ void insert_sorted(uint64_t (&best)[K], uint64_t key) {
+    bool lt[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) lt[i] = key < best[i];
+#pragma unroll
+    for (int i = K - 1; i > 0; --i) best[i] = lt[i - 1] ? best[i - 1] : (lt[i] ? key : best[i]);
+    best[0] = lt[0] ? key : best[0];
+}
+
+template <int D, int K, bool kOrdered, bool kRagged>
+__global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (gid >= a.total_q) return;
+
+    int64_t seg, qbase, qcount, pstart, nstart;
+    int n;
+    if constexpr (kRagged) {
+        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
+        qbase = a.query_offsets[seg];
+        qcount = a.query_offsets[seg + 1] - qbase;
+        pstart = a.point_offsets[seg];
+        n = static_cast<int>(a.point_offsets[seg + 1] - pstart);
+        nstart = a.node_offsets[seg];
+    } else {
+        seg = gid / a.M;
+        qbase = seg * a.M;
+        qcount = a.M;
+        n = a.num_leaves;
+        pstart = seg * static_cast<int64_t>(n);
+        nstart = seg * static_cast<int64_t>(a.num_real_nodes);
+    }
+    const int64_t local = gid - qbase;
+    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
+    if (qi < 0 || qi >= qcount) return;  // a corrupt order never indexes out of range
+    const int64_t row = qbase + qi;
+    const float* nodes = a.node_aabbs + nstart * 2 * D;
+    const int64_t* sorted = a.sorted_indices + pstart;
+
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) q[d] = a.queries[row * D + d];
+
+    const int L = tree::leaf_level(n);
+    const int vl = tree::virtual_leaves(n);
+    const int first_leaf = tree::level_first(L);
+
+    uint64_t best[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
+
+    uint64_t stack[kStackDepth];
+    int sp = 0;
+    int node = 0;
+    float nd = box_distance<D>(q, nodes);
+
+    while (true) {
+        const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
+        if (nd <= worst) {
+            if (node >= first_leaf) {
+                const uint32_t idx = static_cast<uint32_t>(sorted[node - first_leaf]);
+                const uint64_t key = candidate_key(nd, idx);
+                if (nd < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+            } else {
+                const int lc = 2 * node + 1;
+                const int rc = lc + 1;
+                const bool right_real = !tree::is_virtual(vl, L, rc);
+                const int lrow = tree::memory_index(vl, L, lc);
+                const float* box = nodes + static_cast<int64_t>(lrow) * 2 * D;
+                const float ld = box_distance<D>(q, box);
+                const float rd = right_real ? box_distance<D>(q, box + 2 * D) : kFar;
+                const bool left_near = ld <= rd;
+                const int near_node = left_near ? lc : rc;
+                const int far_node = left_near ? rc : lc;
+                const float near_d = left_near ? ld : rd;
+                const float far_d = left_near ? rd : ld;
+                const bool far_real = left_near ? right_real : true;
+                const bool near_real = left_near ? true : right_real;
+                if (far_real && far_d <= worst) {
+                    stack[sp++] = (static_cast<uint64_t>(far_node) << 32) | __float_as_uint(far_d);
+                }
+                if (near_real && near_d <= worst) {
+                    node = near_node;
+                    nd = near_d;
+                    continue;
+                }
+            }
+        }
+        if (sp == 0) break;
+        const uint64_t e = stack[--sp];
+        node = static_cast<int>(e >> 32);
+        nd = __uint_as_float(static_cast<uint32_t>(e));
+    }
+
+    int64_t* oi = a.out_indices + row * K;
+    float* od = a.out_distances + row * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        oi[i] = static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(best[i])));
+        od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
+    }
+}
+
+template <int D, int K>
+hipError_t launch_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>((a.total_q + kBlock - 1) / kBlock);
+    const bool ordered = a.order != nullptr;
+    if (ragged) {
+        if (ordered) knn_kernel<D, K, true, true><<<grid, kBlock, 0, stream>>>(a);
+        else knn_kernel<D, K, false, true><<<grid, kBlock, 0, stream>>>(a);
+    } else {
+        if (ordered) knn_kernel<D, K, true, false><<<grid, kBlock, 0, stream>>>(a);
+        else knn_kernel<D, K, false, false><<<grid, kBlock, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_d(const KnnArgs& a, int K, bool ragged, hipStream_t stream) {
+    switch (K) {
+        case 4: return launch_dk<D, 4>(a, ragged, stream);
+        case 8: return launch_dk<D, 8>(a, ragged, stream);
+        case 16: return launch_dk<D, 16>(a, ragged, stream);
+        case 32: return launch_dk<D, 32>(a, ragged, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream) {
+    if (a.total_q == 0) return hipSuccess;
+    return D == 3 ? launch_d<3>(a, K, ragged, stream) : launch_d<2>(a, K, ragged, stream);
+}
+
+}  // namespace tbvh

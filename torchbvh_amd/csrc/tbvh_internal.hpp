@@ -1,0 +1,139 @@
+// Internal (non-ABI) declarations shared by the HIP translation units:
+// wavefront helpers and the host-side launchers each unit provides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "tbvh_common.hpp"
+
+namespace tbvh {
+
+constexpr int kWave = 64;     // CDNA wavefront width
+constexpr int kBlock = 256;   // threads per work-group for every kernel here
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;
+constexpr float kSeedLo = 1.0e30f;   // bounds seeds (reference: bvh_build.cu:466-467)
+constexpr float kSeedHi = -1.0e30f;
+
+// ---------------------------------------------------------------------------
+// Wavefront / work-group helpers (device)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return static_cast<int>(__lane_id()); }
+
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = __shfl_up(v, d, kWave);
+        if (lane_id() >= d) v += o;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) v = fminf(v, __shfl_xor(v, d, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, kWave));
+    return v;
+}
+
+// Exclusive prefix sum of one value per thread over a kBlock-thread group.
+// `scratch` must hold kBlock / kWave words.  Contains __syncthreads().
+__device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* scratch,
+                                                        uint32_t* total = nullptr) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    const uint32_t incl = wave_inclusive_sum(v);
+    if (lane == kWave - 1) scratch[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w) {
+        const uint32_t t = scratch[w];
+        before += (w < wave) ? t : 0u;
+        all += t;
+    }
+    __syncthreads();
+    if (total) *total = all;
+    return before + incl - v;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (host).  Every launcher enqueues on `stream` and returns the
+// launch status.
+// ---------------------------------------------------------------------------
+// Planning: fill the segment table.
+hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream);
+hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
+                               int64_t* node_offsets, hipStream_t stream);
+
+// Bounds: per-tile partials, then per-segment reduction into scene_min/max.
+hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
+                         int64_t tiles_bound, float* partials,
+                         float* scene_min, float* scene_max, hipStream_t stream);
+
+// Morton codes of every row against its segment's bounds, plus the digit-0
+// tile histograms of the first sort pass.
+hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
+                         int64_t tiles_bound, const float* scene_min, const float* scene_max,
+                         uint32_t* keys, uint32_t* hist, uint32_t* dpre, hipStream_t stream);
+
+// Stable LSD sort of (key, local index) per segment; writes int64 local
+// indices in key order into `order`.  `keys` is clobbered.
+struct SortBuffers {
+    uint32_t* keys_a;   // input keys (Morton kernel output)
+    uint32_t* keys_b;
+    uint32_t* vals_a;
+    uint32_t* vals_b;
+    uint32_t* hist;     // kRadix * tiles_bound words
+    uint32_t* dpre;     // kRadix * tiles_bound words
+};
+hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles_bound, int key_bits,
+                       const SortBuffers& buf, int64_t* order, hipStream_t stream);
+
+// Implicit-tree node AABBs (all passes) and traversal arrays.
+// `max_n` bounds the largest cloud (it decides how many passes run).
+hipError_t launch_tree(const float* points, int D, const Segment* segs, int64_t S,
+                       int64_t total, int64_t max_n, const int64_t* sorted, float* node_aabbs,
+                       hipStream_t stream);
+hipError_t launch_traversal_arrays(const Segment* segs, int64_t S, int64_t total_nodes,
+                                   int32_t* left, int32_t* right, int32_t* leaf,
+                                   hipStream_t stream);
+
+// k-NN traversal.
+struct KnnArgs {
+    const float* node_aabbs;
+    const int64_t* sorted_indices;
+    const float* queries;
+    const int64_t* order;          // may be null
+    const int64_t* point_offsets;  // ragged only
+    const int64_t* node_offsets;   // ragged only
+    const int64_t* query_offsets;  // ragged only
+    int64_t B;
+    int64_t M;                     // batched: queries per cloud
+    int64_t total_q;
+    int32_t num_leaves;            // batched only
+    int32_t num_real_nodes;        // batched only
+    int64_t* out_indices;
+    float* out_distances;
+};
+hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
+
+// Tile-count bound for S segments holding `total` rows in kSortTile tiles.
+inline int64_t tiles_bound(int64_t total, int64_t S) {
+    return (total + kSortTile - 1) / kSortTile + S;
+}
+
+}  // namespace tbvh
