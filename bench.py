@@ -170,6 +170,8 @@ def main() -> int:
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-sample", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--implicit-reps", type=int, default=1,
+                    help="also time the traversal over the implicit tree (0 = skip)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -240,7 +242,7 @@ def main() -> int:
     # native calls on the current stream (the traversal is a single kernel).
     from torchbvh_amd._native import _C
 
-    sort_ms = trav_ms = 0.0
+    sort_ms = trav_ms = implicit_ms = 0.0
     if kind != "ragged":
         bvh, _ = step()
         data = bvh
@@ -249,6 +251,7 @@ def main() -> int:
         smax = data["scene_max"] if kind == "batched" else data["scene_max"].unsqueeze(0)
         nodes = data["node_aabbs"] if kind == "batched" else data["node_aabbs"].unsqueeze(0)
         sidx = data["sorted_indices"] if kind == "batched" else data["sorted_indices"].unsqueeze(0)
+        accel = bvh._aux["accel"]
         reps = max(args.steps, 5)
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3 * reps)]
         torch.cuda.synchronize()
@@ -257,11 +260,22 @@ def main() -> int:
             order = _C.morton_sort_queries_narrow(qb, smin, smax)
             e[3 * r + 1].record()
             _C.query_knn_batched_cached_bounds_ordered(
-                nodes, sidx, qb, order, data["num_leaves"], data["num_real_nodes"], D, k)
+                nodes, sidx, qb, order, data["num_leaves"], data["num_real_nodes"], D, k,
+                accel=accel)
             e[3 * r + 2].record()
         torch.cuda.synchronize()
         sort_ms = sum(e[3 * r].elapsed_time(e[3 * r + 1]) for r in range(reps)) / reps
         trav_ms = sum(e[3 * r + 1].elapsed_time(e[3 * r + 2]) for r in range(reps)) / reps
+        if args.implicit_reps > 0:
+            # The same query over the reference's implicit tree, for comparison.
+            ei = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ei[0].record()
+            for _ in range(args.implicit_reps):
+                _C.query_knn_batched_cached_bounds_ordered(
+                    nodes, sidx, qb, order, data["num_leaves"], data["num_real_nodes"], D, k)
+            ei[1].record()
+            torch.cuda.synchronize()
+            implicit_ms = ei[0].elapsed_time(ei[1]) / args.implicit_reps
 
     value = total_q / (ms_per_step * 1e-3)
     trav_gbs = n_bytes / (trav_ms * 1e-3) / 1e9 if trav_ms > 0 else None
@@ -290,13 +304,14 @@ def main() -> int:
         "query_ms": query_ms,
         "query_sort_ms": sort_ms,
         "traversal_ms": trav_ms,
+        "traversal_implicit_tree_ms": implicit_ms or None,
         "queries_per_s_excl_build": total_q / (query_ms * 1e-3) if query_ms > 0 else None,
         "build_hbm_frac_algorithmic": (b_bytes / (build_ms * 1e-3) / 1e9) / HBM_PEAK_GBS,
         "query_sort_hbm_frac_algorithmic": ((s_bytes / (sort_ms * 1e-3) / 1e9) / HBM_PEAK_GBS
                                             if sort_ms > 0 else None),
         "roofline": {
             "bound": "hbm",
-            "kernel": "knn_kernel (traversal)",
+            "kernel": "knn_accel_kernel (traversal)",
             "achieved": trav_gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

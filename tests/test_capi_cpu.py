@@ -117,3 +117,20 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(RuntimeError, match="not built"):
         _native.load()
+
+
+def test_accel_argument_errors():
+    L = _native.load()
+    size = ctypes.c_size_t()
+    assert L.tbvh_accel_size(2, 1, 3, ctypes.byref(size)) == 1
+    assert L.tbvh_accel_size(2, 1000, 3, ctypes.byref(size)) == 0
+    assert size.value == ((1000 * 16 + 255) // 256) * 256 + (1000 - 2) * 16 * 4
+    assert L.tbvh_accel_workspace_size(1, 1000, 2, ctypes.byref(size)) == 0
+    need = size.value
+    args = [FAKE] * 5 + [1, 1000, 2, FAKE]
+    assert L.tbvh_accel_build(*args, FAKE, need - 1, None) == 2
+    assert L.tbvh_accel_build(*([FAKE] * 5), 1, (1 << 28) + 1, 3, FAKE, FAKE, 1 << 40, None) == 1
+    assert "2^28" in _err(L)
+    assert L.tbvh_knn_accel(FAKE, FAKE, None, 1, 10, 3, 3, 4, FAKE, FAKE, None) == 1
+    assert "num_leaves must be >= k" in _err(L)
+    assert L.tbvh_knn_accel(None, None, None, 1, 0, 100, 3, 4, None, None, None) == 0

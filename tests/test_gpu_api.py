@@ -84,14 +84,15 @@ def test_sort_queries_routes_through_ordered_traversal(monkeypatch):
         B, M, _ = qb.shape
         return torch.arange(M, device=qb.device).expand(B, M).contiguous()
 
-    def fake_ordered(*args):
+    def fake_ordered(*args, accel=None):
+        assert accel is not None
         calls.append(("ordered", tuple(args[3].shape), args[-1]))
         B, M, _ = args[2].shape
         k = int(args[-1])
         return (torch.zeros((B, M, k), device=DEV, dtype=torch.int64),
                 torch.zeros((B, M, k), device=DEV))
 
-    def fake_unordered(*args):
+    def fake_unordered(*args, **kwargs):
         raise AssertionError("unordered route must not be used when sort_queries=True")
 
     monkeypatch.setattr(query_module._C, "morton_sort_queries_narrow", fake_sort)
@@ -246,8 +247,9 @@ def test_noncontiguous_inputs_match_contiguous():
     b_i, b_d = tb.query_knn(tb.build_bvh(pts.contiguous()), q.contiguous(), 8)
     assert torch.equal(a_i, b_i) and torch.equal(a_d, b_d)
     with tb.BVH(pts) as bvh:
-        c_i, _ = bvh.knn(q, 8, source_points=pts)
+        c_i, _, c_p = bvh.knn(q, 8, source_points=pts)
     assert torch.equal(c_i, a_i)
+    assert torch.equal(c_p, pts[a_i])
 
 
 @pytest.mark.parametrize("batched", [False, True])

@@ -20,6 +20,7 @@ from parity import (
     knn_pathological_clouds,
     unit_direction_points,
 )
+from torchbvh_amd._native import _C
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -30,17 +31,33 @@ def dev(a) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
 
 
+def implicit_knn(h, queries: torch.Tensor, k: int, sort: bool):
+    """The traversal over the reference's implicit tree (no accel)."""
+    nodes, sidx, q = h["node_aabbs"][None], h["sorted_indices"][None], queries[None]
+    if sort:
+        order = _C.morton_sort_queries_narrow(q, h["scene_min"][None], h["scene_max"][None])
+        out = _C.query_knn_batched_cached_bounds_ordered(
+            nodes, sidx, q, order, h["num_leaves"], h["num_real_nodes"], h["dim"], k)
+    else:
+        out = _C.query_knn_batched_cached_bounds(
+            nodes, sidx, q, h["num_leaves"], h["num_real_nodes"], h["dim"], k)
+    return out[0][0], out[1][0]
+
+
 def check_single(points: np.ndarray, queries: np.ndarray, k: int) -> None:
     h = tb.build_bvh(dev(points))
+    assert h._aux["accel"] is not None
     ei, ed = oracle.knn(points, queries, k)
+    qd = dev(queries)
     for sort in (True, False):
-        idx, dist = tb.query_knn(h, dev(queries), k, sort_queries=sort)
-        assert idx.dtype == torch.int64 and dist.dtype == torch.float32
-        assert tuple(idx.shape) == (queries.shape[0], k)
-        idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
-        np.testing.assert_allclose(dist, ed, rtol=DIST_RTOL, atol=0)
-        assert_same_int(idx, ei, f"indices sort={sort}")
-        assert_same_f32(dist, ed, f"distances sort={sort}")
+        for path, (idx, dist) in (("accel", tb.query_knn(h, qd, k, sort_queries=sort)),
+                                  ("implicit", implicit_knn(h, qd, k, sort))):
+            assert idx.dtype == torch.int64 and dist.dtype == torch.float32
+            assert tuple(idx.shape) == (queries.shape[0], k)
+            idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+            np.testing.assert_allclose(dist, ed, rtol=DIST_RTOL, atol=0)
+            assert_same_int(idx, ei, f"{path} indices sort={sort}")
+            assert_same_f32(dist, ed, f"{path} distances sort={sort}")
 
 
 @pytest.mark.parametrize("dim", [2, 3])
@@ -179,6 +196,11 @@ def test_ragged_knn_matches_oracle(dim, k):
     ei, ed = oracle.knn_ragged(p, po, q, qo, k)
     assert_same_int(idx.cpu().numpy(), ei, "indices")
     assert_same_f32(dist.cpu().numpy(), ed, "distances")
+    packed = h._aux["packed"]
+    ii, idd = _C.query_knn_ragged(packed["node_aabbs"], packed["sorted_indices"], dev(po),
+                                  packed["node_offsets"], dev(q), dev(qo), None, len(counts), dim, k)
+    assert_same_int(ii.cpu().numpy(), ei, "implicit ragged indices")
+    assert_same_f32(idd.cpu().numpy(), ed, "implicit ragged distances")
     rows = np.repeat(po[:-1], qcounts)
     assert_same_f32(pos.cpu().numpy(), p[ei + rows[:, None]], "positions")
 

@@ -59,11 +59,23 @@ def _declare(L) -> None:
     L.tbvh_knn_ragged.argtypes = (
         [_vp] * 7 + [_i64, _i64, _int, _int, _vp, _vp, _vp]
     )
+    L.tbvh_accel_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_accel_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_accel_build.argtypes = [_vp] * 5 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
+    L.tbvh_accel_build_ragged.argtypes = (
+        [_vp] * 6 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
+    )
+    L.tbvh_knn_accel.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    L.tbvh_knn_accel_ragged.argtypes = (
+        [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    )
     for name in (
         "tbvh_build_workspace_size", "tbvh_build", "tbvh_build_ragged_workspace_size",
         "tbvh_build_ragged", "tbvh_sort_queries_workspace_size", "tbvh_sort_queries",
         "tbvh_sort_queries_ragged_workspace_size", "tbvh_sort_queries_ragged",
-        "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged",
+        "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
+        "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
+        "tbvh_knn_accel", "tbvh_knn_accel_ragged",
     ):
         getattr(L, name).restype = _int
 
@@ -147,6 +159,10 @@ def virtual_leaves(n: int) -> int:
 
 def real_node_count(n: int) -> int:
     return int(load().tbvh_real_node_count(n))
+
+
+# Largest cloud the acceleration structure supports (28-bit bucket starts).
+MAX_ACCEL_CLOUD = 1 << 28
 
 
 # ---------------------------------------------------------------------------
@@ -242,6 +258,51 @@ class _NativeOps:
         }
 
     @staticmethod
+    def build_accel(points: torch.Tensor, data: dict) -> torch.Tensor | None:
+        """Acceleration structure for a batched build payload ([B, N, D]
+        points and the tensors `build_bvh_batched_cooperative` returned);
+        None when a cloud exceeds MAX_ACCEL_CLOUD points."""
+        op = "build_accel"
+        _require_device_f32(op, points, "points")
+        B, N, D = (int(s) for s in points.shape)
+        if N > MAX_ACCEL_CLOUD:
+            return None
+        L = load()
+        dev = points.device
+        with torch.cuda.device(dev):
+            nbytes = _size(L.tbvh_accel_size, B, B * N, D)
+            ws_bytes = _size(L.tbvh_accel_workspace_size, B, B * N, D)
+            accel = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_accel_build(
+                _ptr(points), _ptr(data["sorted_indices"]), _ptr(data["node_aabbs"]),
+                _ptr(data["scene_min"]), _ptr(data["scene_max"]), B, N, D, _ptr(accel),
+                _ptr(ws), ws.numel(), _stream(dev)))
+        return accel
+
+    @staticmethod
+    def build_accel_ragged(points: torch.Tensor, batch_offsets: torch.Tensor, packed: dict,
+                           counts: list[int]) -> torch.Tensor | None:
+        op = "build_accel_ragged"
+        _require_device_f32(op, points, "points")
+        if max(counts) > MAX_ACCEL_CLOUD:
+            return None
+        L = load()
+        T, D = (int(s) for s in points.shape)
+        B = len(counts)
+        dev = points.device
+        with torch.cuda.device(dev):
+            nbytes = _size(L.tbvh_accel_size, B, T, D)
+            ws_bytes = _size(L.tbvh_accel_workspace_size, B, T, D)
+            accel = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_accel_build_ragged(
+                _ptr(points), _ptr(batch_offsets), _ptr(packed["sorted_indices"]),
+                _ptr(packed["node_aabbs"]), _ptr(packed["scene_min"]), _ptr(packed["scene_max"]),
+                B, T, D, _ptr(accel), _ptr(ws), ws.numel(), _stream(dev)))
+        return accel
+
+    @staticmethod
     def morton_sort_queries_narrow(queries: torch.Tensor, scene_min: torch.Tensor,
                                    scene_max: torch.Tensor) -> torch.Tensor:
         op = "morton_sort_queries_narrow"
@@ -316,7 +377,7 @@ class _NativeOps:
 
     @staticmethod
     def _knn(op, node_aabbs, sorted_indices, query_points, query_order, num_leaves,
-             num_real_nodes, dim, k):
+             num_real_nodes, dim, k, accel=None):
         _require(dim in (2, 3), op, "D must be 2 or 3")
         _require_device_f32(op, query_points, "query_points")
         _require(query_points.dim() == 3 and query_points.size(2) == dim, op,
@@ -344,27 +405,39 @@ class _NativeOps:
             return indices, distances
         L = load()
         with torch.cuda.device(dev):
-            _check(L.tbvh_knn(
-                _ptr(node_aabbs), _ptr(sorted_indices), _ptr(query_points), _ptr(query_order),
-                B, M, int(num_leaves), int(num_real_nodes), int(dim), int(k),
-                _ptr(indices), _ptr(distances), _stream(dev)))
+            if accel is not None:
+                _require(accel.is_cuda and accel.device == dev, op, "accel must be on the queries' device")
+                _check(L.tbvh_knn_accel(
+                    _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
+                    int(dim), int(k), _ptr(indices), _ptr(distances), _stream(dev)))
+            else:
+                _check(L.tbvh_knn(
+                    _ptr(node_aabbs), _ptr(sorted_indices), _ptr(query_points), _ptr(query_order),
+                    B, M, int(num_leaves), int(num_real_nodes), int(dim), int(k),
+                    _ptr(indices), _ptr(distances), _stream(dev)))
         return indices, distances
 
     @classmethod
     def query_knn_batched_cached_bounds(cls, node_aabbs, sorted_indices, query_points,
-                                        num_leaves, num_real_nodes, dim, k):
+                                        num_leaves, num_real_nodes, dim, k, *, accel=None):
+        """Unordered traversal; with `accel` the accelerated traversal
+        (identical results)."""
         return cls._knn("query_knn_batched_cached_bounds", node_aabbs, sorted_indices,
-                        query_points, None, num_leaves, num_real_nodes, dim, k)
+                        query_points, None, num_leaves, num_real_nodes, dim, k, accel)
 
     @classmethod
     def query_knn_batched_cached_bounds_ordered(cls, node_aabbs, sorted_indices, query_points,
-                                                query_order, num_leaves, num_real_nodes, dim, k):
+                                                query_order, num_leaves, num_real_nodes, dim, k,
+                                                *, accel=None):
+        """Morton-ordered traversal; with `accel` the accelerated traversal
+        (identical results)."""
         return cls._knn("query_knn_batched_cached_bounds_ordered", node_aabbs, sorted_indices,
-                        query_points, query_order, num_leaves, num_real_nodes, dim, k)
+                        query_points, query_order, num_leaves, num_real_nodes, dim, k, accel)
 
     @staticmethod
     def query_knn_ragged(node_aabbs, sorted_indices, point_offsets, node_offsets, query_points,
-                         query_offsets, query_order, batch_size, dim, k):
+                         query_offsets, query_order, batch_size, dim, k, *, accel=None,
+                         total_points=None):
         op = "query_knn_ragged"
         _require_device_f32(op, query_points, "query_points")
         _require_device_f32(op, node_aabbs, "node_aabbs")
@@ -380,10 +453,16 @@ class _NativeOps:
             return indices, distances
         L = load()
         with torch.cuda.device(dev):
-            _check(L.tbvh_knn_ragged(
-                _ptr(node_aabbs), _ptr(sorted_indices), _ptr(point_offsets), _ptr(node_offsets),
-                _ptr(query_points), _ptr(query_offsets), _ptr(query_order), int(batch_size), T,
-                int(dim), int(k), _ptr(indices), _ptr(distances), _stream(dev)))
+            if accel is not None:
+                _check(L.tbvh_knn_accel_ragged(
+                    _ptr(accel), _ptr(point_offsets), int(total_points), _ptr(query_points),
+                    _ptr(query_offsets), _ptr(query_order), int(batch_size), T, int(dim), int(k),
+                    _ptr(indices), _ptr(distances), _stream(dev)))
+            else:
+                _check(L.tbvh_knn_ragged(
+                    _ptr(node_aabbs), _ptr(sorted_indices), _ptr(point_offsets), _ptr(node_offsets),
+                    _ptr(query_points), _ptr(query_offsets), _ptr(query_order), int(batch_size), T,
+                    int(dim), int(k), _ptr(indices), _ptr(distances), _stream(dev)))
         return indices, distances
 
 

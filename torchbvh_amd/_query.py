@@ -53,12 +53,14 @@ def _build_bvh_single(points: torch.Tensor) -> BVHHandle:
     _validate_cuda_float32("build_bvh", points, "points")
     points = _as_contiguous(points)
     _validate_narrow_build_extent("build_bvh", points)
-    data = _C.build_bvh_batched_cooperative(points.unsqueeze(0))
+    batched = points.unsqueeze(0)
+    data = _C.build_bvh_batched_cooperative(batched)
+    accel = _C.build_accel(batched, data)
     # A single handle carries the payload without the batch dimension.
     del data["batch_size"]
     for key in ("node_aabbs", "sorted_indices", "scene_min", "scene_max"):
         data[key] = data[key].squeeze(0)
-    return BVHHandle(data)
+    return BVHHandle(data, aux={"accel": accel})
 
 
 def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
@@ -69,7 +71,8 @@ def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
     _validate_cuda_float32("build_bvh", points, "points")
     points = _as_contiguous(points)
     _validate_narrow_build_extent("build_bvh", points)
-    return BatchedBVHHandle(_C.build_bvh_batched_cooperative(points))
+    data = _C.build_bvh_batched_cooperative(points)
+    return BatchedBVHHandle(data, aux={"accel": _C.build_accel(points, data)})
 
 
 def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> RaggedBVHHandle:
@@ -79,6 +82,7 @@ def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> Ragg
     _validate_narrow_build_extent("build_bvh", points)
     counts = [b - a for a, b in zip(offsets, offsets[1:])]
     packed = _C.build_bvh_ragged(points, batch_offsets, counts)
+    accel = _C.build_accel_ragged(points, batch_offsets, packed, counts)
     dim = int(points.size(1))
     node_offsets = packed["host_node_offsets"]
     handles = []
@@ -114,6 +118,7 @@ def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> Ragg
         aux={
             "packed": packed,
             "host_offsets": offsets,
+            "accel": accel,
         },
     )
 
@@ -165,18 +170,19 @@ def _query_knn_single(
     queries = _as_contiguous(query_points).unsqueeze(0)
     node_aabbs = data["node_aabbs"].unsqueeze(0)
     sorted_indices = data["sorted_indices"].unsqueeze(0)
+    accel = bvh._aux.get("accel")
     if sort_queries:
         order = _C.morton_sort_queries_narrow(
             queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0)
         )
         indices, distances = _C.query_knn_batched_cached_bounds_ordered(
             node_aabbs, sorted_indices, queries, order.contiguous(),
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
         )
     else:
         indices, distances = _C.query_knn_batched_cached_bounds(
             node_aabbs, sorted_indices, queries,
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
         )
     indices = indices.squeeze(0)
     distances = distances.squeeze(0)
@@ -239,16 +245,17 @@ def _query_knn_batched(
     if query_points.device != data["sorted_indices"].device:
         raise ValueError("query_knn: query_points must be on the same device as the BVH")
     queries = _as_contiguous(query_points)
+    accel = bvh._aux.get("accel")
     if sort_queries:
         order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"])
         indices, distances = _C.query_knn_batched_cached_bounds_ordered(
             data["node_aabbs"], data["sorted_indices"], queries, order.contiguous(),
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
         )
     else:
         indices, distances = _C.query_knn_batched_cached_bounds(
             data["node_aabbs"], data["sorted_indices"], queries,
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
         )
     if source_points is None:
         return indices, distances
@@ -309,7 +316,7 @@ def _query_knn_ragged(
     indices, distances = _C.query_knn_ragged(
         packed["node_aabbs"], packed["sorted_indices"], data["batch_offsets"],
         packed["node_offsets"], queries, query_offsets, order, data["batch_size"],
-        data["dim"], k,
+        data["dim"], k, accel=bvh._aux.get("accel"), total_points=p_offsets[-1],
     )
     if source_points is None:
         return indices, distances

@@ -1,0 +1,204 @@
+// k-NN acceleration structure derived from a finished implicit BVH.
+//
+// The implicit tree (the reference's payload, bit-exact) splits Morton-sorted
+// points into fixed power-of-two runs; a run usually straddles a Morton cell
+// boundary, so its box spans two cells and sibling boxes overlap heavily.  A
+// radix tree over the same sorted codes (Karras, "Maximizing Parallelism in
+// the Construction of BVHs, Octrees, and k-d Trees", HPG 2012) splits where
+// the codes' common prefix ends, i.e. on Morton cell boundaries, and visits
+// roughly ten times fewer nodes per query.  Because results are the k
+// smallest (distance, index) pairs, the traversal structure cannot change
+// them: this is a pure speed-up with identical output.
+//
+// Layout of one accel buffer (per cloud, clouds packed back to back):
+//   points  [n]    float4 (x, y, z|0, original index as int bits), Morton order
+//   records [n-1]  per radix-tree internal node i: left box (2D floats), right
+//                  box (2D floats), left ref, right ref, 2 pad words
+//                  (16 floats = 64 B in 3-D, 12 floats = 48 B in 2-D)
+// A child ref >= 0 is an internal node; a negative ref is a bucket of <= 8
+// consecutive points: 0x80000000 | (count - 1) << 28 | first.  Cloud c's
+// records start at row (first point of c) - c.
+//
+// Child boxes are exact: each is the min/max over its point range, assembled
+// from the implicit tree's node AABBs with an iterative segment-tree cover of
+// the range (min/max is exact and idempotent), so no pass here needs
+// cross-work-group synchronisation.
+#include <float.h>
+
+#include "tbvh_internal.hpp"
+
+namespace tbvh {
+namespace {
+
+// Number of differing-prefix bits between sorted positions i and j of one
+// cloud, on the 64-bit key (code << 32 | position); -1 outside the cloud.
+__device__ __forceinline__ int prefix_len(const uint32_t* codes, int n, int i, int j) {
+    if (j < 0 || j >= n) return -1;
+    const uint64_t a = (static_cast<uint64_t>(codes[i]) << 32) | static_cast<uint32_t>(i);
+    const uint64_t b = (static_cast<uint64_t>(codes[j]) << 32) | static_cast<uint32_t>(j);
+    return __clzll(static_cast<long long>(a ^ b));
+}
+
+template <int D>
+__device__ __forceinline__ void merge_row(float* box, const float* row) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        box[d] = fminf(box[d], row[d]);
+        box[D + d] = fmaxf(box[D + d], row[D + d]);
+    }
+}
+
+// Exact box of sorted positions [a, b] (inclusive) from the implicit tree:
+// heap node h has 1-based index h + 1, leaves are [2^L, 2^(L+1)), and the
+// classic bottom-up cover visits O(log n) nodes whose ranges tile [a, b].
+template <int D>
+__device__ void range_box(const float* nodes, int vl, int L, int a, int b, float* box) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        box[d] = FLT_MAX;
+        box[D + d] = -FLT_MAX;
+    }
+    int64_t lo = static_cast<int64_t>(a) + (int64_t(1) << L);
+    int64_t hi = static_cast<int64_t>(b) + 1 + (int64_t(1) << L);
+    while (lo < hi) {
+        if (lo & 1) {
+            const int row = tree::memory_index(vl, L, static_cast<int>(lo - 1));
+            merge_row<D>(box, nodes + static_cast<int64_t>(row) * 2 * D);
+            ++lo;
+        }
+        if (hi & 1) {
+            --hi;
+            const int row = tree::memory_index(vl, L, static_cast<int>(hi - 1));
+            merge_row<D>(box, nodes + static_cast<int64_t>(row) * 2 * D);
+        }
+        lo >>= 1;
+        hi >>= 1;
+    }
+}
+
+__device__ __forceinline__ int32_t child_ref(int first, int last, int internal) {
+    const int count = last - first + 1;
+    if (count <= kAccelBucket) {
+        return static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(count - 1) << 28) |
+                                    static_cast<uint32_t>(first));
+    }
+    return internal;
+}
+
+// Pass 1: Morton-ordered points (float4) and their codes, one thread per point.
+template <int D>
+__global__ __launch_bounds__(kBlock) void accel_points_kernel(
+    const float* __restrict__ points, const int64_t* __restrict__ sorted,
+    const Segment* __restrict__ segs, int S, int64_t total, const float* __restrict__ scene_min,
+    const float* __restrict__ scene_max, float4* __restrict__ leaf_points,
+    uint32_t* __restrict__ codes) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (r >= total) return;
+    const int s = find_segment([&](int i) { return segs[i].start; }, S, r);
+    const Segment g = segs[s];
+    const int64_t idx = min(max(sorted[r], int64_t(0)), int64_t(g.n - 1));
+    float p[D], lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        p[d] = points[(g.start + idx) * D + d];
+        lo[d] = scene_min[static_cast<int64_t>(s) * D + d];
+        hi[d] = scene_max[static_cast<int64_t>(s) * D + d];
+    }
+    codes[r] = morton::encode<D>(p, lo, hi);
+    float4 v;
+    v.x = p[0];
+    v.y = p[1];
+    v.z = D == 3 ? p[D - 1] : 0.0f;
+    v.w = __int_as_float(static_cast<int>(idx));
+    leaf_points[r] = v;
+}
+
+// Pass 2: radix-tree internal nodes (Karras 2012, section 4), one thread per
+// node; nodes inside a bucket are not referenced and write nothing.
+template <int D>
+__global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
+    const Segment* __restrict__ segs, int S, int64_t total_internal,
+    const uint32_t* __restrict__ all_codes, const float* __restrict__ node_aabbs,
+    float* __restrict__ records) {
+    constexpr int R = 4 * D + 4;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (r >= total_internal) return;
+    const int s = find_segment([&](int c) { return segs[c].start - c; }, S, r);
+    const Segment g = segs[s];
+    const int n = g.n;
+    const int i = static_cast<int>(r - (g.start - s));
+    if (i >= n - 1) return;
+    const uint32_t* c = all_codes + g.start;
+
+    const int dir = prefix_len(c, n, i, i + 1) - prefix_len(c, n, i, i - 1) > 0 ? 1 : -1;
+    const int dmin = prefix_len(c, n, i, i - dir);
+    int lmax = 2;
+    while (prefix_len(c, n, i, i + lmax * dir) > dmin) lmax <<= 1;
+    int l = 0;
+    for (int t = lmax >> 1; t >= 1; t >>= 1) {
+        if (prefix_len(c, n, i, i + (l + t) * dir) > dmin) l += t;
+    }
+    const int j = i + l * dir;
+    const int dnode = prefix_len(c, n, i, j);
+    int split = 0;
+    int t = l;
+    do {
+        t = (t + 1) >> 1;
+        if (prefix_len(c, n, i, i + (split + t) * dir) > dnode) split += t;
+    } while (t > 1);
+    const int gamma = i + split * dir + (dir < 0 ? dir : 0);
+    const int first = min(i, j);
+    const int last = max(i, j);
+    if (i != 0 && last - first + 1 <= kAccelBucket) return;
+
+    const float* nodes = node_aabbs + g.node_start * 2 * D;
+    float* rec = records + r * R;
+    float box[2 * D];
+    range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, box);
+#pragma unroll
+    for (int k = 0; k < 2 * D; ++k) rec[k] = box[k];
+    range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
+#pragma unroll
+    for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
+    rec[4 * D] = __int_as_float(child_ref(first, gamma, gamma));
+    rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
+    rec[4 * D + 2] = 0.0f;
+    rec[4 * D + 3] = 0.0f;
+}
+
+inline unsigned grid_for(int64_t items) {
+    return static_cast<unsigned>((items + kBlock - 1) / kBlock);
+}
+
+}  // namespace
+
+size_t accel_bytes(int64_t total, int64_t S, int D) {
+    return accel_points_bytes(total) + static_cast<size_t>(total - S) * (4 * D + 4) * sizeof(float);
+}
+
+hipError_t launch_accel_build(const float* points, const int64_t* sorted, const float* node_aabbs,
+                              const float* scene_min, const float* scene_max, int D,
+                              const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
+                              void* accel, hipStream_t stream) {
+    float4* leaf_points = static_cast<float4*>(accel);
+    float* records = reinterpret_cast<float*>(static_cast<char*>(accel) + accel_points_bytes(total));
+    const int Si = static_cast<int>(S);
+    if (D == 3) {
+        accel_points_kernel<3><<<grid_for(total), kBlock, 0, stream>>>(
+            points, sorted, segs, Si, total, scene_min, scene_max, leaf_points, codes);
+        if (total - S > 0) {
+            accel_nodes_kernel<3><<<grid_for(total - S), kBlock, 0, stream>>>(
+                segs, Si, total - S, codes, node_aabbs, records);
+        }
+    } else {
+        accel_points_kernel<2><<<grid_for(total), kBlock, 0, stream>>>(
+            points, sorted, segs, Si, total, scene_min, scene_max, leaf_points, codes);
+        if (total - S > 0) {
+            accel_nodes_kernel<2><<<grid_for(total - S), kBlock, 0, stream>>>(
+                segs, Si, total - S, codes, node_aabbs, records);
+        }
+    }
+    return hipGetLastError();
+}
+
+}  // namespace tbvh

@@ -394,4 +394,146 @@ int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
     return ok();
 }
 
+// ---------------------------------------------------------------------------
+// Acceleration structure
+// ---------------------------------------------------------------------------
+namespace {
+
+size_t accel_workspace_bytes(int64_t S, int64_t total) {
+    return align_up(static_cast<size_t>(S) * sizeof(Segment)) + align_up(static_cast<size_t>(total) * 4);
+}
+
+int check_accel_extent(const char* op, int64_t B, int64_t total, int D) {
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || total < B) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total >= B", op);
+    if (total > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    return TBVH_OK;
+}
+
+}  // namespace
+
+int tbvh_accel_size(int64_t B, int64_t total_points, int D, size_t* bytes) {
+    const char* op = "tbvh_accel_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_accel_extent(op, B, total_points, D)) return r;
+    *bytes = accel_bytes(total_points, B, D);
+    return ok();
+}
+
+int tbvh_accel_workspace_size(int64_t B, int64_t total_points, int D, size_t* bytes) {
+    const char* op = "tbvh_accel_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_accel_extent(op, B, total_points, D)) return r;
+    *bytes = accel_workspace_bytes(B, total_points);
+    return ok();
+}
+
+int tbvh_accel_build(const float* points, const int64_t* sorted_indices, const float* node_aabbs,
+                     const float* scene_min, const float* scene_max, int64_t B, int64_t N, int D,
+                     void* accel, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_accel_build";
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    if (N > kMaxAccelCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: clouds may hold at most 2^28 points", op);
+    if (!points || !sorted_indices || !node_aabbs || !scene_min || !scene_max || !accel) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const int64_t total = B * N;
+    if (int r = check_workspace(op, workspace, workspace_bytes, accel_workspace_bytes(B, total))) return r;
+    if (reinterpret_cast<uintptr_t>(accel) % kAlign != 0) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, 0);
+    uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
+    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
+    TBVH_TRY(op, launch_accel_build(points, sorted_indices, node_aabbs, scene_min, scene_max, D, segs,
+                                    B, total, codes, accel, stream));
+    return ok();
+}
+
+int tbvh_accel_build_ragged(const float* points, const int64_t* offsets, const int64_t* sorted_indices,
+                            const float* node_aabbs, const float* scene_min, const float* scene_max,
+                            int64_t B, int64_t total, int D, void* accel, void* workspace,
+                            size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_accel_build_ragged";
+    if (int r = check_accel_extent(op, B, total, D)) return r;
+    if (!points || !offsets || !sorted_indices || !node_aabbs || !scene_min || !scene_max || !accel) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    if (int r = check_workspace(op, workspace, workspace_bytes, accel_workspace_bytes(B, total))) return r;
+    if (reinterpret_cast<uintptr_t>(accel) % kAlign != 0) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, 0);
+    uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
+    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, nullptr, stream));
+    TBVH_TRY(op, launch_accel_build(points, sorted_indices, node_aabbs, scene_min, scene_max, D, segs,
+                                    B, total, codes, accel, stream));
+    return ok();
+}
+
+int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order, int64_t B,
+                   int64_t M, int64_t num_leaves, int D, int k, int64_t* out_indices,
+                   float* out_distances, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel";
+    if (int r = check_dim(op, D)) return r;
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (num_leaves < 1 || num_leaves > kMaxAccelCloud) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_leaves must be in [1, 2^28]", op);
+    }
+    if (num_leaves < k) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_leaves must be >= k", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (B > kMaxRows / num_leaves) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    if (M == 0) return ok();
+    if (!accel || !queries || !out_indices || !out_distances) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    KnnArgs a{};
+    a.queries = queries;
+    a.order = order;
+    a.B = B;
+    a.M = M;
+    a.total_q = B * M;
+    a.num_leaves = static_cast<int32_t>(num_leaves);
+    a.out_indices = out_indices;
+    a.out_distances = out_distances;
+    a.accel = accel;
+    a.total_points = B * num_leaves;
+    TBVH_TRY(op, launch_knn_accel(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets, int64_t total_points,
+                          const float* queries, const int64_t* query_offsets, const int64_t* order,
+                          int64_t B, int64_t total_q, int D, int k, int64_t* out_indices,
+                          float* out_distances, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_ragged";
+    if (int r = check_dim(op, D)) return r;
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
+    if (total_q > kMaxRows || total_points > kMaxRows || total_points < B) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: counts must fit in signed int32 (and total_points >= B)", op);
+    }
+    if (total_q == 0) return ok();
+    if (!accel || !point_offsets || !queries || !query_offsets || !out_indices || !out_distances) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    KnnArgs a{};
+    a.queries = queries;
+    a.order = order;
+    a.point_offsets = point_offsets;
+    a.query_offsets = query_offsets;
+    a.B = B;
+    a.total_q = total_q;
+    a.out_indices = out_indices;
+    a.out_distances = out_distances;
+    a.accel = accel;
+    a.total_points = total_points;
+    TBVH_TRY(op, launch_knn_accel(a, D, k, true, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
 }  // extern "C"

@@ -149,6 +149,155 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
     }
 }
 
+// Exact distance to a point stored as float4: the leaf-box formula above on
+// a degenerate box (lo = hi = p), i.e. delta = |q - p| per axis.
+template <int D>
+__device__ __forceinline__ float point_distance(const float* q, const float4 p) {
+    const float pc[3] = {p.x, p.y, p.z};
+    float s = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const float delta = fmaxf(pc[d] - q[d], fmaxf(0.0f, q[d] - pc[d]));
+        s = d == 0 ? delta * delta : __builtin_fmaf(delta, delta, s);
+    }
+    return s;
+}
+
+constexpr int kAccelStackDepth = 64;  // radix-tree depth <= 64 (64-bit keys)
+
+// Branch-and-bound over the acceleration structure (see accel.hip): same
+// pruning rule, near-first order and cached far-child distances as above;
+// a bucket ref brute-forces its <= 8 consecutive points.
+template <int D, int K, bool kOrdered, bool kRagged>
+__global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
+    constexpr int R = 4 * D + 4;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (gid >= a.total_q) return;
+
+    int64_t seg, qbase, qcount, pstart;
+    int n;
+    if constexpr (kRagged) {
+        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
+        qbase = a.query_offsets[seg];
+        qcount = a.query_offsets[seg + 1] - qbase;
+        pstart = a.point_offsets[seg];
+        n = static_cast<int>(a.point_offsets[seg + 1] - pstart);
+    } else {
+        seg = gid / a.M;
+        qbase = seg * a.M;
+        qcount = a.M;
+        n = a.num_leaves;
+        pstart = seg * static_cast<int64_t>(n);
+    }
+    const int64_t local = gid - qbase;
+    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
+    if (qi < 0 || qi >= qcount) return;
+    const int64_t row = qbase + qi;
+    const float4* pts = static_cast<const float4*>(a.accel) + pstart;
+    const float* recs = reinterpret_cast<const float*>(static_cast<const char*>(a.accel) +
+                                                       accel_points_bytes(a.total_points)) +
+                        (pstart - seg) * R;
+
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) q[d] = a.queries[row * D + d];
+
+    uint64_t best[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
+
+    uint64_t stack[kAccelStackDepth];
+    int sp = 0;
+    int32_t ref = n <= kAccelBucket
+                      ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
+                      : 0;
+    float nd = 0.0f;
+
+    while (true) {
+        const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
+        if (nd <= worst) {
+            if (ref < 0) {
+                const int first = ref & 0x0fffffff;
+                const int count = ((ref >> 28) & 7) + 1;
+                if (first + count <= n) {
+                    for (int j = 0; j < count; ++j) {
+                        const float4 p = pts[first + j];
+                        const float d = point_distance<D>(q, p);
+                        const uint64_t key = candidate_key(d, __float_as_uint(p.w));
+                        if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+                    }
+                }
+            } else if (ref < n - 1) {
+                const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
+                float rec[R];
+#pragma unroll
+                for (int v = 0; v < R / 4; ++v) {
+                    const float4 x = r4[v];
+                    rec[4 * v] = x.x;
+                    rec[4 * v + 1] = x.y;
+                    rec[4 * v + 2] = x.z;
+                    rec[4 * v + 3] = x.w;
+                }
+                const float ld = box_distance<D>(q, rec);
+                const float rd = box_distance<D>(q, rec + 2 * D);
+                const int32_t lref = __float_as_int(rec[4 * D]);
+                const int32_t rref = __float_as_int(rec[4 * D + 1]);
+                const bool left_near = ld <= rd;
+                const int32_t near_ref = left_near ? lref : rref;
+                const int32_t far_ref = left_near ? rref : lref;
+                const float near_d = left_near ? ld : rd;
+                const float far_d = left_near ? rd : ld;
+                if (far_d <= worst && sp < kAccelStackDepth) {
+                    stack[sp++] = (static_cast<uint64_t>(__float_as_uint(far_d)) << 32) |
+                                  static_cast<uint32_t>(far_ref);
+                }
+                if (near_d <= worst) {
+                    ref = near_ref;
+                    nd = near_d;
+                    continue;
+                }
+            }
+        }
+        if (sp == 0) break;
+        const uint64_t e = stack[--sp];
+        ref = static_cast<int32_t>(static_cast<uint32_t>(e));
+        nd = __uint_as_float(static_cast<uint32_t>(e >> 32));
+    }
+
+    int64_t* oi = a.out_indices + row * K;
+    float* od = a.out_distances + row * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        oi[i] = static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(best[i])));
+        od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
+    }
+}
+
+template <int D, int K>
+hipError_t launch_accel_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>((a.total_q + kBlock - 1) / kBlock);
+    const bool ordered = a.order != nullptr;
+    if (ragged) {
+        if (ordered) knn_accel_kernel<D, K, true, true><<<grid, kBlock, 0, stream>>>(a);
+        else knn_accel_kernel<D, K, false, true><<<grid, kBlock, 0, stream>>>(a);
+    } else {
+        if (ordered) knn_accel_kernel<D, K, true, false><<<grid, kBlock, 0, stream>>>(a);
+        else knn_accel_kernel<D, K, false, false><<<grid, kBlock, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_accel_d(const KnnArgs& a, int K, bool ragged, hipStream_t stream) {
+    switch (K) {
+        case 4: return launch_accel_dk<D, 4>(a, ragged, stream);
+        case 8: return launch_accel_dk<D, 8>(a, ragged, stream);
+        case 16: return launch_accel_dk<D, 16>(a, ragged, stream);
+        case 32: return launch_accel_dk<D, 32>(a, ragged, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int D, int K>
 hipError_t launch_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>((a.total_q + kBlock - 1) / kBlock);
@@ -179,6 +328,11 @@ hipError_t launch_d(const KnnArgs& a, int K, bool ragged, hipStream_t stream) {
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream) {
     if (a.total_q == 0) return hipSuccess;
     return D == 3 ? launch_d<3>(a, K, ragged, stream) : launch_d<2>(a, K, ragged, stream);
+}
+
+hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream) {
+    if (a.total_q == 0) return hipSuccess;
+    return D == 3 ? launch_accel_d<3>(a, K, ragged, stream) : launch_accel_d<2>(a, K, ragged, stream);
 }
 
 }  // namespace tbvh

@@ -112,6 +112,19 @@ hipError_t launch_traversal_arrays(const Segment* segs, int64_t S, int64_t total
                                    int32_t* left, int32_t* right, int32_t* leaf,
                                    hipStream_t stream);
 
+// k-NN acceleration structure (radix tree + Morton-ordered float4 points).
+constexpr int kAccelBucket = 8;                       // max points per leaf bucket
+constexpr int64_t kMaxAccelCloud = int64_t(1) << 28;  // bucket refs hold 28-bit starts
+__host__ __device__ inline size_t accel_points_bytes(int64_t total) {
+    return (static_cast<size_t>(total) * 16 + 255) / 256 * 256;
+}
+size_t accel_bytes(int64_t total, int64_t S, int D);
+// `codes` is scratch for `total` u32 Morton codes.
+hipError_t launch_accel_build(const float* points, const int64_t* sorted, const float* node_aabbs,
+                              const float* scene_min, const float* scene_max, int D,
+                              const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
+                              void* accel, hipStream_t stream);
+
 // k-NN traversal.
 struct KnnArgs {
     const float* node_aabbs;
@@ -128,8 +141,11 @@ struct KnnArgs {
     int32_t num_real_nodes;        // batched only
     int64_t* out_indices;
     float* out_distances;
+    const void* accel;             // accelerated traversal only
+    int64_t total_points;          // accelerated traversal only
 };
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
+hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 
 // Tile-count bound for S segments holding `total` rows in kSortTile tiles.
 inline int64_t tiles_bound(int64_t total, int64_t S) {
