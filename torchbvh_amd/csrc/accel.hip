@@ -15,7 +15,7 @@
 //   records [n-1]  per radix-tree internal node i: left box (2D floats), right
 //                  box (2D floats), left ref, right ref, 2 pad words
 //                  (16 floats = 64 B in 3-D, 12 floats = 48 B in 2-D)
-// A child ref >= 0 is an internal node; a negative ref is a bucket of <= 8
+// A child ref >= 0 is an internal node; a negative ref is a bucket of <= 4
 // consecutive points: 0x80000000 | (count - 1) << 28 | first.  Cloud c's
 // records start at row (first point of c) - c.
 //

@@ -149,29 +149,43 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
     }
 }
 
-// Exact distance to a point stored as float4: the leaf-box formula above on
-// a degenerate box (lo = hi = p), i.e. delta = |q - p| per axis.
+// Exact distance to a point stored as float4.  On a leaf's degenerate box
+// the box formula above gives delta = |q - p| per axis; e = p - q has the
+// same square (IEEE subtraction is sign-symmetric), so the fused chain over
+// e is bit-identical and costs half the instructions.
 template <int D>
 __device__ __forceinline__ float point_distance(const float* q, const float4 p) {
     const float pc[3] = {p.x, p.y, p.z};
     float s = 0.0f;
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        const float delta = fmaxf(pc[d] - q[d], fmaxf(0.0f, q[d] - pc[d]));
-        s = d == 0 ? delta * delta : __builtin_fmaf(delta, delta, s);
+        const float e = pc[d] - q[d];
+        s = d == 0 ? e * e : __builtin_fmaf(e, e, s);
     }
     return s;
 }
 
-constexpr int kAccelStackDepth = 64;  // radix-tree depth <= 64 (64-bit keys)
+constexpr int kAccelStackDepth = 64;   // radix-tree depth <= 64 (64-bit keys)
+constexpr int kLdsStack = 12;          // top stack entries kept in LDS per lane
+constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 
 // Branch-and-bound over the acceleration structure (see accel.hip): same
 // pruning rule, near-first order and cached far-child distances as above;
-// a bucket ref brute-forces its <= 8 consecutive points.
+// a bucket ref brute-forces its <= kAccelBucket consecutive points, loaded
+// together.  The deferred-node stack keeps its top kLdsStack entries in LDS
+// (one column per lane) and spills deeper entries to scratch.
+//
+// Tile order: consecutive work-groups land on different XCDs, each with its
+// own L2; logical tile t = (block % 8) * (grid / 8) + block / 8 gives every
+// XCD a contiguous run of Morton-ordered queries, so one XCD's L2 serves a
+// compact region of the tree.
 template <int D, int K, bool kOrdered, bool kRagged>
 __global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
     constexpr int R = 4 * D + 4;
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    __shared__ uint64_t lds_stack[kLdsStack * kBlock];
+    const int64_t per_xcd = gridDim.x / kXcds;
+    const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    const int64_t gid = tile * kBlock + threadIdx.x;
     if (gid >= a.total_q) return;
 
     int64_t seg, qbase, qcount, pstart;
@@ -206,7 +220,8 @@ __global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
 #pragma unroll
     for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
 
-    uint64_t stack[kAccelStackDepth];
+    uint64_t spill[kAccelStackDepth - kLdsStack];
+    uint64_t* lds_col = lds_stack + threadIdx.x;
     int sp = 0;
     int32_t ref = n <= kAccelBucket
                       ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
@@ -220,11 +235,18 @@ __global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
                 const int first = ref & 0x0fffffff;
                 const int count = ((ref >> 28) & 7) + 1;
                 if (first + count <= n) {
-                    for (int j = 0; j < count; ++j) {
-                        const float4 p = pts[first + j];
-                        const float d = point_distance<D>(q, p);
-                        const uint64_t key = candidate_key(d, __float_as_uint(p.w));
-                        if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+                    float4 p[kAccelBucket];
+#pragma unroll
+                    for (int j = 0; j < kAccelBucket; ++j) {
+                        p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    }
+#pragma unroll
+                    for (int j = 0; j < kAccelBucket; ++j) {
+                        if (j < count) {
+                            const float d = point_distance<D>(q, p[j]);
+                            const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
+                            if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+                        }
                     }
                 }
             } else if (ref < n - 1) {
@@ -248,8 +270,11 @@ __global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
                 const float near_d = left_near ? ld : rd;
                 const float far_d = left_near ? rd : ld;
                 if (far_d <= worst && sp < kAccelStackDepth) {
-                    stack[sp++] = (static_cast<uint64_t>(__float_as_uint(far_d)) << 32) |
-                                  static_cast<uint32_t>(far_ref);
+                    const uint64_t e = (static_cast<uint64_t>(__float_as_uint(far_d)) << 32) |
+                                       static_cast<uint32_t>(far_ref);
+                    if (sp < kLdsStack) lds_col[sp * kBlock] = e;
+                    else spill[sp - kLdsStack] = e;
+                    ++sp;
                 }
                 if (near_d <= worst) {
                     ref = near_ref;
@@ -259,7 +284,8 @@ __global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
             }
         }
         if (sp == 0) break;
-        const uint64_t e = stack[--sp];
+        --sp;
+        const uint64_t e = sp < kLdsStack ? lds_col[sp * kBlock] : spill[sp - kLdsStack];
         ref = static_cast<int32_t>(static_cast<uint32_t>(e));
         nd = __uint_as_float(static_cast<uint32_t>(e >> 32));
     }
@@ -275,7 +301,9 @@ __global__ __launch_bounds__(kBlock) void knn_accel_kernel(KnnArgs a) {
 
 template <int D, int K>
 hipError_t launch_accel_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
-    const unsigned grid = static_cast<unsigned>((a.total_q + kBlock - 1) / kBlock);
+    // Whole XCD rounds (see knn_accel_kernel); surplus tiles exit at once.
+    const int64_t tiles = (a.total_q + kBlock - 1) / kBlock;
+    const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
     const bool ordered = a.order != nullptr;
     if (ragged) {
         if (ordered) knn_accel_kernel<D, K, true, true><<<grid, kBlock, 0, stream>>>(a);

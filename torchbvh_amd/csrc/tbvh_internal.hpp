@@ -113,7 +113,7 @@ hipError_t launch_traversal_arrays(const Segment* segs, int64_t S, int64_t total
                                    hipStream_t stream);
 
 // k-NN acceleration structure (radix tree + Morton-ordered float4 points).
-constexpr int kAccelBucket = 8;                       // max points per leaf bucket
+constexpr int kAccelBucket = 4;                       // max points per leaf bucket
 constexpr int64_t kMaxAccelCloud = int64_t(1) << 28;  // bucket refs hold 28-bit starts
 __host__ __device__ inline size_t accel_points_bytes(int64_t total) {
     return (static_cast<size_t>(total) * 16 + 255) / 256 * 256;
