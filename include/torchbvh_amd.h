@@ -95,6 +95,30 @@ int tbvh_build_ragged(const float* points, const int64_t* offsets,
                       int64_t total_nodes,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- build + acceleration structure in one call ------------------------------
+ * No counterpart in the reference (it has no acceleration structure).  Same
+ * outputs as tbvh_build / tbvh_build_ragged and, in the same launch sequence,
+ * the k-NN acceleration structure that tbvh_accel_build(_ragged) would build
+ * from them (sized by tbvh_accel_size, 256-byte aligned); it reuses the sort's
+ * keys and the tree passes' point reads instead of recomputing them.  Every
+ * cloud must hold at most 2^28 points.  Same workspace size as the plain
+ * builds. */
+int tbvh_build_with_accel(const float* points, int64_t B, int64_t N, int D,
+                          float* node_aabbs, int64_t* sorted_indices,
+                          float* scene_min, float* scene_max,
+                          int32_t* left_child_mem, int32_t* right_child_mem,
+                          int32_t* mem_to_leaf, void* accel,
+                          void* workspace, size_t workspace_bytes, void* stream);
+int tbvh_build_ragged_with_accel(const float* points, const int64_t* offsets,
+                                 int64_t B, int64_t total, int D,
+                                 float* node_aabbs, int64_t* sorted_indices,
+                                 float* scene_min, float* scene_max,
+                                 int32_t* left_child_mem, int32_t* right_child_mem,
+                                 int32_t* mem_to_leaf, int64_t* node_offsets,
+                                 int64_t total_nodes, void* accel,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* ---- query ordering -----------------------------------------------------------
  * Replaces `morton_sort_queries_narrow` (torchbvh/csrc/morton_sort.cu:212-287):
  * Morton codes of the queries against the BVH's scene bounds, stable sort,

@@ -134,3 +134,31 @@ def test_accel_argument_errors():
     assert L.tbvh_knn_accel(FAKE, FAKE, None, 1, 10, 3, 3, 4, FAKE, FAKE, None) == 1
     assert "num_leaves must be >= k" in _err(L)
     assert L.tbvh_knn_accel(None, None, None, 1, 0, 100, 3, 4, None, None, None) == 0
+
+
+def test_build_with_accel_argument_errors():
+    L = _native.load()
+    size = ctypes.c_size_t()
+    assert L.tbvh_build_workspace_size(2, 1000, 3, ctypes.byref(size)) == 0
+    need = size.value
+    outs = [FAKE] * 7
+    # Null accel.
+    assert L.tbvh_build_with_accel(FAKE, 2, 1000, 3, *outs, None, FAKE, need, None) == 1
+    assert "accel is null" in _err(L)
+    # Misaligned accel.
+    assert L.tbvh_build_with_accel(FAKE, 2, 1000, 3, *outs, ctypes.c_void_p(0x100010), FAKE,
+                                   need, None) == 1
+    assert "aligned" in _err(L)
+    # Clouds above 2^28 points.
+    assert L.tbvh_build_with_accel(FAKE, 1, (1 << 28) + 1, 3, *outs, FAKE, FAKE, 1 << 40,
+                                   None) == 1
+    assert "2^28" in _err(L)
+    # Workspace too small.
+    assert L.tbvh_build_with_accel(FAKE, 2, 1000, 3, *outs, FAKE, FAKE, need - 1, None) == 2
+    # Ragged: null accel, then total_nodes too small.
+    assert L.tbvh_build_ragged_with_accel(FAKE, FAKE, 2, 100, 3, *([FAKE] * 8), 1000, None,
+                                          FAKE, 1 << 20, None) == 1
+    assert "accel is null" in _err(L)
+    assert L.tbvh_build_ragged_with_accel(FAKE, FAKE, 2, 100, 3, *([FAKE] * 8), 10, FAKE,
+                                          FAKE, 1 << 20, None) == 1
+    assert "total_nodes" in _err(L)

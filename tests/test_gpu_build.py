@@ -140,3 +140,67 @@ def test_build_is_deterministic_across_calls():
     b = tb.build_bvh(p)
     assert torch.equal(a["node_aabbs"], b["node_aabbs"])
     assert torch.equal(a["sorted_indices"], b["sorted_indices"])
+
+
+def assert_same_accel(a: torch.Tensor, b: torch.Tensor, counts: list[int], dim: int) -> None:
+    """Accel buffers agree on every byte traversal can read: the `total`
+    16-byte points, and the node records reachable from each cloud's root
+    (records of ranges that fit one bucket are never written, nor is the
+    padding after the points)."""
+    assert a.shape == b.shape
+    total = sum(counts)
+    pts = total * 16
+    assert torch.equal(a[:pts], b[:pts]), "accel points differ"
+    off = (pts + 255) // 256 * 256
+    width = 4 * dim + 4
+    ra = a[off:].cpu().numpy().view(np.int32).reshape(-1, width)
+    rb = b[off:].cpu().numpy().view(np.int32).reshape(-1, width)
+    start = 0
+    for c, n in enumerate(counts):
+        base = start - c  # cloud c's records start here
+        start += n
+        if n < 2:
+            continue
+        frontier = np.array([0])
+        while frontier.size:
+            rows = base + frontier
+            assert np.array_equal(ra[rows], rb[rows]), f"cloud {c}: records differ"
+            refs = rb[rows, 4 * dim:4 * dim + 2].ravel()
+            frontier = refs[refs >= 0]
+
+
+def _standalone_accel(points: torch.Tensor, h) -> torch.Tensor:
+    data = {k: h[k][None] for k in ("sorted_indices", "node_aabbs", "scene_min", "scene_max")}
+    return _C.build_accel(points[None], data)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("n", [1, 5, 4097, 200_001])
+def test_fused_accel_matches_standalone_build(n, dim):
+    """The build that also emits the accel (one launch sequence) and the
+    accel built afterwards from the finished BVH hold the same bytes."""
+    rng = np.random.default_rng(n + 7 * dim)
+    p = dev(rng.random((n, dim), dtype=np.float32))
+    h = tb.build_bvh(p)
+    fused = h._aux["accel"]
+    assert fused is not None
+    assert_same_accel(fused, _standalone_accel(p, h), [n], dim)
+
+
+def test_fused_accel_matches_standalone_ragged():
+    rng = np.random.default_rng(41)
+    counts = [1, 3, 4096, 9000, 70_001, 2]
+    pts = np.concatenate([rng.random((c, 3), dtype=np.float32) * (b + 1) for b, c in enumerate(counts)])
+    offsets = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    p, o = dev(pts), dev(offsets)
+    h = tb.build_bvh(p, batch_offsets=o)
+    fused = h._aux["accel"]
+    packed = {k: h._aux["packed"][k] for k in ("sorted_indices", "node_aabbs", "scene_min", "scene_max")}
+    assert_same_accel(fused, _C.build_accel_ragged(p, o, packed, counts), counts, 3)
+
+
+def test_build_million_points_many_tiles():
+    """245 sort tiles per pass: long look-back chains and the last-tile bounds
+    reduction, bit-exact against the oracle."""
+    rng = np.random.default_rng(2024)
+    check_single_build(rng.random((1_000_000, 3), dtype=np.float32))

@@ -48,6 +48,12 @@ def _declare(L) -> None:
     L.tbvh_build_ragged.argtypes = (
         [_vp, _vp, _i64, _i64, _int] + [_vp] * 8 + [_i64, _vp, ctypes.c_size_t, _vp]
     )
+    L.tbvh_build_with_accel.argtypes = (
+        [_vp, _i64, _i64, _int] + [_vp] * 8 + [_vp, ctypes.c_size_t, _vp]
+    )
+    L.tbvh_build_ragged_with_accel.argtypes = (
+        [_vp, _vp, _i64, _i64, _int] + [_vp] * 8 + [_i64, _vp, _vp, ctypes.c_size_t, _vp]
+    )
     L.tbvh_sort_queries_workspace_size.argtypes = [_i64, _i64, _int, _szp]
     L.tbvh_sort_queries.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_sort_queries_ragged_workspace_size.argtypes = [_i64, _i64, _int, _szp]
@@ -71,7 +77,8 @@ def _declare(L) -> None:
     )
     for name in (
         "tbvh_build_workspace_size", "tbvh_build", "tbvh_build_ragged_workspace_size",
-        "tbvh_build_ragged", "tbvh_sort_queries_workspace_size", "tbvh_sort_queries",
+        "tbvh_build_ragged", "tbvh_build_with_accel", "tbvh_build_ragged_with_accel",
+        "tbvh_sort_queries_workspace_size", "tbvh_sort_queries",
         "tbvh_sort_queries_ragged_workspace_size", "tbvh_sort_queries_ragged",
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
@@ -172,7 +179,10 @@ class _NativeOps:
     """Torch-level wrappers over the C ABI, named as the reference's `_C`."""
 
     @staticmethod
-    def build_bvh_batched_cooperative(points: torch.Tensor) -> dict:
+    def build_bvh_batched_cooperative(points: torch.Tensor, *, with_accel: bool = False) -> dict:
+        """Batched build.  With `with_accel` (and N <= MAX_ACCEL_CLOUD) the
+        same launch sequence also builds the k-NN acceleration structure,
+        returned under "accel" (None otherwise)."""
         op = "build_bvh_batched_cooperative"
         _require_device_f32(op, points, "points")
         _require(points.dim() == 3 and points.size(0) >= 1 and points.size(1) >= 1
@@ -191,11 +201,20 @@ class _NativeOps:
             right = torch.empty(nr, dtype=torch.int32, device=dev)
             leaf = torch.empty(nr, dtype=torch.int32, device=dev)
             ws = _workspace(ws_bytes, dev)
-            _check(L.tbvh_build(
-                _ptr(points), B, N, D, _ptr(node_aabbs), _ptr(sorted_indices),
-                _ptr(scene_min), _ptr(scene_max), _ptr(left), _ptr(right), _ptr(leaf),
-                _ptr(ws), ws.numel(), _stream(dev)))
-        return {
+            accel = None
+            if with_accel and N <= MAX_ACCEL_CLOUD:
+                accel = torch.empty(_size(L.tbvh_accel_size, B, B * N, D), dtype=torch.uint8,
+                                    device=dev)
+                _check(L.tbvh_build_with_accel(
+                    _ptr(points), B, N, D, _ptr(node_aabbs), _ptr(sorted_indices),
+                    _ptr(scene_min), _ptr(scene_max), _ptr(left), _ptr(right), _ptr(leaf),
+                    _ptr(accel), _ptr(ws), ws.numel(), _stream(dev)))
+            else:
+                _check(L.tbvh_build(
+                    _ptr(points), B, N, D, _ptr(node_aabbs), _ptr(sorted_indices),
+                    _ptr(scene_min), _ptr(scene_max), _ptr(left), _ptr(right), _ptr(leaf),
+                    _ptr(ws), ws.numel(), _stream(dev)))
+        out = {
             "node_aabbs": node_aabbs,
             "sorted_indices": sorted_indices,
             "scene_min": scene_min,
@@ -210,13 +229,17 @@ class _NativeOps:
             "right_child_mem": right,
             "mem_to_leaf": leaf,
         }
+        if with_accel:
+            out["accel"] = accel
+        return out
 
     @staticmethod
     def build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor,
-                         counts: list[int]) -> dict:
+                         counts: list[int], *, with_accel: bool = False) -> dict:
         """Segmented build of packed clouds; `counts` are the host-side cloud
         sizes (already validated).  Returns packed tensors and per-cloud node
-        offsets."""
+        offsets; with `with_accel` (and every cloud <= MAX_ACCEL_CLOUD) also
+        the acceleration structure under "accel" (None otherwise)."""
         op = "build_bvh_ragged"
         _require_device_f32(op, points, "points")
         _require_device_i64(op, batch_offsets, "batch_offsets")
@@ -237,11 +260,21 @@ class _NativeOps:
             leaf = torch.empty(total_nodes, dtype=torch.int32, device=dev)
             node_offsets = torch.empty(B + 1, dtype=torch.int64, device=dev)
             ws = _workspace(ws_bytes, dev)
-            _check(L.tbvh_build_ragged(
-                _ptr(points), _ptr(batch_offsets), B, T, D, _ptr(node_aabbs),
-                _ptr(sorted_indices), _ptr(scene_min), _ptr(scene_max), _ptr(left),
-                _ptr(right), _ptr(leaf), _ptr(node_offsets), total_nodes,
-                _ptr(ws), ws.numel(), _stream(dev)))
+            accel = None
+            if with_accel and max(counts) <= MAX_ACCEL_CLOUD:
+                accel = torch.empty(_size(L.tbvh_accel_size, B, T, D), dtype=torch.uint8,
+                                    device=dev)
+                _check(L.tbvh_build_ragged_with_accel(
+                    _ptr(points), _ptr(batch_offsets), B, T, D, _ptr(node_aabbs),
+                    _ptr(sorted_indices), _ptr(scene_min), _ptr(scene_max), _ptr(left),
+                    _ptr(right), _ptr(leaf), _ptr(node_offsets), total_nodes, _ptr(accel),
+                    _ptr(ws), ws.numel(), _stream(dev)))
+            else:
+                _check(L.tbvh_build_ragged(
+                    _ptr(points), _ptr(batch_offsets), B, T, D, _ptr(node_aabbs),
+                    _ptr(sorted_indices), _ptr(scene_min), _ptr(scene_max), _ptr(left),
+                    _ptr(right), _ptr(leaf), _ptr(node_offsets), total_nodes,
+                    _ptr(ws), ws.numel(), _stream(dev)))
         host_node_offsets = [0]
         for c in node_counts:
             host_node_offsets.append(host_node_offsets[-1] + c)
@@ -255,6 +288,7 @@ class _NativeOps:
             "mem_to_leaf": leaf,
             "node_offsets": node_offsets,
             "host_node_offsets": host_node_offsets,
+            "accel": accel,
         }
 
     @staticmethod

@@ -54,8 +54,8 @@ def _build_bvh_single(points: torch.Tensor) -> BVHHandle:
     points = _as_contiguous(points)
     _validate_narrow_build_extent("build_bvh", points)
     batched = points.unsqueeze(0)
-    data = _C.build_bvh_batched_cooperative(batched)
-    accel = _C.build_accel(batched, data)
+    data = _C.build_bvh_batched_cooperative(batched, with_accel=True)
+    accel = data.pop("accel")
     # A single handle carries the payload without the batch dimension.
     del data["batch_size"]
     for key in ("node_aabbs", "sorted_indices", "scene_min", "scene_max"):
@@ -71,8 +71,9 @@ def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
     _validate_cuda_float32("build_bvh", points, "points")
     points = _as_contiguous(points)
     _validate_narrow_build_extent("build_bvh", points)
-    data = _C.build_bvh_batched_cooperative(points)
-    return BatchedBVHHandle(data, aux={"accel": _C.build_accel(points, data)})
+    data = _C.build_bvh_batched_cooperative(points, with_accel=True)
+    accel = data.pop("accel")
+    return BatchedBVHHandle(data, aux={"accel": accel})
 
 
 def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> RaggedBVHHandle:
@@ -81,8 +82,8 @@ def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> Ragg
     offsets = _validate_ragged_points("build_bvh", points, batch_offsets)
     _validate_narrow_build_extent("build_bvh", points)
     counts = [b - a for a, b in zip(offsets, offsets[1:])]
-    packed = _C.build_bvh_ragged(points, batch_offsets, counts)
-    accel = _C.build_accel_ragged(points, batch_offsets, packed, counts)
+    packed = _C.build_bvh_ragged(points, batch_offsets, counts, with_accel=True)
+    accel = packed["accel"]
     dim = int(points.size(1))
     node_offsets = packed["host_node_offsets"]
     handles = []

@@ -176,27 +176,33 @@ size_t accel_bytes(int64_t total, int64_t S, int D) {
     return accel_points_bytes(total) + static_cast<size_t>(total - S) * (4 * D + 4) * sizeof(float);
 }
 
-hipError_t launch_accel_build(const float* points, const int64_t* sorted, const float* node_aabbs,
-                              const float* scene_min, const float* scene_max, int D,
-                              const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
-                              void* accel, hipStream_t stream) {
+hipError_t launch_accel_points(const float* points, const int64_t* sorted, const float* scene_min,
+                               const float* scene_max, int D, const Segment* segs, int64_t S,
+                               int64_t total, uint32_t* codes, void* accel, hipStream_t stream) {
     float4* leaf_points = static_cast<float4*>(accel);
-    float* records = reinterpret_cast<float*>(static_cast<char*>(accel) + accel_points_bytes(total));
     const int Si = static_cast<int>(S);
     if (D == 3) {
         accel_points_kernel<3><<<grid_for(total), kBlock, 0, stream>>>(
             points, sorted, segs, Si, total, scene_min, scene_max, leaf_points, codes);
-        if (total - S > 0) {
-            accel_nodes_kernel<3><<<grid_for(total - S), kBlock, 0, stream>>>(
-                segs, Si, total - S, codes, node_aabbs, records);
-        }
     } else {
         accel_points_kernel<2><<<grid_for(total), kBlock, 0, stream>>>(
             points, sorted, segs, Si, total, scene_min, scene_max, leaf_points, codes);
-        if (total - S > 0) {
-            accel_nodes_kernel<2><<<grid_for(total - S), kBlock, 0, stream>>>(
-                segs, Si, total - S, codes, node_aabbs, records);
-        }
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* segs, int64_t S,
+                              int64_t total, const uint32_t* sorted_codes, void* accel,
+                              hipStream_t stream) {
+    if (total - S <= 0) return hipSuccess;
+    float* records = reinterpret_cast<float*>(static_cast<char*>(accel) + accel_points_bytes(total));
+    const int Si = static_cast<int>(S);
+    if (D == 3) {
+        accel_nodes_kernel<3><<<grid_for(total - S), kBlock, 0, stream>>>(
+            segs, Si, total - S, sorted_codes, node_aabbs, records);
+    } else {
+        accel_nodes_kernel<2><<<grid_for(total - S), kBlock, 0, stream>>>(
+            segs, Si, total - S, sorted_codes, node_aabbs, records);
     }
     return hipGetLastError();
 }

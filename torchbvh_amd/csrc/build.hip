@@ -1,6 +1,6 @@
 // BVH build kernels: segment planning, per-cloud bounds, Morton codes (with
-// the first sort pass's tile histograms), implicit-tree node AABBs and the
-// traversal arrays.
+// every sort pass's digit histograms), implicit-tree node AABBs, fused with
+// the traversal arrays and the accel's Morton-ordered points.
 //
 // Reference behaviour followed (torchbvh/csrc/bvh_build.cu):
 //   bounds      :453-494  fminf/fmaxf from +-1e30 seeds, per cloud
@@ -75,22 +75,37 @@ __device__ inline void fill_segment(Segment& g, int64_t start, int n, bool with_
 }
 
 __global__ __launch_bounds__(kBlock) void plan_uniform_kernel(Segment* segs, int64_t S, int n,
-                                                              bool with_tree) {
-    const int64_t s = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (s >= S) return;
-    Segment g;
-    fill_segment(g, s * n, n, with_tree);
-    g.tile_first = static_cast<int32_t>(s * g.tiles);
-    g.node_start = s * g.nr;
-    for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(s * g.groups[p]);
-    segs[s] = g;
+                                                              bool with_tree, uint32_t* clear,
+                                                              int64_t clear_words) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    const int64_t span = S > clear_words ? S : clear_words;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < span; i += stride) {
+        if (i < clear_words) clear[i] = 0u;
+        if (i < S) {
+            Segment g;
+            fill_segment(g, i * n, n, with_tree);
+            g.tile_first = static_cast<int32_t>(i * g.tiles);
+            g.node_start = i * g.nr;
+            for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(i * g.groups[p]);
+            segs[i] = g;
+        }
+    }
 }
 
-// One work-group scans all segments in chunks of kBlock.
+// Work-group 0 scans all segments in chunks of kBlock; the others clear.
 __global__ __launch_bounds__(kBlock) void plan_offsets_kernel(Segment* segs, const int64_t* offsets,
                                                               int64_t S, bool with_tree,
-                                                              int64_t* node_offsets) {
+                                                              int64_t* node_offsets, uint32_t* clear,
+                                                              int64_t clear_words) {
     __shared__ int64_t scratch[kBlock / kWave];
+    if (blockIdx.x > 0) {
+        const int64_t stride = static_cast<int64_t>(gridDim.x - 1) * kBlock;
+        for (int64_t i = static_cast<int64_t>(blockIdx.x - 1) * kBlock + threadIdx.x; i < clear_words;
+             i += stride) {
+            clear[i] = 0u;
+        }
+        return;
+    }
     int64_t carry_tiles = 0, carry_nodes = 0;
     int64_t carry_groups[kMaxTreePasses] = {0, 0, 0, 0};
     for (int64_t base = 0; base < S; base += kBlock) {
@@ -136,12 +151,41 @@ __device__ __forceinline__ int block_find_segment(F firsts, int S, int64_t x, in
 // ---------------------------------------------------------------------------
 // Bounds
 // ---------------------------------------------------------------------------
+// Block-wide min (c < D) / max (c >= D) of per-thread boxes; the result for
+// component c lands in out[c] for threads c < 2D.
 template <int D>
-__global__ __launch_bounds__(kBlock) void bounds_partial_kernel(const float* __restrict__ points,
-                                                                const Segment* __restrict__ segs,
-                                                                int S, float* __restrict__ partials) {
+__device__ __forceinline__ void block_box(float (&lo)[D], float (&hi)[D], float (*s_red)[2 * D],
+                                          float* out) {
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        lo[d] = wave_min(lo[d]);
+        hi[d] = wave_max(hi[d]);
+    }
+    if (lane_id() == 0) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) { s_red[wave][d] = lo[d]; s_red[wave][D + d] = hi[d]; }
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * D) {
+        const int c = threadIdx.x;
+        float v = s_red[0][c];
+        for (int w = 1; w < kBlock / kWave; ++w) v = c < D ? fminf(v, s_red[w][c]) : fmaxf(v, s_red[w][c]);
+        out[c] = v;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict__ points,
+                                                        const Segment* __restrict__ segs, int S,
+                                                        float* __restrict__ partials,
+                                                        uint32_t* __restrict__ seg_done,
+                                                        float* __restrict__ scene_min,
+                                                        float* __restrict__ scene_max) {
     __shared__ int s_seg;
+    __shared__ int s_last;
     __shared__ float s_red[kBlock / kWave][2 * D];
+    __shared__ float s_out[2 * D];
     const int64_t t = blockIdx.x;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
                                      S, t, &s_seg);
@@ -163,34 +207,26 @@ __global__ __launch_bounds__(kBlock) void bounds_partial_kernel(const float* __r
             hi[d] = fmaxf(hi[d], v);
         }
     }
-    const int wave = threadIdx.x / kWave;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        lo[d] = wave_min(lo[d]);
-        hi[d] = wave_max(hi[d]);
+    block_box<D>(lo, hi, s_red, s_out);
+    if (g.tiles == 1) {
+        // The whole cloud is this tile.
+        if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
+        else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
+        return;
     }
-    if (lane_id() == 0) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) { s_red[wave][d] = lo[d]; s_red[wave][D + d] = hi[d]; }
+    if (threadIdx.x < 2 * D) {
+        partials[t * 2 * D + threadIdx.x] = s_out[threadIdx.x];
+        __threadfence();  // publish the partial before this tile is counted
     }
     __syncthreads();
-    if (threadIdx.x < 2 * D) {
-        const int c = threadIdx.x;
-        float v = s_red[0][c];
-        for (int w = 1; w < kBlock / kWave; ++w) v = c < D ? fminf(v, s_red[w][c]) : fmaxf(v, s_red[w][c]);
-        partials[t * 2 * D + c] = v;
+    if (threadIdx.x == 0) {
+        const uint32_t prior = __hip_atomic_fetch_add(seg_done + s, 1u, __ATOMIC_ACQ_REL,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prior == static_cast<uint32_t>(g.tiles - 1);
     }
-}
-
-template <int D>
-__global__ __launch_bounds__(kBlock) void bounds_final_kernel(const Segment* __restrict__ segs,
-                                                              const float* __restrict__ partials,
-                                                              float* __restrict__ scene_min,
-                                                              float* __restrict__ scene_max) {
-    __shared__ float s_red[kBlock / kWave][2 * D];
-    const int s = blockIdx.x;
-    const Segment g = segs[s];
-    float lo[D], hi[D];
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();  // every other tile's partial is now visible
 #pragma unroll
     for (int d = 0; d < D; ++d) { lo[d] = kSeedLo; hi[d] = kSeedHi; }
     for (int j = threadIdx.x; j < g.tiles; j += kBlock) {
@@ -201,45 +237,27 @@ __global__ __launch_bounds__(kBlock) void bounds_final_kernel(const Segment* __r
             hi[d] = fmaxf(hi[d], p[D + d]);
         }
     }
-    const int wave = threadIdx.x / kWave;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        lo[d] = wave_min(lo[d]);
-        hi[d] = wave_max(hi[d]);
-    }
-    if (lane_id() == 0) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) { s_red[wave][d] = lo[d]; s_red[wave][D + d] = hi[d]; }
-    }
-    __syncthreads();
-    if (threadIdx.x < 2 * D) {
-        const int c = threadIdx.x;
-        float v = s_red[0][c];
-        for (int w = 1; w < kBlock / kWave; ++w) v = c < D ? fminf(v, s_red[w][c]) : fmaxf(v, s_red[w][c]);
-        if (c < D) scene_min[static_cast<int64_t>(s) * D + c] = v;
-        else scene_max[static_cast<int64_t>(s) * D + c - D] = v;
-    }
+    __syncthreads();  // s_red is reused
+    block_box<D>(lo, hi, s_red, s_out);
+    if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
+    else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
-// Morton codes + digit-0 tile histograms
+// Morton codes + all sort passes' digit histograms
 // ---------------------------------------------------------------------------
-// Each wave walks its 1024-row slice of the tile in 16 rounds of 64 rows; the
-// lanes that share a digit in a round are found with kRadixBits ballots and
-// the lowest such lane bumps the wave's LDS counter for that digit.
+// One work-group per tile.  Digit counts of the four sort passes are gathered
+// with LDS atomics, then added to the segment's global histograms with one
+// device atomic per non-zero bin.
 template <int D>
 __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict__ points,
                                                         const Segment* __restrict__ segs, int S,
                                                         const float* __restrict__ scene_min,
                                                         const float* __restrict__ scene_max,
                                                         uint32_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ hist,
-                                                        uint32_t* __restrict__ dpre) {
-    constexpr int kWaves = kBlock / kWave;
-    constexpr int kItems = kSortTile / kBlock;
+                                                        uint32_t* __restrict__ hist) {
     __shared__ int s_seg;
-    __shared__ uint32_t s_cnt[kWaves][kRadix];
-    __shared__ uint32_t s_scan[kWaves];
+    __shared__ uint32_t s_hist[kMaxSortPasses][kRadix];
     const int64_t t = blockIdx.x;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
                                      S, t, &s_seg);
@@ -248,50 +266,32 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
     if (lt >= g.tiles) return;
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
+    for (int i = threadIdx.x; i < kMaxSortPasses * kRadix; i += kBlock) (&s_hist[0][0])[i] = 0u;
     float lo[D], hi[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         lo[d] = scene_min[static_cast<int64_t>(s) * D + d];
         hi[d] = scene_max[static_cast<int64_t>(s) * D + d];
     }
-    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0u;
     __syncthreads();
 
-    const int lane = lane_id();
-    const int wave = threadIdx.x / kWave;
-    const uint64_t below = (1ull << lane) - 1ull;
-#pragma unroll 4
-    for (int i = 0; i < kItems; ++i) {
-        const int pos = wave * kWave * kItems + i * kWave + lane;
-        const bool valid = pos < count;
-        uint32_t code = 0xffffffffu;
-        if (valid) {
-            float p[D];
+    for (int j = threadIdx.x; j < count; j += kBlock) {
+        float p[D];
 #pragma unroll
-            for (int d = 0; d < D; ++d) p[d] = points[(row0 + pos) * D + d];
-            code = morton::encode<D>(p, lo, hi);
-            keys[row0 + pos] = code;
-        }
-        const uint32_t digit = code & (kRadix - 1);
-        uint64_t peers = __ballot(valid);
+        for (int d = 0; d < D; ++d) p[d] = points[(row0 + j) * D + d];
+        const uint32_t code = morton::encode<D>(p, lo, hi);
+        keys[row0 + j] = code;
 #pragma unroll
-        for (int b = 0; b < kRadixBits; ++b) {
-            const bool bit = (digit >> b) & 1u;
-            const uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
+        for (int pass = 0; pass < kMaxSortPasses; ++pass) {
+            atomicAdd(&s_hist[pass][(code >> (pass * kRadixBits)) & (kRadix - 1)], 1u);
         }
-        if (valid && (peers & below) == 0) s_cnt[wave][digit] += static_cast<uint32_t>(__popcll(peers));
-        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    uint32_t c = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) c += s_cnt[w][threadIdx.x];
-    const uint32_t excl = block_exclusive_sum(c, s_scan);
-    const int64_t at = static_cast<int64_t>(kRadix) * g.tile_first +
-                       static_cast<int64_t>(threadIdx.x) * g.tiles + lt;
-    hist[at] = c;
-    dpre[at] = excl;
+    for (int pass = 0; pass < kMaxSortPasses; ++pass) {
+        const uint32_t c = s_hist[pass][threadIdx.x];
+        if (c) atomicAdd(hist + (static_cast<int64_t>(pass) * S + s) * kRadix + threadIdx.x, c);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -300,12 +300,15 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
 // Work-group `gl` of pass p owns 2^up consecutive nodes of level lvl_in
 // (leaves for p == 0) and produces the `up` levels above them in LDS,
 // writing every real node it forms.  Nodes of a level are contiguous in
-// storage, so each level's writes are coalesced rows of 2D floats.
+// storage, so each level's writes are coalesced rows of 2D floats.  The same
+// thread that writes a node writes its traversal-array entries (left/right
+// child rows, leaf rank) and, for leaves, the accel's float4 point.
 template <int D, bool kFromPoints>
 __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restrict__ points,
                                                            const Segment* __restrict__ segs, int S,
                                                            const int64_t* __restrict__ sorted,
-                                                           float* __restrict__ node_aabbs, int p) {
+                                                           float* __restrict__ node_aabbs, int p,
+                                                           TreeOutputs out) {
     __shared__ int s_seg;
     __shared__ float s_box[(2 * kSubtreeLeaves - 1) * 2 * D];
     const int64_t grp = blockIdx.x;
@@ -320,6 +323,8 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
     const int up = lvl_in > kSubtreeLevels ? kSubtreeLevels : lvl_in;
     const int width = 1 << up;
     float* nodes = node_aabbs + g.node_start * 2 * D;
+    const bool arrays = out.left != nullptr && (out.arrays_packed || s == 0);
+    const int64_t arr0 = out.arrays_packed ? g.node_start : 0;
     const int tid = threadIdx.x;
 
     if (tid < width) {
@@ -340,6 +345,19 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                 }
 #pragma unroll
                 for (int c = 0; c < 2 * D; ++c) nodes[row * 2 * D + c] = dst[c];
+                if (arrays) {
+                    out.left[arr0 + row] = -1;
+                    out.right[arr0 + row] = -1;
+                    out.leaf[arr0 + row] = j;
+                }
+                if (out.accel_points) {
+                    float4 v;
+                    v.x = dst[0];
+                    v.y = dst[1];
+                    v.z = D == 3 ? dst[D - 1] : 0.0f;
+                    v.w = __int_as_float(static_cast<int>(idx));
+                    out.accel_points[g.start + j] = v;
+                }
             } else {
 #pragma unroll
                 for (int c = 0; c < 2 * D; ++c) dst[c] = nodes[row * 2 * D + c];
@@ -367,43 +385,15 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                 const int64_t row = tree::memory_index(vl, L, heap);
 #pragma unroll
                 for (int c = 0; c < 2 * D; ++c) nodes[row * 2 * D + c] = dst[c];
+                if (arrays) {
+                    const int left_row = tree::memory_index(vl, L, 2 * heap + 1);
+                    out.left[arr0 + row] = left_row;
+                    out.right[arr0 + row] = right_real ? left_row + 1 : -1;
+                    out.leaf[arr0 + row] = -1;
+                }
             }
         }
         __syncthreads();
-    }
-}
-
-// One thread per stored node row: recover the heap index from the row and
-// emit child rows (-1 for leaves / virtual right children) and leaf ranks.
-__global__ __launch_bounds__(kBlock) void traversal_arrays_kernel(const Segment* __restrict__ segs,
-                                                                  int S, int64_t total_nodes,
-                                                                  int32_t* __restrict__ left,
-                                                                  int32_t* __restrict__ right,
-                                                                  int32_t* __restrict__ leaf) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (r >= total_nodes) return;
-    const int s = find_segment([&](int i) { return segs[i].node_start; }, S, r);
-    const Segment g = segs[s];
-    const int lr = static_cast<int>(r - g.node_start);
-    const int L = g.leaf_level;
-    const int vl = g.vl;
-    // Row range of level l starts at level_first(l) - virtual_above(l).
-    int level = 0;
-    while (level < L &&
-           lr >= tree::level_first(level + 1) - tree::virtual_above(vl, L, level + 1)) {
-        ++level;
-    }
-    const int heap = lr + tree::virtual_above(vl, L, level);
-    if (level == L) {
-        left[r] = -1;
-        right[r] = -1;
-        leaf[r] = heap - tree::level_first(L);
-    } else {
-        const int lc = 2 * heap + 1;
-        const int rc = lc + 1;
-        left[r] = tree::memory_index(vl, L, lc);
-        right[r] = tree::is_virtual(vl, L, rc) ? -1 : tree::memory_index(vl, L, rc);
-        leaf[r] = -1;
     }
 }
 
@@ -411,76 +401,78 @@ inline unsigned grid_for(int64_t items) {
     return static_cast<unsigned>((items + kBlock - 1) / kBlock);
 }
 
+// Grid for a clearing/planning launch over `items` words: enough groups to
+// stream the memory, capped (the kernels are grid-stride).
+inline unsigned clear_grid(int64_t items) {
+    const int64_t g = (items + kBlock * 4 - 1) / (kBlock * 4);
+    return static_cast<unsigned>(g < 1 ? 1 : (g > 2048 ? 2048 : g));
+}
+
 }  // namespace
 
-hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream) {
-    plan_uniform_kernel<<<grid_for(S), kBlock, 0, stream>>>(segs, S, static_cast<int>(n), tree);
+hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, uint32_t* clear,
+                               int64_t clear_words, hipStream_t stream) {
+    plan_uniform_kernel<<<clear_grid(S > clear_words ? S : clear_words), kBlock, 0, stream>>>(
+        segs, S, static_cast<int>(n), tree, clear, clear_words);
     return hipGetLastError();
 }
 
 hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
-                               int64_t* node_offsets, hipStream_t stream) {
-    plan_offsets_kernel<<<1, kBlock, 0, stream>>>(segs, offsets, S, tree, node_offsets);
+                               int64_t* node_offsets, uint32_t* clear, int64_t clear_words,
+                               hipStream_t stream) {
+    const unsigned grid = 1 + (clear_words > 0 ? clear_grid(clear_words) : 0);
+    plan_offsets_kernel<<<grid, kBlock, 0, stream>>>(segs, offsets, S, tree, node_offsets, clear,
+                                                     clear_words);
     return hipGetLastError();
 }
 
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
-                         int64_t tiles, float* partials, float* scene_min, float* scene_max,
-                         hipStream_t stream) {
+                         int64_t tiles, float* partials, uint32_t* seg_done, float* scene_min,
+                         float* scene_max, hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>(tiles);
+    const int Si = static_cast<int>(S);
     if (D == 3) {
-        bounds_partial_kernel<3><<<static_cast<unsigned>(tiles), kBlock, 0, stream>>>(
-            points, segs, static_cast<int>(S), partials);
-        bounds_final_kernel<3><<<static_cast<unsigned>(S), kBlock, 0, stream>>>(
-            segs, partials, scene_min, scene_max);
+        bounds_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, partials, seg_done, scene_min, scene_max);
     } else {
-        bounds_partial_kernel<2><<<static_cast<unsigned>(tiles), kBlock, 0, stream>>>(
-            points, segs, static_cast<int>(S), partials);
-        bounds_final_kernel<2><<<static_cast<unsigned>(S), kBlock, 0, stream>>>(
-            segs, partials, scene_min, scene_max);
+        bounds_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, partials, seg_done, scene_min, scene_max);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S, int64_t tiles,
                          const float* scene_min, const float* scene_max, uint32_t* keys,
-                         uint32_t* hist, uint32_t* dpre, hipStream_t stream) {
+                         uint32_t* hist, hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>(tiles);
+    const int Si = static_cast<int>(S);
     if (D == 3) {
-        morton_kernel<3><<<static_cast<unsigned>(tiles), kBlock, 0, stream>>>(
-            points, segs, static_cast<int>(S), scene_min, scene_max, keys, hist, dpre);
+        morton_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist);
     } else {
-        morton_kernel<2><<<static_cast<unsigned>(tiles), kBlock, 0, stream>>>(
-            points, segs, static_cast<int>(S), scene_min, scene_max, keys, hist, dpre);
+        morton_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_tree(const float* points, int D, const Segment* segs, int64_t S, int64_t total,
-                       int64_t max_n, const int64_t* sorted, float* node_aabbs, hipStream_t stream) {
+                       int64_t max_n, const int64_t* sorted, float* node_aabbs,
+                       const TreeOutputs& out, hipStream_t stream) {
     // Passes needed by the deepest cloud.
     const int L = tree::leaf_level(static_cast<int>(max_n));
     const int passes = L == 0 ? 1 : (L + kSubtreeLevels - 1) / kSubtreeLevels;
+    const int Si = static_cast<int>(S);
     for (int p = 0; p < passes; ++p) {
         const int64_t groups = (total >> (kSubtreeLevels * (p + 1))) + S + 1;
         const unsigned grid = static_cast<unsigned>(groups);
         if (D == 3) {
-            if (p == 0) tree_pass_kernel<3, true><<<grid, kBlock, 0, stream>>>(points, segs, static_cast<int>(S), sorted, node_aabbs, p);
-            else tree_pass_kernel<3, false><<<grid, kBlock, 0, stream>>>(points, segs, static_cast<int>(S), sorted, node_aabbs, p);
+            if (p == 0) tree_pass_kernel<3, true><<<grid, kBlock, 0, stream>>>(points, segs, Si, sorted, node_aabbs, p, out);
+            else tree_pass_kernel<3, false><<<grid, kBlock, 0, stream>>>(points, segs, Si, sorted, node_aabbs, p, out);
         } else {
-            if (p == 0) tree_pass_kernel<2, true><<<grid, kBlock, 0, stream>>>(points, segs, static_cast<int>(S), sorted, node_aabbs, p);
-            else tree_pass_kernel<2, false><<<grid, kBlock, 0, stream>>>(points, segs, static_cast<int>(S), sorted, node_aabbs, p);
+            if (p == 0) tree_pass_kernel<2, true><<<grid, kBlock, 0, stream>>>(points, segs, Si, sorted, node_aabbs, p, out);
+            else tree_pass_kernel<2, false><<<grid, kBlock, 0, stream>>>(points, segs, Si, sorted, node_aabbs, p, out);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
-}
-
-hipError_t launch_traversal_arrays(const Segment* segs, int64_t S, int64_t total_nodes,
-                                   int32_t* left, int32_t* right, int32_t* leaf,
-                                   hipStream_t stream) {
-    traversal_arrays_kernel<<<grid_for(total_nodes), kBlock, 0, stream>>>(
-        segs, static_cast<int>(S), total_nodes, left, right, leaf);
-    return hipGetLastError();
 }
 
 }  // namespace tbvh

@@ -48,24 +48,27 @@ constexpr int64_t kMaxRows = 2147483647;  // INT32_MAX
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-// Workspace carve-out shared by build and query sort.
+// Workspace carve-out shared by build and query sort.  The histogram,
+// look-back status and ticket words are contiguous: the planning kernel
+// clears them in one sweep.
 struct Layout {
     size_t segs = 0, partials = 0, keys_a = 0, keys_b = 0, vals_a = 0, vals_b = 0;
-    size_t hist = 0, dpre = 0, total = 0;
+    size_t clear = 0, total = 0;
+    int64_t tiles = 0, clear_words = 0;
 };
 
 Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials) {
     Layout l;
-    const int64_t tiles = tiles_bound(rows, S);
+    l.tiles = tiles_bound(rows, S);
+    l.clear_words = sort_clear_words(S, l.tiles);
     size_t at = 0;
     l.segs = at; at = align_up(at + static_cast<size_t>(S) * sizeof(Segment));
-    l.partials = at; at = align_up(at + (with_partials ? static_cast<size_t>(tiles) * 2 * D * sizeof(float) : 0));
+    l.partials = at; at = align_up(at + (with_partials ? static_cast<size_t>(l.tiles) * 2 * D * sizeof(float) : 0));
     l.keys_a = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.keys_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.vals_a = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.vals_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
-    l.hist = at; at = align_up(at + static_cast<size_t>(tiles) * kRadix * 4);
-    l.dpre = at; at = align_up(at + static_cast<size_t>(tiles) * kRadix * 4);
+    l.clear = at; at = align_up(at + static_cast<size_t>(l.clear_words) * 4);
     l.total = at;
     return l;
 }
@@ -75,16 +78,21 @@ T* carve(void* ws, size_t off) {
     return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-SortBuffers sort_buffers(void* ws, const Layout& l) {
+SortBuffers sort_buffers(void* ws, const Layout& l, int64_t S) {
     SortBuffers b;
     b.keys_a = carve<uint32_t>(ws, l.keys_a);
     b.keys_b = carve<uint32_t>(ws, l.keys_b);
     b.vals_a = carve<uint32_t>(ws, l.vals_a);
     b.vals_b = carve<uint32_t>(ws, l.vals_b);
-    b.hist = carve<uint32_t>(ws, l.hist);
-    b.dpre = carve<uint32_t>(ws, l.dpre);
+    b.hist = carve<uint32_t>(ws, l.clear);
+    b.status = b.hist + static_cast<int64_t>(kMaxSortPasses) * S * kRadix;
+    b.tickets = b.status + static_cast<int64_t>(kMaxSortPasses) * l.tiles * kRadix;
+    b.seg_done = b.tickets + kMaxSortPasses + 1;
     return b;
 }
+
+// Keys of the last of four passes land in keys_a (passes alternate a->b->a).
+uint32_t* last_pass_keys(const SortBuffers& b) { return b.keys_a; }
 
 int check_dim(const char* op, int D) {
     if (D != 2 && D != 3) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: D must be 2 or 3, got %d", op, D);
@@ -110,6 +118,85 @@ int check_workspace(const char* op, void* ws, size_t have, size_t need) {
 }
 
 bool supported_k(int k) { return k == 4 || k == 8 || k == 16 || k == 32; }
+
+
+// Everything one build call launches, in order: plan (+ clear), bounds,
+// Morton (+ all pass histograms), four sort passes, implicit-tree passes
+// (+ traversal arrays, + accel points) and, when `accel` is given, the
+// accel's radix-tree records.
+struct BuildOut {
+    float* node_aabbs;
+    int64_t* sorted_indices;
+    float* scene_min;
+    float* scene_max;
+    int32_t* left;
+    int32_t* right;
+    int32_t* leaf;
+    int64_t* node_offsets;  // ragged only
+    void* accel;            // optional
+};
+
+hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int64_t n_uniform,
+                     int64_t rows, int D, const BuildOut& o, void* ws, hipStream_t stream) {
+    const Layout l = make_layout(S, rows, D, true);
+    Segment* segs = carve<Segment>(ws, l.segs);
+    const SortBuffers sb = sort_buffers(ws, l, S);
+    const bool ragged = offsets != nullptr;
+    hipError_t e = ragged ? launch_plan_offsets(segs, offsets, S, true, o.node_offsets, sb.hist,
+                                                l.clear_words, stream)
+                          : launch_plan_uniform(segs, S, n_uniform, true, sb.hist, l.clear_words,
+                                                stream);
+    if (e != hipSuccess) return e;
+    float* partials = carve<float>(ws, l.partials);
+    if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, sb.seg_done, o.scene_min,
+                           o.scene_max, stream)) != hipSuccess) {
+        return e;
+    }
+    if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.hist,
+                           stream)) != hipSuccess) {
+        return e;
+    }
+    uint32_t* sorted_keys = o.accel ? last_pass_keys(sb) : nullptr;
+    if ((e = launch_sort(segs, S, l.tiles, D == 3 ? 30 : 32, sb, o.sorted_indices, sorted_keys,
+                         stream)) != hipSuccess) {
+        return e;
+    }
+    TreeOutputs to;
+    to.left = o.left;
+    to.right = o.right;
+    to.leaf = o.leaf;
+    to.arrays_packed = ragged;
+    to.accel_points = o.accel ? static_cast<float4*>(o.accel) : nullptr;
+    const int64_t max_n = ragged ? (rows < kMaxCloud ? rows : kMaxCloud) : n_uniform;
+    if ((e = launch_tree(points, D, segs, S, rows, max_n, o.sorted_indices, o.node_aabbs, to,
+                         stream)) != hipSuccess) {
+        return e;
+    }
+    if (o.accel) return launch_accel_nodes(o.node_aabbs, D, segs, S, rows, sorted_keys, o.accel, stream);
+    return hipSuccess;
+}
+
+hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t S, int64_t m_uniform,
+                          int64_t rows, int D, const float* scene_min, const float* scene_max,
+                          int64_t* order, uint32_t* codes_only, void* ws, hipStream_t stream) {
+    const Layout l = make_layout(S, rows, D, false);
+    Segment* segs = carve<Segment>(ws, l.segs);
+    const SortBuffers sb = sort_buffers(ws, l, S);
+    hipError_t e = offsets ? launch_plan_offsets(segs, offsets, S, false, nullptr, sb.hist,
+                                                 l.clear_words, stream)
+                           : launch_plan_uniform(segs, S, m_uniform, false, sb.hist, l.clear_words,
+                                                 stream);
+    if (e != hipSuccess) return e;
+    uint32_t* keys = codes_only ? codes_only : sb.keys_a;
+    if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys, sb.hist,
+                           stream)) != hipSuccess) {
+        return e;
+    }
+    if (codes_only) return hipSuccess;
+    return launch_sort(segs, S, l.tiles, D == 3 ? 30 : 32, sb, order, nullptr, stream);
+}
+
+bool aligned(const void* p) { return reinterpret_cast<uintptr_t>(p) % kAlign == 0; }
 
 }  // namespace
 
@@ -146,36 +233,44 @@ int tbvh_build_workspace_size(int64_t B, int64_t N, int D, size_t* bytes) {
     return ok();
 }
 
+static int build_batched(const char* op, const float* points, int64_t B, int64_t N, int D,
+                         const BuildOut& o, void* workspace, size_t workspace_bytes,
+                         void* stream_ptr) {
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    if (!points || !o.node_aabbs || !o.sorted_indices || !o.scene_min || !o.scene_max || !o.left ||
+        !o.right || !o.leaf) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    if (o.accel) {
+        if (N > kMaxAccelCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: clouds may hold at most 2^28 points", op);
+        if (!aligned(o.accel)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
+    }
+    const Layout l = make_layout(B, B * N, D, true);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    TBVH_TRY(op, run_build(points, nullptr, B, N, B * N, D, o, workspace,
+                           static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
 int tbvh_build(const float* points, int64_t B, int64_t N, int D, float* node_aabbs,
                int64_t* sorted_indices, float* scene_min, float* scene_max,
                int32_t* left_child_mem, int32_t* right_child_mem, int32_t* mem_to_leaf,
                void* workspace, size_t workspace_bytes, void* stream_ptr) {
-    const char* op = "tbvh_build";
-    if (int r = check_dim(op, D)) return r;
-    if (int r = check_batched_extent(op, B, N)) return r;
-    if (!points || !node_aabbs || !sorted_indices || !scene_min || !scene_max ||
-        !left_child_mem || !right_child_mem || !mem_to_leaf) {
-        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
-    }
-    const int64_t rows = B * N;
-    const Layout l = make_layout(B, rows, D, true);
-    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    Segment* segs = carve<Segment>(workspace, l.segs);
-    const int64_t tiles = tiles_bound(rows, B);
-    const SortBuffers sb = sort_buffers(workspace, l);
-    const int nr = tree::real_node_count(static_cast<int>(N));
+    const BuildOut o{node_aabbs, sorted_indices, scene_min, scene_max, left_child_mem,
+                     right_child_mem, mem_to_leaf, nullptr, nullptr};
+    return build_batched("tbvh_build", points, B, N, D, o, workspace, workspace_bytes, stream_ptr);
+}
 
-    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
-    TBVH_TRY(op, launch_bounds(points, D, segs, B, tiles, carve<float>(workspace, l.partials),
-                               scene_min, scene_max, stream));
-    TBVH_TRY(op, launch_morton(points, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
-                               sb.hist, sb.dpre, stream));
-    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, sorted_indices, stream));
-    TBVH_TRY(op, launch_tree(points, D, segs, B, rows, N, sorted_indices, node_aabbs, stream));
-    TBVH_TRY(op, launch_traversal_arrays(segs, 1, nr, left_child_mem, right_child_mem, mem_to_leaf,
-                                         stream));
-    return ok();
+int tbvh_build_with_accel(const float* points, int64_t B, int64_t N, int D, float* node_aabbs,
+                          int64_t* sorted_indices, float* scene_min, float* scene_max,
+                          int32_t* left_child_mem, int32_t* right_child_mem, int32_t* mem_to_leaf,
+                          void* accel, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    if (!accel) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_build_with_accel: accel is null");
+    const BuildOut o{node_aabbs, sorted_indices, scene_min, scene_max, left_child_mem,
+                     right_child_mem, mem_to_leaf, nullptr, accel};
+    return build_batched("tbvh_build_with_accel", points, B, N, D, o, workspace, workspace_bytes,
+                         stream_ptr);
 }
 
 int tbvh_build_ragged_workspace_size(int64_t B, int64_t total, int D, size_t* bytes) {
@@ -188,12 +283,9 @@ int tbvh_build_ragged_workspace_size(int64_t B, int64_t total, int D, size_t* by
     return ok();
 }
 
-int tbvh_build_ragged(const float* points, const int64_t* offsets, int64_t B, int64_t total, int D,
-                      float* node_aabbs, int64_t* sorted_indices, float* scene_min,
-                      float* scene_max, int32_t* left_child_mem, int32_t* right_child_mem,
-                      int32_t* mem_to_leaf, int64_t* node_offsets, int64_t total_nodes,
-                      void* workspace, size_t workspace_bytes, void* stream_ptr) {
-    const char* op = "tbvh_build_ragged";
+static int build_ragged(const char* op, const float* points, const int64_t* offsets, int64_t B,
+                        int64_t total, int D, const BuildOut& o, int64_t total_nodes,
+                        void* workspace, size_t workspace_bytes, void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
     if (B < 1 || total < B) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total >= B", op);
     if (total > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
@@ -201,28 +293,46 @@ int tbvh_build_ragged(const float* points, const int64_t* offsets, int64_t B, in
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total_nodes is smaller than any tree over %lld points",
                     op, static_cast<long long>(total));
     }
-    if (!points || !offsets || !node_aabbs || !sorted_indices || !scene_min || !scene_max ||
-        !left_child_mem || !right_child_mem || !mem_to_leaf || !node_offsets) {
+    if (!points || !offsets || !o.node_aabbs || !o.sorted_indices || !o.scene_min || !o.scene_max ||
+        !o.left || !o.right || !o.leaf || !o.node_offsets) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    if (o.accel && !aligned(o.accel)) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
     }
     const Layout l = make_layout(B, total, D, true);
     if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    Segment* segs = carve<Segment>(workspace, l.segs);
-    const int64_t tiles = tiles_bound(total, B);
-    const SortBuffers sb = sort_buffers(workspace, l);
-    const int64_t max_n = total < kMaxCloud ? total : kMaxCloud;
-
-    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, node_offsets, stream));
-    TBVH_TRY(op, launch_bounds(points, D, segs, B, tiles, carve<float>(workspace, l.partials),
-                               scene_min, scene_max, stream));
-    TBVH_TRY(op, launch_morton(points, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
-                               sb.hist, sb.dpre, stream));
-    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, sorted_indices, stream));
-    TBVH_TRY(op, launch_tree(points, D, segs, B, total, max_n, sorted_indices, node_aabbs, stream));
-    TBVH_TRY(op, launch_traversal_arrays(segs, B, total_nodes, left_child_mem, right_child_mem,
-                                         mem_to_leaf, stream));
+    TBVH_TRY(op, run_build(points, offsets, B, 0, total, D, o, workspace,
+                           static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_build_ragged(const float* points, const int64_t* offsets, int64_t B, int64_t total, int D,
+                      float* node_aabbs, int64_t* sorted_indices, float* scene_min,
+                      float* scene_max, int32_t* left_child_mem, int32_t* right_child_mem,
+                      int32_t* mem_to_leaf, int64_t* node_offsets, int64_t total_nodes,
+                      void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const BuildOut o{node_aabbs, sorted_indices, scene_min, scene_max, left_child_mem,
+                     right_child_mem, mem_to_leaf, node_offsets, nullptr};
+    return build_ragged("tbvh_build_ragged", points, offsets, B, total, D, o, total_nodes, workspace,
+                        workspace_bytes, stream_ptr);
+}
+
+int tbvh_build_ragged_with_accel(const float* points, const int64_t* offsets, int64_t B,
+                                 int64_t total, int D, float* node_aabbs, int64_t* sorted_indices,
+                                 float* scene_min, float* scene_max, int32_t* left_child_mem,
+                                 int32_t* right_child_mem, int32_t* mem_to_leaf,
+                                 int64_t* node_offsets, int64_t total_nodes, void* accel,
+                                 void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    if (!accel) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_build_ragged_with_accel: accel is null");
+    if (total > kMaxAccelCloud * B) {
+        // A cheap necessary condition; the caller checks each cloud's size.
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_build_ragged_with_accel: clouds may hold at most 2^28 points");
+    }
+    const BuildOut o{node_aabbs, sorted_indices, scene_min, scene_max, left_child_mem,
+                     right_child_mem, mem_to_leaf, node_offsets, accel};
+    return build_ragged("tbvh_build_ragged_with_accel", points, offsets, B, total, D, o, total_nodes,
+                        workspace, workspace_bytes, stream_ptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -238,54 +348,38 @@ int tbvh_sort_queries_workspace_size(int64_t B, int64_t M, int D, size_t* bytes)
     return ok();
 }
 
-int tbvh_sort_queries(const float* queries, int64_t B, int64_t M, int D, const float* scene_min,
-                      const float* scene_max, int64_t* order, void* workspace,
-                      size_t workspace_bytes, void* stream_ptr) {
-    const char* op = "tbvh_sort_queries";
+static int sort_batched(const char* op, const float* queries, int64_t B, int64_t M, int D,
+                        const float* scene_min, const float* scene_max, int64_t* order,
+                        uint32_t* codes, void* workspace, size_t workspace_bytes, void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
     if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
     if (M == 0) return ok();
     if (M > kMaxCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: at most 2^30 queries per cloud", op);
-    if (!queries || !scene_min || !scene_max || !order) {
+    if (!queries || !scene_min || !scene_max || (!order && !codes)) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }
-    const int64_t rows = B * M;
-    const Layout l = make_layout(B, rows, D, false);
+    const Layout l = make_layout(B, B * M, D, false);
     if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    Segment* segs = carve<Segment>(workspace, l.segs);
-    const int64_t tiles = tiles_bound(rows, B);
-    const SortBuffers sb = sort_buffers(workspace, l);
-    TBVH_TRY(op, launch_plan_uniform(segs, B, M, false, stream));
-    TBVH_TRY(op, launch_morton(queries, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
-                               sb.hist, sb.dpre, stream));
-    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, order, stream));
+    TBVH_TRY(op, run_query_sort(queries, nullptr, B, M, B * M, D, scene_min, scene_max, order, codes,
+                                workspace, static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_sort_queries(const float* queries, int64_t B, int64_t M, int D, const float* scene_min,
+                      const float* scene_max, int64_t* order, void* workspace,
+                      size_t workspace_bytes, void* stream_ptr) {
+    if (!order && M > 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_sort_queries: null input or output pointer");
+    return sort_batched("tbvh_sort_queries", queries, B, M, D, scene_min, scene_max, order, nullptr,
+                        workspace, workspace_bytes, stream_ptr);
 }
 
 int tbvh_morton_codes(const float* rows, int64_t B, int64_t M, int D, const float* scene_min,
                       const float* scene_max, uint32_t* codes, void* workspace,
                       size_t workspace_bytes, void* stream_ptr) {
-    const char* op = "tbvh_morton_codes";
-    if (int r = check_dim(op, D)) return r;
-    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
-    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total row count must fit in signed int32", op);
-    if (M == 0) return ok();
-    if (M > kMaxCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: at most 2^30 rows per cloud", op);
-    if (!rows || !scene_min || !scene_max || !codes) {
-        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
-    }
-    const int64_t n = B * M;
-    const Layout l = make_layout(B, n, D, false);
-    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    Segment* segs = carve<Segment>(workspace, l.segs);
-    const SortBuffers sb = sort_buffers(workspace, l);
-    TBVH_TRY(op, launch_plan_uniform(segs, B, M, false, stream));
-    TBVH_TRY(op, launch_morton(rows, D, segs, B, tiles_bound(n, B), scene_min, scene_max, codes,
-                               sb.hist, sb.dpre, stream));
-    return ok();
+    if (!codes && M > 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_morton_codes: null input or output pointer");
+    return sort_batched("tbvh_morton_codes", rows, B, M, D, scene_min, scene_max, nullptr, codes,
+                        workspace, workspace_bytes, stream_ptr);
 }
 
 int tbvh_sort_queries_ragged_workspace_size(int64_t B, int64_t total_q, int D, size_t* bytes) {
@@ -312,14 +406,8 @@ int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets,
     }
     const Layout l = make_layout(B, total_q, D, false);
     if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    Segment* segs = carve<Segment>(workspace, l.segs);
-    const int64_t tiles = tiles_bound(total_q, B);
-    const SortBuffers sb = sort_buffers(workspace, l);
-    TBVH_TRY(op, launch_plan_offsets(segs, query_offsets, B, false, nullptr, stream));
-    TBVH_TRY(op, launch_morton(queries, D, segs, B, tiles, scene_min, scene_max, sb.keys_a,
-                               sb.hist, sb.dpre, stream));
-    TBVH_TRY(op, launch_sort(segs, B, tiles, D == 3 ? 30 : 32, sb, order, stream));
+    TBVH_TRY(op, run_query_sort(queries, query_offsets, B, 0, total_q, D, scene_min, scene_max, order,
+                                nullptr, workspace, static_cast<hipStream_t>(stream_ptr)));
     return ok();
 }
 
@@ -446,9 +534,10 @@ int tbvh_accel_build(const float* points, const int64_t* sorted_indices, const f
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     Segment* segs = carve<Segment>(workspace, 0);
     uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
-    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
-    TBVH_TRY(op, launch_accel_build(points, sorted_indices, node_aabbs, scene_min, scene_max, D, segs,
-                                    B, total, codes, accel, stream));
+    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, nullptr, 0, stream));
+    TBVH_TRY(op, launch_accel_points(points, sorted_indices, scene_min, scene_max, D, segs, B, total,
+                                     codes, accel, stream));
+    TBVH_TRY(op, launch_accel_nodes(node_aabbs, D, segs, B, total, codes, accel, stream));
     return ok();
 }
 
@@ -468,9 +557,10 @@ int tbvh_accel_build_ragged(const float* points, const int64_t* offsets, const i
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     Segment* segs = carve<Segment>(workspace, 0);
     uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
-    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, nullptr, stream));
-    TBVH_TRY(op, launch_accel_build(points, sorted_indices, node_aabbs, scene_min, scene_max, D, segs,
-                                    B, total, codes, accel, stream));
+    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, nullptr, nullptr, 0, stream));
+    TBVH_TRY(op, launch_accel_points(points, sorted_indices, scene_min, scene_max, D, segs, B, total,
+                                     codes, accel, stream));
+    TBVH_TRY(op, launch_accel_nodes(node_aabbs, D, segs, B, total, codes, accel, stream));
     return ok();
 }
 

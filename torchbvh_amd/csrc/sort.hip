@@ -7,14 +7,23 @@
 // stable counting sort give exactly that.
 //
 // Design (gfx950): 8-bit digits, kSortTile = 4096 keys per tile, 256-thread
-// work-groups, tiles never straddle segments.  Per pass:
-//   upsweep  per-tile digit counts (wave64 ballot matching, no atomics)
-//   spine    one wave per (segment, digit): scatter base of every tile
-//   scatter  rank keys inside the tile (stable), stage the tile in LDS in
-//            digit order, then write each digit run contiguously
-// The digit-0 counts come from the Morton kernel, so pass 0 has no upsweep;
-// pass 0 synthesises the values (local row index) and the last pass writes
-// the int64 indices directly.
+// work-groups, tiles never straddle segments.  The Morton kernel accumulates
+// every pass's per-segment digit histogram, so each pass is one kernel
+// ("onesweep": Adinets & Merrill, 2022):
+//   1. the work-group takes the next tile ticket (tickets follow dispatch
+//      order, so every lower ticket belongs to a running or finished group);
+//   2. ranks its keys stably (wave64 ballot matching, striped order);
+//   3. publishes each digit's count, then looks back over earlier tiles of
+//      its segment, summing published counts until it meets an inclusive
+//      prefix, and publishes its own inclusive prefix;
+//   4. stages the tile in LDS in digit order and writes each digit run
+//      contiguously at segment start + digit start + prefix.
+// Status words pack flag and count in one 32-bit word and are read and
+// written with agent-scope atomics, so they are coherent across XCDs.  A
+// group publishes all its aggregates before it waits on anyone, so every
+// wait ends; the spin is also bounded and a shared abort flag ends all spins
+// at once should that bound ever be reached (the output is then invalid, but
+// the kernel exits).
 #include "tbvh_internal.hpp"
 
 namespace tbvh {
@@ -22,13 +31,17 @@ namespace {
 
 constexpr int kWaves = kBlock / kWave;
 constexpr int kItems = kSortTile / kBlock;
+constexpr uint32_t kFlagAggregate = 1u << 30;
+constexpr uint32_t kFlagPrefix = 2u << 30;
+constexpr uint32_t kCountMask = (1u << 30) - 1;
+constexpr int kSpinLimit = 1 << 20;
 
-__device__ __forceinline__ int tile_segment(const Segment* segs, int S, int64_t t, int* s_seg) {
-    if (threadIdx.x == 0) {
-        *s_seg = find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); }, S, t);
-    }
-    __syncthreads();
-    return *s_seg;
+__device__ __forceinline__ uint32_t load_status(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void store_status(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Lanes of the current wave holding the same digit as this lane (among
@@ -44,84 +57,10 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
     return peers;
 }
 
-__global__ __launch_bounds__(kBlock) void upsweep_kernel(const Segment* __restrict__ segs, int S,
-                                                         const uint32_t* __restrict__ keys, int shift,
-                                                         uint32_t* __restrict__ hist,
-                                                         uint32_t* __restrict__ dpre) {
-    __shared__ int s_seg;
-    __shared__ uint32_t s_cnt[kWaves][kRadix];
-    __shared__ uint32_t s_scan[kWaves];
-    const int64_t t = blockIdx.x;
-    const Segment g = segs[tile_segment(segs, S, t, &s_seg)];
-    const int lt = static_cast<int>(t - g.tile_first);
-    if (lt >= g.tiles) return;
-    const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
-    const int count = min(kSortTile, g.n - lt * kSortTile);
-    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0u;
-    __syncthreads();
-    const int lane = lane_id();
-    const int wave = threadIdx.x / kWave;
-    const uint64_t below = (1ull << lane) - 1ull;
-#pragma unroll 4
-    for (int i = 0; i < kItems; ++i) {
-        const int pos = wave * kWave * kItems + i * kWave + lane;
-        const bool valid = pos < count;
-        const uint32_t key = valid ? keys[row0 + pos] : 0u;
-        const uint32_t digit = (key >> shift) & (kRadix - 1);
-        const uint64_t peers = match_digit(digit, valid);
-        if (valid && (peers & below) == 0) s_cnt[wave][digit] += static_cast<uint32_t>(__popcll(peers));
-        __builtin_amdgcn_wave_barrier();
-    }
-    __syncthreads();
-    uint32_t c = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) c += s_cnt[w][threadIdx.x];
-    const uint32_t excl = block_exclusive_sum(c, s_scan);
-    const int64_t at = static_cast<int64_t>(kRadix) * g.tile_first +
-                       static_cast<int64_t>(threadIdx.x) * g.tiles + lt;
-    hist[at] = c;
-    dpre[at] = excl;
-}
-
-// One wave per (segment, digit).  Input, per segment block laid out
-// digit-major ([digit][tile]): hist = tile counts, dpre = per-tile count of
-// smaller digits.  Output (in place over hist): the row, relative to the
-// segment start, at which the tile's run of this digit starts =
-//   #(keys of the segment with a smaller digit)
-//   + #(keys with this digit in earlier tiles of the segment).
-__global__ __launch_bounds__(kBlock) void spine_kernel(const Segment* __restrict__ segs, int S,
-                                                       uint32_t* __restrict__ hist,
-                                                       const uint32_t* __restrict__ dpre) {
-    const int64_t gw = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
-    const int64_t s = gw / kRadix;
-    if (s >= S) return;
-    const int d = static_cast<int>(gw % kRadix);
-    const Segment g = segs[s];
-    const int lane = lane_id();
-    const int64_t blk = static_cast<int64_t>(kRadix) * g.tile_first + static_cast<int64_t>(d) * g.tiles;
-    uint32_t smaller = 0;
-    for (int j = lane; j < g.tiles; j += kWave) smaller += dpre[blk + j];
-    smaller = wave_sum(smaller);
-    // Rows are < 2^31, so the digit base fits 32 bits relative to the segment.
-    uint32_t carry = smaller;
-    for (int j0 = 0; j0 < g.tiles; j0 += kWave) {
-        const int j = j0 + lane;
-        const uint32_t c = j < g.tiles ? hist[blk + j] : 0u;
-        const uint32_t incl = wave_inclusive_sum(c);
-        if (j < g.tiles) hist[blk + j] = carry + incl - c;
-        carry += __shfl(incl, kWave - 1, kWave);
-    }
-}
-
-// base[] rows are relative to the segment start (segments hold < 2^31 rows).
 template <bool kFirst, bool kLast>
-__global__ __launch_bounds__(kBlock) void scatter_kernel(const Segment* __restrict__ segs, int S,
-                                                         const uint32_t* __restrict__ keys_in,
-                                                         const uint32_t* __restrict__ vals_in,
-                                                         uint32_t* __restrict__ keys_out,
-                                                         uint32_t* __restrict__ vals_out,
-                                                         int64_t* __restrict__ idx_out,
-                                                         const uint32_t* __restrict__ base, int shift) {
+__global__ __launch_bounds__(kBlock) void onesweep_kernel(const Segment* __restrict__ segs, int S,
+                                                          int64_t tiles_total, SortPass pass) {
+    __shared__ int64_t s_tile;
     __shared__ int s_seg;
     __shared__ uint32_t s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
@@ -129,16 +68,29 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(const Segment* __restri
     __shared__ uint32_t s_start[kRadix];
     __shared__ uint32_t s_base[kRadix];
     __shared__ uint32_t s_scan[kWaves];
-    const int64_t t = blockIdx.x;
-    const Segment g = segs[tile_segment(segs, S, t, &s_seg)];
+    if (threadIdx.x == 0) {
+        const int64_t t = atomicAdd(pass.ticket, 1u);
+        s_tile = t;
+        s_seg = t < tiles_total
+                    ? find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); }, S, t)
+                    : 0;
+    }
+    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0u;
+    __syncthreads();
+    const int64_t t = s_tile;
+    if (t >= tiles_total) return;
+    const Segment g = segs[s_seg];
     const int lt = static_cast<int>(t - g.tile_first);
-    if (lt >= g.tiles) return;
+    uint32_t* status = pass.status + t * kRadix;
+    if (lt >= g.tiles) {
+        // A ticket past the segment's last tile (surplus grid): nothing to
+        // sort, but publish zero prefixes so no later tile can wait on it.
+        store_status(status + threadIdx.x, kFlagPrefix);
+        return;
+    }
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
-    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0u;
-    s_base[threadIdx.x] = base[static_cast<int64_t>(kRadix) * g.tile_first +
-                               static_cast<int64_t>(threadIdx.x) * g.tiles + lt];
-    __syncthreads();
+    const int shift = pass.shift;
 
     const int lane = lane_id();
     const int wave = threadIdx.x / kWave;
@@ -148,11 +100,11 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(const Segment* __restri
     for (int i = 0; i < kItems; ++i) {
         const int pos = wave * kWave * kItems + i * kWave + lane;
         const bool valid = pos < count;
-        key[i] = valid ? keys_in[row0 + pos] : 0xffffffffu;
+        key[i] = valid ? pass.keys_in[row0 + pos] : 0xffffffffu;
         if constexpr (kFirst) {
             val[i] = static_cast<uint32_t>(lt * kSortTile + pos);
         } else {
-            val[i] = valid ? vals_in[row0 + pos] : 0u;
+            val[i] = valid ? pass.vals_in[row0 + pos] : 0u;
         }
     }
 #pragma unroll
@@ -169,18 +121,50 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(const Segment* __restri
         rank[i] = prior + before;
     }
     __syncthreads();
-    {
-        const int d = threadIdx.x;
-        uint32_t run = 0;
+
+    // Thread d owns digit d: tile count, publish, look back.
+    const int d = threadIdx.x;
+    uint32_t run = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const uint32_t c = s_cnt[w][d];
-            s_cnt[w][d] = run;
-            run += c;
-        }
-        s_start[d] = block_exclusive_sum(run, s_scan);
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t c = s_cnt[w][d];
+        s_cnt[w][d] = run;
+        run += c;
     }
+    const uint32_t tile_count = run;
+    uint32_t before_tiles = 0;
+    if (lt == 0) {
+        store_status(status + d, kFlagPrefix | tile_count);
+    } else {
+        store_status(status + d, kFlagAggregate | tile_count);
+        for (int64_t j = t - 1;; --j) {
+            const uint32_t* other = pass.status + j * kRadix + d;
+            uint32_t v = load_status(other);
+            int spins = 0;
+            while ((v >> 30) == 0) {
+                if (++spins > kSpinLimit) {
+                    store_status(pass.abort, 1u);
+                }
+                if ((spins & 63) == 0 && load_status(pass.abort) != 0u) {
+                    v = kFlagPrefix;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                v = load_status(other);
+            }
+            before_tiles += v & kCountMask;
+            if ((v & ~kCountMask) == kFlagPrefix) break;
+        }
+        store_status(status + d, kFlagPrefix | ((before_tiles + tile_count) & kCountMask));
+    }
+    // Digit starts of the segment from its global histogram; tile-local
+    // digit starts from the tile counts.
+    const uint32_t seg_count = pass.hist[static_cast<int64_t>(s_seg) * kRadix + d];
+    const uint32_t digit_start = block_exclusive_sum(seg_count, s_scan);
+    s_base[d] = digit_start + before_tiles;
+    s_start[d] = block_exclusive_sum(tile_count, s_scan);
     __syncthreads();
+
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const int pos = wave * kWave * kItems + i * kWave + lane;
@@ -200,10 +184,11 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(const Segment* __restri
         if (rel >= static_cast<uint32_t>(g.n)) continue;  // unreachable when counts agree
         const int64_t row = g.start + rel;
         if constexpr (kLast) {
-            idx_out[row] = static_cast<int64_t>(s_vals[j]);
+            pass.idx_out[row] = static_cast<int64_t>(s_vals[j]);
+            if (pass.keys_out) pass.keys_out[row] = k;
         } else {
-            keys_out[row] = k;
-            vals_out[row] = s_vals[j];
+            pass.keys_out[row] = k;
+            pass.vals_out[row] = s_vals[j];
         }
     }
 }
@@ -211,9 +196,9 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(const Segment* __restri
 }  // namespace
 
 hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles, int key_bits,
-                       const SortBuffers& b, int64_t* order, hipStream_t stream) {
+                       const SortBuffers& b, int64_t* order, uint32_t* sorted_keys,
+                       hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
-    const unsigned spine_grid = static_cast<unsigned>((S * kRadix + kWaves - 1) / kWaves);
     const int passes = (key_bits + kRadixBits - 1) / kRadixBits;
     const int Si = static_cast<int>(S);
     uint32_t* kin = b.keys_a;
@@ -221,19 +206,28 @@ hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles, int key_bi
     uint32_t* kout = b.keys_b;
     uint32_t* vout = b.vals_b;
     for (int p = 0; p < passes; ++p) {
-        const int shift = p * kRadixBits;
-        if (p > 0) upsweep_kernel<<<grid, kBlock, 0, stream>>>(segs, Si, kin, shift, b.hist, b.dpre);
-        spine_kernel<<<spine_grid, kBlock, 0, stream>>>(segs, Si, b.hist, b.dpre);
+        SortPass pass;
+        pass.keys_in = kin;
+        pass.vals_in = vin;
+        pass.keys_out = kout;
+        pass.vals_out = vout;
+        pass.idx_out = order;
+        pass.hist = b.hist + static_cast<int64_t>(p) * S * kRadix;
+        pass.status = b.status + static_cast<int64_t>(p) * tiles * kRadix;
+        pass.ticket = b.tickets + p;
+        pass.abort = b.tickets + kMaxSortPasses;
+        pass.shift = p * kRadixBits;
         const bool first = p == 0;
         const bool last = p == passes - 1;
+        if (last) pass.keys_out = sorted_keys;
         if (first && last) {
-            scatter_kernel<true, true><<<grid, kBlock, 0, stream>>>(segs, Si, kin, vin, kout, vout, order, b.hist, shift);
+            onesweep_kernel<true, true><<<grid, kBlock, 0, stream>>>(segs, Si, tiles, pass);
         } else if (first) {
-            scatter_kernel<true, false><<<grid, kBlock, 0, stream>>>(segs, Si, kin, vin, kout, vout, order, b.hist, shift);
+            onesweep_kernel<true, false><<<grid, kBlock, 0, stream>>>(segs, Si, tiles, pass);
         } else if (last) {
-            scatter_kernel<false, true><<<grid, kBlock, 0, stream>>>(segs, Si, kin, vin, kout, vout, order, b.hist, shift);
+            onesweep_kernel<false, true><<<grid, kBlock, 0, stream>>>(segs, Si, tiles, pass);
         } else {
-            scatter_kernel<false, false><<<grid, kBlock, 0, stream>>>(segs, Si, kin, vin, kout, vout, order, b.hist, shift);
+            onesweep_kernel<false, false><<<grid, kBlock, 0, stream>>>(segs, Si, tiles, pass);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -74,43 +74,85 @@ __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* sc
 // Launchers (host).  Every launcher enqueues on `stream` and returns the
 // launch status.
 // ---------------------------------------------------------------------------
-// Planning: fill the segment table.
-hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream);
-hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
-                               int64_t* node_offsets, hipStream_t stream);
+constexpr int kMaxSortPasses = 4;   // 32-bit keys, 8-bit digits
 
-// Bounds: per-tile partials, then per-segment reduction into scene_min/max.
-hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
-                         int64_t tiles_bound, float* partials,
-                         float* scene_min, float* scene_max, hipStream_t stream);
-
-// Morton codes of every row against its segment's bounds, plus the digit-0
-// tile histograms of the first sort pass.
-hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
-                         int64_t tiles_bound, const float* scene_min, const float* scene_max,
-                         uint32_t* keys, uint32_t* hist, uint32_t* dpre, hipStream_t stream);
-
-// Stable LSD sort of (key, local index) per segment; writes int64 local
-// indices in key order into `order`.  `keys` is clobbered.
+// Sort scratch: ping-pong keys/values, per-pass digit histograms of every
+// segment ([pass][segment][digit]), per-pass look-back status words
+// ([pass][tile][digit]), per-pass tile tickets plus one abort word.
 struct SortBuffers {
     uint32_t* keys_a;   // input keys (Morton kernel output)
     uint32_t* keys_b;
     uint32_t* vals_a;
     uint32_t* vals_b;
-    uint32_t* hist;     // kRadix * tiles_bound words
-    uint32_t* dpre;     // kRadix * tiles_bound words
+    uint32_t* hist;     // kMaxSortPasses * S * kRadix words
+    uint32_t* status;   // kMaxSortPasses * tiles_bound * kRadix words
+    uint32_t* tickets;  // kMaxSortPasses + 1 words
+    uint32_t* seg_done; // S words: bounds tiles finished per segment
 };
-hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles_bound, int key_bits,
-                       const SortBuffers& buf, int64_t* order, hipStream_t stream);
 
-// Implicit-tree node AABBs (all passes) and traversal arrays.
-// `max_n` bounds the largest cloud (it decides how many passes run).
+// One onesweep pass (device-side view).
+struct SortPass {
+    const uint32_t* keys_in;
+    const uint32_t* vals_in;
+    uint32_t* keys_out;
+    uint32_t* vals_out;
+    int64_t* idx_out;
+    const uint32_t* hist;   // this pass: [segment][digit]
+    uint32_t* status;       // this pass: [tile][digit]
+    uint32_t* ticket;
+    uint32_t* abort;
+    int shift;
+};
+
+// Words the planning kernel clears: histograms, status words, tickets and
+// the bounds counters, contiguous from `hist` in that order.
+inline int64_t sort_clear_words(int64_t S, int64_t tiles) {
+    return static_cast<int64_t>(kMaxSortPasses) * S * kRadix +
+           static_cast<int64_t>(kMaxSortPasses) * tiles * kRadix + kMaxSortPasses + 1 + S;
+}
+
+// Planning: fill the segment table and clear `clear_words` words at `clear`.
+hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, uint32_t* clear,
+                               int64_t clear_words, hipStream_t stream);
+hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
+                               int64_t* node_offsets, uint32_t* clear, int64_t clear_words,
+                               hipStream_t stream);
+
+// Per-cloud bounds: one work-group per tile writes a partial box; the last
+// tile of a cloud to finish (counted in `seg_done`, zeroed beforehand)
+// reduces the cloud's partials into scene_min/max.
+hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
+                         int64_t tiles_bound, float* partials, uint32_t* seg_done,
+                         float* scene_min, float* scene_max, hipStream_t stream);
+
+// Morton codes of every row against its segment's bounds, plus every sort
+// pass's per-segment digit histogram (`hist`, zeroed beforehand).
+hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
+                         int64_t tiles_bound, const float* scene_min, const float* scene_max,
+                         uint32_t* keys, uint32_t* hist, hipStream_t stream);
+
+// Stable LSD sort of (key, local index) per segment; writes int64 local
+// indices in key order into `order` and, if `sorted_keys` is non-null, the
+// keys in that order.  Input keys are in buf.keys_a (clobbered).
+hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles_bound, int key_bits,
+                       const SortBuffers& buf, int64_t* order, uint32_t* sorted_keys,
+                       hipStream_t stream);
+
+// Extra outputs of the implicit-tree passes.
+struct TreeOutputs {
+    int32_t* left;         // traversal arrays (null: not written)
+    int32_t* right;
+    int32_t* leaf;
+    bool arrays_packed;    // ragged: per-segment arrays at node_start; batched: segment 0 only
+    float4* accel_points;  // Morton-ordered float4 points for the accel (null: not written)
+};
+
+// Implicit-tree node AABBs (all passes), optionally the traversal arrays and
+// the accel's points.  `max_n` bounds the largest cloud (it decides how
+// many passes run).
 hipError_t launch_tree(const float* points, int D, const Segment* segs, int64_t S,
                        int64_t total, int64_t max_n, const int64_t* sorted, float* node_aabbs,
-                       hipStream_t stream);
-hipError_t launch_traversal_arrays(const Segment* segs, int64_t S, int64_t total_nodes,
-                                   int32_t* left, int32_t* right, int32_t* leaf,
-                                   hipStream_t stream);
+                       const TreeOutputs& out, hipStream_t stream);
 
 // k-NN acceleration structure (radix tree + Morton-ordered float4 points).
 constexpr int kAccelBucket = 4;                       // max points per leaf bucket
@@ -119,11 +161,15 @@ __host__ __device__ inline size_t accel_points_bytes(int64_t total) {
     return (static_cast<size_t>(total) * 16 + 255) / 256 * 256;
 }
 size_t accel_bytes(int64_t total, int64_t S, int D);
-// `codes` is scratch for `total` u32 Morton codes.
-hipError_t launch_accel_build(const float* points, const int64_t* sorted, const float* node_aabbs,
-                              const float* scene_min, const float* scene_max, int D,
-                              const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
-                              void* accel, hipStream_t stream);
+// Accel points + codes from a finished BVH (`codes`: scratch for `total`
+// u32), then the radix-tree records.
+hipError_t launch_accel_points(const float* points, const int64_t* sorted, const float* scene_min,
+                               const float* scene_max, int D, const Segment* segs, int64_t S,
+                               int64_t total, uint32_t* codes, void* accel, hipStream_t stream);
+// Radix-tree records from Morton-sorted codes and the implicit tree.
+hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* segs, int64_t S,
+                              int64_t total, const uint32_t* sorted_codes, void* accel,
+                              hipStream_t stream);
 
 // k-NN traversal.
 struct KnnArgs {
