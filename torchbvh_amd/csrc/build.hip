@@ -195,16 +195,45 @@ __global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict_
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
 
+    // The tile's count*D floats are contiguous: thread t loads floats
+    // t, t + kBlock, ... (coalesced, all loads in flight at once).  Float f
+    // is component f % D; with kBlock = 256 the component of load i is
+    // (i * kBlock + t) % D, so accumulator a = (i * kBlock) % D is fixed at
+    // compile time and maps to component (a + t) % D.
+    constexpr int kF = kSortTile * D / kBlock;
+    const int nf = count * D;
+    const float* base = points + row0 * D;
+    float acc_lo[D], acc_hi[D];
+#pragma unroll
+    for (int a = 0; a < D; ++a) { acc_lo[a] = kSeedLo; acc_hi[a] = kSeedHi; }
+    float v[kF];
+#pragma unroll
+    for (int i = 0; i < kF; ++i) {
+        const int f = i * kBlock + threadIdx.x;
+        v[i] = f < nf ? base[f] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kF; ++i) {
+        const int f = i * kBlock + threadIdx.x;
+        constexpr int kStep = kBlock % D;
+        const int a = (i * kStep) % D;
+        if (f < nf) {
+            acc_lo[a] = fminf(acc_lo[a], v[i]);
+            acc_hi[a] = fmaxf(acc_hi[a], v[i]);
+        }
+    }
     float lo[D], hi[D];
+    const int r = threadIdx.x % D;
 #pragma unroll
-    for (int d = 0; d < D; ++d) { lo[d] = kSeedLo; hi[d] = kSeedHi; }
-    for (int j = threadIdx.x; j < count; j += kBlock) {
-        const float* p = points + (row0 + j) * D;
+    for (int c = 0; c < D; ++c) {
+        // accumulator holding component c: a with (a + r) % D == c
+        const int want = (c - r + D) % D;
+        lo[c] = acc_lo[0];
+        hi[c] = acc_hi[0];
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const float v = p[d];
-            lo[d] = fminf(lo[d], v);
-            hi[d] = fmaxf(hi[d], v);
+        for (int a = 1; a < D; ++a) {
+            lo[c] = want == a ? acc_lo[a] : lo[c];
+            hi[c] = want == a ? acc_hi[a] : hi[c];
         }
     }
     block_box<D>(lo, hi, s_red, s_out);
@@ -258,6 +287,7 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
                                                         uint32_t* __restrict__ hist) {
     __shared__ int s_seg;
     __shared__ uint32_t s_hist[kMaxSortPasses][kRadix];
+    __shared__ float s_pts[kSortTile * D];
     const int64_t t = blockIdx.x;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
                                      S, t, &s_seg);
@@ -267,6 +297,18 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
     for (int i = threadIdx.x; i < kMaxSortPasses * kRadix; i += kBlock) (&s_hist[0][0])[i] = 0u;
+    // Stage the tile's points in LDS with coalesced loads.
+    constexpr int kF = kSortTile * D / kBlock;
+    const int nf = count * D;
+    const float* base = points + row0 * D;
+    float v[kF];
+#pragma unroll
+    for (int i = 0; i < kF; ++i) {
+        const int f = i * kBlock + threadIdx.x;
+        v[i] = f < nf ? base[f] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kF; ++i) s_pts[i * kBlock + threadIdx.x] = v[i];
     float lo[D], hi[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -278,7 +320,7 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
     for (int j = threadIdx.x; j < count; j += kBlock) {
         float p[D];
 #pragma unroll
-        for (int d = 0; d < D; ++d) p[d] = points[(row0 + j) * D + d];
+        for (int d = 0; d < D; ++d) p[d] = s_pts[j * D + d];
         const uint32_t code = morton::encode<D>(p, lo, hi);
         keys[row0 + j] = code;
 #pragma unroll

@@ -49,8 +49,9 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Exclusive prefix sum of one value per thread over a kBlock-thread group.
-// `scratch` must hold kBlock / kWave words.  Contains __syncthreads().
+// Exclusive prefix sum of one value per thread over a kThreads-thread group.
+// `scratch` must hold kThreads / kWave words.  Contains __syncthreads().
+template <int kThreads = kBlock>
 __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* scratch,
                                                         uint32_t* total = nullptr) {
     const int lane = lane_id();
@@ -60,7 +61,7 @@ __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* sc
     __syncthreads();
     uint32_t before = 0, all = 0;
 #pragma unroll
-    for (int w = 0; w < kBlock / kWave; ++w) {
+    for (int w = 0; w < kThreads / kWave; ++w) {
         const uint32_t t = scratch[w];
         before += (w < wave) ? t : 0u;
         all += t;
