@@ -112,6 +112,33 @@ def test_knn_ties_take_lowest_indices(dim, k):
 
 
 @pytest.mark.parametrize("dim", [2, 3])
+def test_knn_ties_take_lowest_indices_k32(dim):
+    """K = 32 (the buffered-merge traversal): 16 copies of each unit
+    direction, all at distance 1 from the origin, plus farther points."""
+    eye = np.eye(dim, dtype=np.float32)
+    dirs = np.concatenate([np.stack((eye[d], -eye[d])) for d in range(dim)])
+    p = np.concatenate((np.repeat(dirs, 16, axis=0), 3.0 * dirs, 5.0 * dirs)).astype(np.float32)
+    q = np.zeros((3, dim), np.float32)
+    check_single(p, q, 32)
+    idx, dist = tb.query_knn(tb.build_bvh(dev(p)), dev(q), 32)
+    assert torch.all(dist == 1.0)
+    assert torch.equal(idx.cpu(), torch.arange(32).repeat(3, 1))
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_batched_knn_k32_matches_oracle(dim):
+    rng = np.random.default_rng(13150 + dim)
+    p = rng.random((4, 3000, dim), dtype=np.float32)
+    p[1, :1000] = p[1, 1000:2000]  # exact duplicates: ties by index
+    q = rng.random((4, 700, dim), dtype=np.float32)
+    idx, dist = tb.query_knn(tb.build_bvh(dev(p)), dev(q), 32)
+    for b in range(4):
+        ei, ed = oracle.knn(p[b], q[b], 32)
+        assert_same_int(idx[b].cpu().numpy(), ei, f"batch {b} indices")
+        assert_same_f32(dist[b].cpu().numpy(), ed, f"batch {b} distances")
+
+
+@pytest.mark.parametrize("dim", [2, 3])
 @pytest.mark.parametrize("k", [4, 8, 16, 32])
 def test_knn_robust_matrix(dim, k):
     """tests/test_knn.py:327-356: random points, a tie block, duplicates and
@@ -206,7 +233,7 @@ def test_ragged_knn_matches_oracle(dim, k):
 
 
 @pytest.mark.parametrize("dim", [2, 3])
-@pytest.mark.parametrize("k", [4, 8, 16])
+@pytest.mark.parametrize("k", [4, 8, 16, 32])
 def test_ragged_ties_take_lowest_local_indices(dim, k):
     eye = np.eye(dim, dtype=np.float32)
     dirs = np.concatenate([np.stack((eye[d], -eye[d])) for d in range(dim)])
