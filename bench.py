@@ -21,6 +21,7 @@ import os
 import platform
 import sys
 import time
+from pathlib import Path
 
 import torch
 
@@ -119,6 +120,22 @@ def knn_bytes(q: int, D: int, k: int) -> int:
 
 
 HBM_PEAK_GBS = 8000.0
+PROFILES = Path(__file__).resolve().parent / "profiles"
+
+
+def measured_traffic(config: str):
+    """HBM bytes per traversal launch measured by rocprofv3 (FETCH_SIZE and
+    WRITE_SIZE, each scaled by the same counter's reading for a copy of
+    known size), as recorded in profiles/knn_accel_<config>_counters.md on
+    the line ``traffic_bytes_per_launch: <bytes>``; None when absent."""
+    path = PROFILES / f"knn_accel_{config}_counters.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -168,10 +185,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-sample", type=int, default=1024)
+    ap.add_argument("--cpu-sample", type=int, default=3072)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--implicit-reps", type=int, default=1,
                     help="also time the traversal over the implicit tree (0 = skip)")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="end with a 256 MiB device copy (for rocprofv3 counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -206,7 +225,14 @@ def main() -> int:
     s_bytes = qsort_bytes(total_q, D)
     n_bytes = knn_bytes(total_q, D, k)
 
+    from torchbvh_amd._native import _C
+
     def step(events=None):
+        """One pass of the hot path: build (BVH + accel), query ordering,
+        traversal.  Single and batched clouds call the native ops in the
+        order ``tb.query_knn`` does, with an event between each phase (all
+        on torch's current stream, the stream the kernels are launched on);
+        ragged input goes through the public API (one event pair)."""
         if events:
             events[0].record()
         if kind == "ragged":
@@ -217,17 +243,30 @@ def main() -> int:
             events[1].record()
         if kind == "ragged":
             out = tb.query_knn(bvh, qs, k, query_offsets=qoff)
+            if events:
+                events[2].record()
         else:
-            out = tb.query_knn(bvh, qs, k)
+            one = kind == "single"
+            qb = qs.unsqueeze(0) if one else qs
+            smin = bvh["scene_min"].unsqueeze(0) if one else bvh["scene_min"]
+            smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
+            nodes = bvh["node_aabbs"].unsqueeze(0) if one else bvh["node_aabbs"]
+            sidx = bvh["sorted_indices"].unsqueeze(0) if one else bvh["sorted_indices"]
+            order = _C.morton_sort_queries_narrow(qb, smin, smax)
+            if events:
+                events[2].record()
+            out = _C.query_knn_batched_cached_bounds_ordered(
+                nodes, sidx, qb, order, bvh["num_leaves"], bvh["num_real_nodes"], D, k,
+                accel=bvh._aux["accel"])
         if events:
-            events[2].record()
+            events[3].record()
         return bvh, out
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -236,49 +275,47 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
     build_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    query_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    query_ms = sum(e[1].elapsed_time(e[3]) for e in evs) / args.steps
+    if kind == "ragged":
+        sort_ms = None
+        trav_ms = sum(e[1].elapsed_time(e[3]) for e in evs) / args.steps
+    else:
+        sort_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+        trav_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
 
-    # Split the query phase into ordering and traversal with events around the
-    # native calls on the current stream (the traversal is a single kernel).
-    from torchbvh_amd._native import _C
-
-    sort_ms = trav_ms = implicit_ms = 0.0
-    if kind != "ragged":
+    implicit_ms = None
+    if kind != "ragged" and args.implicit_reps > 0:
+        # The same query over the reference's implicit tree, for comparison
+        # (outside the timed region).
         bvh, _ = step()
-        data = bvh
-        qb = qs if kind == "batched" else qs.unsqueeze(0)
-        smin = data["scene_min"] if kind == "batched" else data["scene_min"].unsqueeze(0)
-        smax = data["scene_max"] if kind == "batched" else data["scene_max"].unsqueeze(0)
-        nodes = data["node_aabbs"] if kind == "batched" else data["node_aabbs"].unsqueeze(0)
-        sidx = data["sorted_indices"] if kind == "batched" else data["sorted_indices"].unsqueeze(0)
-        accel = bvh._aux["accel"]
-        reps = max(args.steps, 5)
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(3 * reps)]
-        torch.cuda.synchronize()
-        for r in range(reps):
-            e[3 * r].record()
-            order = _C.morton_sort_queries_narrow(qb, smin, smax)
-            e[3 * r + 1].record()
+        one = kind == "single"
+        qb = qs.unsqueeze(0) if one else qs
+        smin = bvh["scene_min"].unsqueeze(0) if one else bvh["scene_min"]
+        smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
+        nodes = bvh["node_aabbs"].unsqueeze(0) if one else bvh["node_aabbs"]
+        sidx = bvh["sorted_indices"].unsqueeze(0) if one else bvh["sorted_indices"]
+        order = _C.morton_sort_queries_narrow(qb, smin, smax)
+        ei = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ei[0].record()
+        for _ in range(args.implicit_reps):
             _C.query_knn_batched_cached_bounds_ordered(
-                nodes, sidx, qb, order, data["num_leaves"], data["num_real_nodes"], D, k,
-                accel=accel)
-            e[3 * r + 2].record()
+                nodes, sidx, qb, order, bvh["num_leaves"], bvh["num_real_nodes"], D, k)
+        ei[1].record()
         torch.cuda.synchronize()
-        sort_ms = sum(e[3 * r].elapsed_time(e[3 * r + 1]) for r in range(reps)) / reps
-        trav_ms = sum(e[3 * r + 1].elapsed_time(e[3 * r + 2]) for r in range(reps)) / reps
-        if args.implicit_reps > 0:
-            # The same query over the reference's implicit tree, for comparison.
-            ei = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-            ei[0].record()
-            for _ in range(args.implicit_reps):
-                _C.query_knn_batched_cached_bounds_ordered(
-                    nodes, sidx, qb, order, data["num_leaves"], data["num_real_nodes"], D, k)
-            ei[1].record()
-            torch.cuda.synchronize()
-            implicit_ms = ei[0].elapsed_time(ei[1]) / args.implicit_reps
+        implicit_ms = ei[0].elapsed_time(ei[1]) / args.implicit_reps
+
+    if args.calibration_copy:
+        # A plain device copy of known size, for scaling rocprofv3's
+        # FETCH_SIZE / WRITE_SIZE counters (not part of the measurement).
+        src = torch.ones(64 * 1024 * 1024, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     value = total_q / (ms_per_step * 1e-3)
     trav_gbs = n_bytes / (trav_ms * 1e-3) / 1e9 if trav_ms > 0 else None
+    traffic = measured_traffic(args.config)
     line = {
         "metric": "k-NN queries/sec + BVH build ms, 1M pts/1M queries k=16 3D fp32, 1 GPU",
         "value": value,
@@ -304,11 +341,11 @@ def main() -> int:
         "query_ms": query_ms,
         "query_sort_ms": sort_ms,
         "traversal_ms": trav_ms,
-        "traversal_implicit_tree_ms": implicit_ms or None,
+        "traversal_implicit_tree_ms": implicit_ms,
         "queries_per_s_excl_build": total_q / (query_ms * 1e-3) if query_ms > 0 else None,
         "build_hbm_frac_algorithmic": (b_bytes / (build_ms * 1e-3) / 1e9) / HBM_PEAK_GBS,
         "query_sort_hbm_frac_algorithmic": ((s_bytes / (sort_ms * 1e-3) / 1e9) / HBM_PEAK_GBS
-                                            if sort_ms > 0 else None),
+                                            if sort_ms else None),
         "roofline": {
             "bound": "hbm",
             "kernel": "knn_accel_kernel (traversal)",
@@ -316,7 +353,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": (trav_gbs / HBM_PEAK_GBS) if trav_gbs else None,
-            "traffic": None,
+            "traffic": traffic,
         },
     }
     if not args.no_cpu_baseline:
