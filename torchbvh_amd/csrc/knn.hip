@@ -167,179 +167,79 @@ __device__ __forceinline__ float point_distance(const float* q, const float4 p) 
 
 constexpr int kAccelStackDepth = 64;   // radix-tree depth <= 64 (64-bit keys)
 constexpr int kAccelBlock = 256;
+constexpr int kLdsStack = 12;          // first stack entries kept in LDS per lane
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
-constexpr uint64_t kEmptyKey = (static_cast<uint64_t>(0x7f7fffffu) << 32) | 0xffffffffu;  // (FLT_MAX, -1)
 
-// Compare-exchange of two candidate keys into ascending order.
-__device__ __forceinline__ void cas(uint64_t& x, uint64_t& y) {
-    const bool swap = y < x;
-    const uint64_t lo = swap ? y : x;
-    y = swap ? x : y;
-    x = lo;
-}
-
-// Comparator lists of sorting networks, built at compile time so the
-// unrolled loops below index register arrays with constants.
-template <int N>
-struct Network {
-    int count = 0;
-    int a[N * N] = {};
-    int b[N * N] = {};
-};
-
-// Batcher's odd-even merge sort for N = 2^m inputs.
-template <int N>
-constexpr Network<N> odd_even_merge_sort() {
-    Network<N> net;
-    for (int p = 1; p < N; p <<= 1) {
-        for (int k = p; k >= 1; k >>= 1) {
-            for (int j = k % p; j + k < N; j += 2 * k) {
-                for (int i = 0; i < k && i + j + k < N; ++i) {
-                    if ((i + j) / (2 * p) == (i + j + k) / (2 * p)) {
-                        net.a[net.count] = i + j;
-                        net.b[net.count] = i + j + k;
-                        ++net.count;
-                    }
-                }
-            }
-        }
-    }
-    return net;
-}
-
-// Bitonic merge: sorts a bitonic sequence of N = 2^m keys ascending.
-template <int N>
-constexpr Network<N> bitonic_merge() {
-    Network<N> net;
-    for (int j = N / 2; j >= 1; j >>= 1) {
-        for (int i = 0; i < N; ++i) {
-            if ((i ^ j) > i) {
-                net.a[net.count] = i;
-                net.b[net.count] = i ^ j;
-                ++net.count;
-            }
-        }
-    }
-    return net;
-}
-
-template <int N>
-struct SortNet { static constexpr Network<N> net = odd_even_merge_sort<N>(); };
-template <int N>
-struct MergeNet { static constexpr Network<N> net = bitonic_merge<N>(); };
-
-// Candidate buffering.  Accepting a candidate into the sorted K-list costs
-// O(K) selects, and with one query per lane the wave pays for it whenever
-// any lane inserts.  Lanes can instead append accepted candidates to a
-// private LDS buffer of `cap` keys; once any lane holds >= `threshold` (so
-// the next bucket still fits), every lane merges its buffer in one
-// branch-free pass: sort the buffer, take the elementwise minimum against
-// the reversed list (the K smallest of both, as a bitonic sequence),
-// bitonic-merge.  The list's k-th key stays a valid (if looser) pruning
-// bound meanwhile, so results are unchanged.  Measured on MI355X, this pays
-// off at K = 32 (-18% traversal time on the ragged torus workload) and not
-// at K <= 16, where the extra registers and LDS cost more occupancy than the
-// merges save; the LDS stack is shortened to 4 entries to make room.
-template <int K>
-struct Tuning {
-    static constexpr bool buffered = K >= 32;
-    static constexpr int cap = 16;
-    static constexpr int threshold = cap - kAccelBucket + 1;
-    // Top stack entries kept in LDS per lane (12 measured best for k <= 16:
-    // 16, 20 or 24 entries cost more occupancy than the spills they save).
-    static constexpr int lds_stack = buffered ? 4 : 12;
-};
-
-template <int K, int kCap>
-__device__ __forceinline__ void merge_buffer(uint64_t (&best)[K], const uint64_t* col, int nb) {
-    uint64_t b[kCap];
-#pragma unroll
-    for (int j = 0; j < kCap; ++j) {
-        const uint64_t v = col[j * kAccelBlock];
-        b[j] = j < nb ? v : kEmptyKey;
-    }
-    constexpr Network<kCap> sort_net = SortNet<kCap>::net;
-#pragma unroll
-    for (int c = 0; c < sort_net.count; ++c) cas(b[sort_net.a[c]], b[sort_net.b[c]]);
-    constexpr int M = kCap < K ? kCap : K;
-#pragma unroll
-    for (int i = K - M; i < K; ++i) best[i] = b[K - 1 - i] < best[i] ? b[K - 1 - i] : best[i];
-    constexpr Network<K> merge_net = MergeNet<K>::net;
-#pragma unroll
-    for (int c = 0; c < merge_net.count; ++c) cas(best[merge_net.a[c]], best[merge_net.b[c]]);
-}
-
-// Deferred-node stack of one lane: the first `kLds` entries live in an LDS
-// column (stride kAccelBlock), deeper ones in scratch.
-template <int kLds>
+// Deferred-node stack of one lane: the first kLdsStack entries live in an
+// LDS column (stride kAccelBlock), deeper ones in scratch.  12 LDS entries
+// measured best: 16, 20 or 24 remove the scratch traffic but cost more
+// occupancy than they save.
 struct NodeStack {
     uint64_t* col;
-    uint64_t spill[kAccelStackDepth - kLds];
+    uint64_t spill[kAccelStackDepth - kLdsStack];
     int sp = 0;
     __device__ __forceinline__ void push(float d, int32_t ref) {
-        if (sp >= kAccelStackDepth) return;  // unreachable: radix-tree depth <= 64
         const uint64_t e = (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<uint32_t>(ref);
-        if (sp < kLds) col[sp * kAccelBlock] = e;
-        else spill[sp - kLds] = e;
+        if (sp < kLdsStack) col[sp * kAccelBlock] = e;
+        else spill[sp - kLdsStack] = e;
         ++sp;
     }
     __device__ __forceinline__ void pop(float& d, int32_t& ref) {
         --sp;
-        const uint64_t e = sp < kLds ? col[sp * kAccelBlock] : spill[sp - kLds];
+        const uint64_t e = sp < kLdsStack ? col[sp * kAccelBlock] : spill[sp - kLdsStack];
         ref = static_cast<int32_t>(static_cast<uint32_t>(e));
         d = __uint_as_float(static_cast<uint32_t>(e >> 32));
     }
 };
 
-// Loads a bucket's <= kAccelBucket Morton-ordered points together.
-__device__ __forceinline__ void load_bucket(const float4* pts, int32_t ref, int n, float4 (&p)[kAccelBucket],
-                                            int& count) {
+// Brute-forces one bucket (<= kAccelBucket consecutive Morton-ordered
+// points, loaded together) into the candidate list.
+template <int D, int K>
+__device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int n, const float* q,
+                                            uint64_t (&best)[K]) {
     const int first = ref & 0x0fffffff;
-    count = ((ref >> 28) & 7) + 1;
-    if (first + count > n) count = 0;  // a corrupt ref never reads outside the cloud
+    const int count = ((ref >> 28) & 7) + 1;
+    if (first + count > n) return;  // a corrupt ref never reads outside the cloud
+    float4 p[kAccelBucket];
 #pragma unroll
     for (int j = 0; j < kAccelBucket; ++j) {
         p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-}
-
-// Internal record: near-first order, the far child deferred with its
-// distance if it can still hold a candidate.  Returns true (and the near
-// child in ref/nd) when the traversal descends.
-template <int D, int kLds>
-__device__ __forceinline__ bool visit_internal(const float* recs, const float* q, float worst, int32_t& ref,
-                                               float& nd, NodeStack<kLds>& stack) {
-    constexpr int R = 4 * D + 4;
-    const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
-    float rec[R];
 #pragma unroll
-    for (int v = 0; v < R / 4; ++v) {
-        const float4 x = r4[v];
-        rec[4 * v] = x.x;
-        rec[4 * v + 1] = x.y;
-        rec[4 * v + 2] = x.z;
-        rec[4 * v + 3] = x.w;
+    for (int j = 0; j < kAccelBucket; ++j) {
+        if (j < count) {
+            const float d = point_distance<D>(q, p[j]);
+            const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
+            if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+        }
     }
-    const float ld = box_distance<D>(q, rec);
-    const float rd = box_distance<D>(q, rec + 2 * D);
-    const int32_t lref = __float_as_int(rec[4 * D]);
-    const int32_t rref = __float_as_int(rec[4 * D + 1]);
-    const bool left_near = ld <= rd;
-    const float near_d = left_near ? ld : rd;
-    const float far_d = left_near ? rd : ld;
-    if (far_d <= worst) stack.push(far_d, left_near ? rref : lref);
-    if (near_d <= worst) {
-        ref = left_near ? lref : rref;
-        nd = near_d;
-        return true;
-    }
-    return false;
 }
 
-// Branch-and-bound over the acceleration structure (see accel.hip): same
-// pruning rule, near-first order and cached far-child distances as the
-// implicit-tree kernel above; a bucket ref brute-forces its <= kAccelBucket
-// consecutive points, loaded together.
+// Buckets a lane may park before it waits for the wave's next bucket round
+// (measured on MI355X: two for k <= 8, one for k >= 16).
+template <int K>
+struct Parking {
+    static constexpr int slots = K <= 8 ? 2 : 1;
+};
+
+// Branch-and-bound over the acceleration structure (see accel.hip): the
+// pruning rule, near-first order and cached far-child distances of the
+// implicit-tree kernel above; deferred nodes on a per-lane stack.
+//
+// Postponed buckets.  With one query per lane, the O(K) insertion into the
+// sorted list is the dominant cost, and the wave pays for it whenever any
+// lane inserts.  So a lane that reaches a bucket parks it and keeps
+// traversing; a lane that reaches a bucket with no free parking slot waits.
+// At the loop head, which every lane of the wave passes each iteration, the
+// wave scans all parked buckets together once at least half of its live
+// lanes hold one, or no lane can move: the insertions then run with most
+// lanes active.  Meanwhile a lane prunes with its list's current k-th
+// distance, a valid (looser) bound, and a waiting lane re-tests its bucket
+// after the round, so results are unchanged; the end result is the k
+// smallest (distance, index) pairs whatever the order of visits.  Measured
+// on MI355X against immediate insertion: -20% at k = 16 (cfg2), -13% at
+// k = 8 (cfg4); a variant that buffered candidates in LDS and merged them
+// with sorting networks was slower (fewer waves fit).
 //
 // Tile order: consecutive work-groups land on different XCDs, each with its
 // own L2; logical tile t = (block % 8) * (grid / 8) + block / 8 gives every
@@ -348,9 +248,8 @@ __device__ __forceinline__ bool visit_internal(const float* recs, const float* q
 template <int D, int K, bool kOrdered, bool kRagged>
 __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     constexpr int R = 4 * D + 4;
-    using Tune = Tuning<K>;
-    __shared__ uint64_t lds_stack[Tune::lds_stack * kAccelBlock];
-    __shared__ uint64_t lds_buf[(Tune::buffered ? Tune::cap : 1) * kAccelBlock];
+    constexpr int kSlots = Parking<K>::slots;
+    __shared__ uint64_t lds_stack[kLdsStack * kAccelBlock];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     const int64_t gid = tile * kAccelBlock + threadIdx.x;
@@ -386,114 +285,92 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
 
     uint64_t best[K];
 #pragma unroll
-    for (int i = 0; i < K; ++i) best[i] = kEmptyKey;
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
 
-    NodeStack<Tune::lds_stack> stack;
+    NodeStack stack;
     stack.col = lds_stack + threadIdx.x;
     int32_t ref = n <= kAccelBucket
                       ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
                       : 0;
     float nd = 0.0f;
+    int32_t parked[kSlots];  // bucket refs are negative, so 0 means a free slot
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) parked[s] = 0;
+    bool waiting = false;
+    bool done = false;
 
-    if constexpr (!Tune::buffered) {
-        // Immediate insertion.  Descents `continue` straight to the next
-        // node, which keeps consecutive descents in a tight inner loop (a
-        // flag-based loop of the same work measured 2x slower here).
-        while (true) {
-            const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
-            if (nd <= worst) {
-                if (ref < 0) {
-                    const int first = ref & 0x0fffffff;
-                    const int count = ((ref >> 28) & 7) + 1;
-                    if (first + count <= n) {
-                        float4 p[kAccelBucket];
+    // Descents `continue` straight to the loop head; this shape keeps them
+    // in a tight loop (a flag-driven single loop of the same work measured
+    // 2x slower).
+    while (true) {
+        const uint64_t holding = __ballot(parked[0] != 0);
+        if (holding != 0) {
+            const uint64_t live = __ballot(true);
+            const uint64_t movable = __ballot(!waiting && !done);
+            if (movable == 0 || __popcll(live) <= 2 * __popcll(holding)) {
 #pragma unroll
-                        for (int j = 0; j < kAccelBucket; ++j) {
-                            p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                        }
-#pragma unroll
-                        for (int j = 0; j < kAccelBucket; ++j) {
-                            if (j < count) {
-                                const float d = point_distance<D>(q, p[j]);
-                                const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
-                                if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
-                            }
-                        }
-                    }
-                } else if (ref < n - 1) {
-                    const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
-                    float rec[R];
-#pragma unroll
-                    for (int v = 0; v < R / 4; ++v) {
-                        const float4 x = r4[v];
-                        rec[4 * v] = x.x;
-                        rec[4 * v + 1] = x.y;
-                        rec[4 * v + 2] = x.z;
-                        rec[4 * v + 3] = x.w;
-                    }
-                    const float ld = box_distance<D>(q, rec);
-                    const float rd = box_distance<D>(q, rec + 2 * D);
-                    const int32_t lref = __float_as_int(rec[4 * D]);
-                    const int32_t rref = __float_as_int(rec[4 * D + 1]);
-                    const bool left_near = ld <= rd;
-                    const int32_t near_ref = left_near ? lref : rref;
-                    const int32_t far_ref = left_near ? rref : lref;
-                    const float near_d = left_near ? ld : rd;
-                    const float far_d = left_near ? rd : ld;
-                    if (far_d <= worst && stack.sp < kAccelStackDepth) stack.push(far_d, far_ref);
-                    if (near_d <= worst) {
-                        ref = near_ref;
-                        nd = near_d;
-                        continue;
-                    }
+                for (int s = 0; s < kSlots; ++s) {
+                    if (parked[s] != 0) scan_bucket<D>(pts, parked[s], n, q, best);
+                    parked[s] = 0;
                 }
+                waiting = false;
             }
-            if (stack.sp == 0) break;
-            stack.pop(nd, ref);
         }
-    } else {
-        // Buffered insertion; every lane stays in the loop until the whole
-        // wave is done, so a merge always runs on the full wave.
-        uint64_t* buf_col = lds_buf + threadIdx.x;
-        int nb = 0;
-        bool live = true;
-        while (true) {
-            if (live) {
-                const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
-                bool descend = false;
-                if (nd <= worst) {
-                    if (ref < 0) {
-                        float4 p[kAccelBucket];
-                        int count;
-                        load_bucket(pts, ref, n, p, count);
+        if (done) {
+            if (parked[0] == 0) break;
+            continue;
+        }
+        if (waiting) continue;
+        const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
+        if (nd <= worst) {
+            if (ref < 0) {
+                // Park in the first free slot (slots fill in order), else
+                // wait and revisit this bucket after the next round.
+                bool placed = false;
 #pragma unroll
-                        for (int j = 0; j < kAccelBucket; ++j) {
-                            if (j < count) {
-                                const float d = point_distance<D>(q, p[j]);
-                                const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
-                                if (d < kFar && key < best[K - 1]) {
-                                    buf_col[nb * kAccelBlock] = key;
-                                    ++nb;
-                                }
-                            }
-                        }
-                    } else if (ref < n - 1) {
-                        descend = visit_internal<D>(recs, q, worst, ref, nd, stack);
+                for (int s = 0; s < kSlots; ++s) {
+                    if (!placed && parked[s] == 0) {
+                        parked[s] = ref;
+                        placed = true;
                     }
                 }
-                if (!descend) {
-                    if (stack.sp == 0) live = false;
-                    else stack.pop(nd, ref);
+                if (!placed) {
+                    waiting = true;
+                    continue;
+                }
+            } else if (ref < n - 1) {
+                const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
+                float rec[R];
+#pragma unroll
+                for (int v = 0; v < R / 4; ++v) {
+                    const float4 x = r4[v];
+                    rec[4 * v] = x.x;
+                    rec[4 * v + 1] = x.y;
+                    rec[4 * v + 2] = x.z;
+                    rec[4 * v + 3] = x.w;
+                }
+                const float ld = box_distance<D>(q, rec);
+                const float rd = box_distance<D>(q, rec + 2 * D);
+                const int32_t lref = __float_as_int(rec[4 * D]);
+                const int32_t rref = __float_as_int(rec[4 * D + 1]);
+                const bool left_near = ld <= rd;
+                const int32_t near_ref = left_near ? lref : rref;
+                const int32_t far_ref = left_near ? rref : lref;
+                const float near_d = left_near ? ld : rd;
+                const float far_d = left_near ? rd : ld;
+                if (far_d <= worst && stack.sp < kAccelStackDepth) stack.push(far_d, far_ref);
+                if (near_d <= worst) {
+                    ref = near_ref;
+                    nd = near_d;
+                    continue;
                 }
             }
-            // Wave-uniform decisions: merge when any buffer could overflow on
-            // its next bucket or a finished lane still holds candidates.
-            if (__ballot(nb >= Tune::threshold || (!live && nb > 0)) != 0) {
-                merge_buffer<K, Tune::cap>(best, buf_col, nb);
-                nb = 0;
-            }
-            if (__ballot(live) == 0) break;
         }
+        if (stack.sp == 0) {
+            done = true;  // stays in the loop until its parked buckets are scanned
+            continue;
+        }
+        stack.pop(nd, ref);
     }
 
     int64_t* oi = a.out_indices + row * K;
