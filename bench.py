@@ -252,7 +252,7 @@ def main() -> int:
             smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
             nodes = bvh["node_aabbs"].unsqueeze(0) if one else bvh["node_aabbs"]
             sidx = bvh["sorted_indices"].unsqueeze(0) if one else bvh["sorted_indices"]
-            order = _C.morton_sort_queries_narrow(qb, smin, smax)
+            order = _C.morton_sort_queries_narrow(qb, smin, smax, schedule=True)
             if events:
                 events[2].record()
             out = _C.query_knn_batched_cached_bounds_ordered(
@@ -294,7 +294,7 @@ def main() -> int:
         smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
         nodes = bvh["node_aabbs"].unsqueeze(0) if one else bvh["node_aabbs"]
         sidx = bvh["sorted_indices"].unsqueeze(0) if one else bvh["sorted_indices"]
-        order = _C.morton_sort_queries_narrow(qb, smin, smax)
+        order = _C.morton_sort_queries_narrow(qb, smin, smax, schedule=True)
         ei = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         ei[0].record()
         for _ in range(args.implicit_reps):

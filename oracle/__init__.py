@@ -179,6 +179,16 @@ def query_order(queries, scene_min, scene_max) -> np.ndarray:
     return stable_argsort(morton_codes(queries, scene_min, scene_max))
 
 
+def schedule_order(queries, scene_min, scene_max) -> np.ndarray:
+    """Traversal schedule of this library's query_knn (no reference
+    counterpart; the reference uses query_order above): stable order by the
+    top 16 bits of the Morton code, ties by ascending query index."""
+    q = _f32(queries)
+    bits = 30 if q.shape[1] == 3 else 32
+    codes = morton_codes(q, scene_min, scene_max).astype(np.uint64)
+    return stable_argsort((codes >> np.uint64(bits - 16)).astype(np.uint32))
+
+
 def knn_brute(points, queries, k: int) -> tuple[np.ndarray, np.ndarray]:
     p = _f32(points)
     q = _f32(queries)

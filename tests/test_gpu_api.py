@@ -79,7 +79,8 @@ def test_sort_queries_routes_through_ordered_traversal(monkeypatch):
     bvh = tb.build_bvh(pts)
     calls = []
 
-    def fake_sort(qb, lo, hi):
+    def fake_sort(qb, lo, hi, schedule=False):
+        assert schedule  # query_knn orders its traversal with the schedule sort
         calls.append(("sort", tuple(qb.shape)))
         B, M, _ = qb.shape
         return torch.arange(M, device=qb.device).expand(B, M).contiguous()

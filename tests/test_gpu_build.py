@@ -133,6 +133,32 @@ def test_query_order_bit_exact(dim, m):
         assert_same_int(order[b], oracle.query_order(q[b], lo[b], hi[b]), f"order {b}")
 
 
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("m", [1, 100, 4097, 50_000])
+def test_schedule_order_bit_exact(dim, m):
+    rng = np.random.default_rng(7 * m + dim)
+    q = rng.random((2, m, dim), dtype=np.float32) * 1.2 - 0.1
+    lo = np.zeros((2, dim), np.float32)
+    hi = np.ones((2, dim), np.float32)
+    order = _C.morton_sort_queries_narrow(dev(q), dev(lo), dev(hi), schedule=True).cpu().numpy()
+    for b in range(2):
+        assert_same_int(order[b], oracle.schedule_order(q[b], lo[b], hi[b]), f"schedule {b}")
+
+
+def test_schedule_order_ragged_bit_exact():
+    rng = np.random.default_rng(77)
+    counts = [5, 0, 4097, 300]
+    q = rng.random((sum(counts), 3), dtype=np.float32)
+    offsets = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    lo = np.zeros((4, 3), np.float32)
+    hi = np.full((4, 3), 0.5, np.float32)
+    order = _C.morton_sort_queries_ragged(dev(q), dev(offsets), dev(lo), dev(hi), 4,
+                                          schedule=True).cpu().numpy()
+    for b, c in enumerate(counts):
+        seg = slice(offsets[b], offsets[b + 1])
+        assert_same_int(order[seg], oracle.schedule_order(q[seg], lo[b], hi[b]), f"cloud {b}")
+
+
 def test_build_is_deterministic_across_calls():
     rng = np.random.default_rng(5)
     p = dev(rng.random((50_000, 3), dtype=np.float32))

@@ -147,6 +147,23 @@ def test_stable_argsort_matches_numpy_stable():
         assert_same_int(oracle.stable_argsort(keys), np.argsort(keys, kind="stable"), "argsort")
 
 
+@pytest.mark.parametrize("dim", [2, 3])
+def test_schedule_order_is_stable_sort_on_top_16_code_bits(dim):
+    """The schedule is pinned by its definition through a plain Python sort
+    on (code >> (bits - 16), query index): a wrong shift, an unstable sort or
+    a full-code sort all fail it (the data has many equal top bits)."""
+    rng = np.random.default_rng(61 + dim)
+    q = rng.random((3000, dim), dtype=np.float32)
+    lo = np.zeros(dim, np.float32)
+    hi = np.ones(dim, np.float32)
+    codes = oracle.morton_codes(q, lo, hi).astype(np.int64)
+    shift = (30 if dim == 3 else 32) - 16
+    want = sorted(range(len(codes)), key=lambda i: (codes[i] >> shift, i))
+    got = oracle.schedule_order(q, lo, hi)
+    assert_same_int(got, np.array(want, np.int64), "schedule")
+    assert not np.array_equal(got, oracle.query_order(q, lo, hi))  # coarser than the full order
+
+
 def test_bounds_match_numpy_and_seed_semantics():
     rng = np.random.default_rng(9)
     p = rng.standard_normal((1000, 3)).astype(np.float32)

@@ -60,6 +60,8 @@ def _declare(L) -> None:
     L.tbvh_sort_queries_ragged.argtypes = (
         [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     )
+    L.tbvh_schedule_queries.argtypes = L.tbvh_sort_queries.argtypes
+    L.tbvh_schedule_queries_ragged.argtypes = L.tbvh_sort_queries_ragged.argtypes
     L.tbvh_morton_codes.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_knn.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
     L.tbvh_knn_ragged.argtypes = (
@@ -80,6 +82,7 @@ def _declare(L) -> None:
         "tbvh_build_ragged", "tbvh_build_with_accel", "tbvh_build_ragged_with_accel",
         "tbvh_sort_queries_workspace_size", "tbvh_sort_queries",
         "tbvh_sort_queries_ragged_workspace_size", "tbvh_sort_queries_ragged",
+        "tbvh_schedule_queries", "tbvh_schedule_queries_ragged",
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
         "tbvh_knn_accel", "tbvh_knn_accel_ragged",
@@ -338,7 +341,10 @@ class _NativeOps:
 
     @staticmethod
     def morton_sort_queries_narrow(queries: torch.Tensor, scene_min: torch.Tensor,
-                                   scene_max: torch.Tensor) -> torch.Tensor:
+                                   scene_max: torch.Tensor, *, schedule: bool = False) -> torch.Tensor:
+        """Stable Morton order of [B, M, D] queries against per-cloud bounds.
+        With ``schedule`` only the top 16 code bits are sorted (the
+        traversal schedule ``query_knn`` uses; results do not depend on it)."""
         op = "morton_sort_queries_narrow"
         _require_device_f32(op, queries, "queries")
         _require(scene_min.is_cuda and scene_max.is_cuda and scene_min.is_contiguous()
@@ -356,18 +362,18 @@ class _NativeOps:
         order = torch.empty((B, M), dtype=torch.int64, device=dev)
         if M == 0:
             return order
+        fn = L.tbvh_schedule_queries if schedule else L.tbvh_sort_queries
         with torch.cuda.device(dev):
             ws_bytes = _size(L.tbvh_sort_queries_workspace_size, B, M, D)
             ws = _workspace(ws_bytes, dev)
-            _check(L.tbvh_sort_queries(
-                _ptr(queries), B, M, D, _ptr(scene_min), _ptr(scene_max), _ptr(order),
-                _ptr(ws), ws.numel(), _stream(dev)))
+            _check(fn(_ptr(queries), B, M, D, _ptr(scene_min), _ptr(scene_max), _ptr(order),
+                      _ptr(ws), ws.numel(), _stream(dev)))
         return order
 
     @staticmethod
     def morton_sort_queries_ragged(queries: torch.Tensor, query_offsets: torch.Tensor,
                                    scene_min: torch.Tensor, scene_max: torch.Tensor,
-                                   batch_size: int) -> torch.Tensor:
+                                   batch_size: int, *, schedule: bool = False) -> torch.Tensor:
         op = "morton_sort_queries_ragged"
         _require_device_f32(op, queries, "queries")
         _require_device_i64(op, query_offsets, "query_offsets")
@@ -377,12 +383,12 @@ class _NativeOps:
         order = torch.empty(T, dtype=torch.int64, device=dev)
         if T == 0:
             return order
+        fn = L.tbvh_schedule_queries_ragged if schedule else L.tbvh_sort_queries_ragged
         with torch.cuda.device(dev):
             ws_bytes = _size(L.tbvh_sort_queries_ragged_workspace_size, batch_size, T, D)
             ws = _workspace(ws_bytes, dev)
-            _check(L.tbvh_sort_queries_ragged(
-                _ptr(queries), _ptr(query_offsets), batch_size, T, D, _ptr(scene_min),
-                _ptr(scene_max), _ptr(order), _ptr(ws), ws.numel(), _stream(dev)))
+            _check(fn(_ptr(queries), _ptr(query_offsets), batch_size, T, D, _ptr(scene_min),
+                      _ptr(scene_max), _ptr(order), _ptr(ws), ws.numel(), _stream(dev)))
         return order
 
     @staticmethod

@@ -174,7 +174,7 @@ def _query_knn_single(
     accel = bvh._aux.get("accel")
     if sort_queries:
         order = _C.morton_sort_queries_narrow(
-            queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0)
+            queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0), schedule=True
         )
         indices, distances = _C.query_knn_batched_cached_bounds_ordered(
             node_aabbs, sorted_indices, queries, order.contiguous(),
@@ -248,7 +248,8 @@ def _query_knn_batched(
     queries = _as_contiguous(query_points)
     accel = bvh._aux.get("accel")
     if sort_queries:
-        order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"])
+        order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"],
+                                              schedule=True)
         indices, distances = _C.query_knn_batched_cached_bounds_ordered(
             data["node_aabbs"], data["sorted_indices"], queries, order.contiguous(),
             data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
@@ -312,7 +313,8 @@ def _query_knn_ragged(
 
     packed = bvh._aux["packed"]
     order = _C.morton_sort_queries_ragged(
-        queries, query_offsets, packed["scene_min"], packed["scene_max"], data["batch_size"]
+        queries, query_offsets, packed["scene_min"], packed["scene_max"], data["batch_size"],
+        schedule=True,
     )
     indices, distances = _C.query_knn_ragged(
         packed["node_aabbs"], packed["sorted_indices"], data["batch_offsets"],

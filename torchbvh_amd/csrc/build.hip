@@ -275,7 +275,7 @@ __global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Morton codes + all sort passes' digit histograms
 // ---------------------------------------------------------------------------
-// One work-group per tile.  Digit counts of the four sort passes are gathered
+// One work-group per tile.  Digit counts of the sort passes are gathered
 // with LDS atomics, then added to the segment's global histograms with one
 // device atomic per non-zero bin.
 template <int D>
@@ -284,7 +284,8 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
                                                         const float* __restrict__ scene_min,
                                                         const float* __restrict__ scene_max,
                                                         uint32_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ hist) {
+                                                        uint32_t* __restrict__ hist,
+                                                        int first_bit, int passes) {
     __shared__ int s_seg;
     __shared__ uint32_t s_hist[kMaxSortPasses][kRadix];
     __shared__ float s_pts[kSortTile * D];
@@ -325,12 +326,13 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
         keys[row0 + j] = code;
 #pragma unroll
         for (int pass = 0; pass < kMaxSortPasses; ++pass) {
-            atomicAdd(&s_hist[pass][(code >> (pass * kRadixBits)) & (kRadix - 1)], 1u);
+            if (pass < passes) {
+                atomicAdd(&s_hist[pass][(code >> (first_bit + pass * kRadixBits)) & (kRadix - 1)], 1u);
+            }
         }
     }
     __syncthreads();
-#pragma unroll
-    for (int pass = 0; pass < kMaxSortPasses; ++pass) {
+    for (int pass = 0; pass < passes; ++pass) {
         const uint32_t c = s_hist[pass][threadIdx.x];
         if (c) atomicAdd(hist + (static_cast<int64_t>(pass) * S + s) * kRadix + threadIdx.x, c);
     }
@@ -483,13 +485,16 @@ hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_
 
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S, int64_t tiles,
                          const float* scene_min, const float* scene_max, uint32_t* keys,
-                         uint32_t* hist, hipStream_t stream) {
+                         uint32_t* hist, SortBits bits, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
+    const int passes = bits.passes();
     if (D == 3) {
-        morton_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist);
+        morton_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist,
+                                                      bits.first_bit, passes);
     } else {
-        morton_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist);
+        morton_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist,
+                                                      bits.first_bit, passes);
     }
     return hipGetLastError();
 }

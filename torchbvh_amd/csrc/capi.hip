@@ -120,6 +120,13 @@ int check_workspace(const char* op, void* ws, size_t have, size_t need) {
 bool supported_k(int k) { return k == 4 || k == 8 || k == 16 || k == 32; }
 
 
+int full_key_bits(int D) { return D == 3 ? 30 : 32; }
+
+// Digits of a full Morton sort, and of the traversal schedule (the top 16
+// code bits: two passes instead of four).
+SortBits full_sort(int D) { return SortBits{0, full_key_bits(D)}; }
+SortBits schedule_sort(int D) { return SortBits{full_key_bits(D) - 16, full_key_bits(D)}; }
+
 // Everything one build call launches, in order: plan (+ clear), bounds,
 // Morton (+ all pass histograms), four sort passes, implicit-tree passes
 // (+ traversal arrays, + accel points) and, when `accel` is given, the
@@ -152,13 +159,13 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
                            o.scene_max, stream)) != hipSuccess) {
         return e;
     }
+    const SortBits bits = full_sort(D);
     if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.hist,
-                           stream)) != hipSuccess) {
+                           bits, stream)) != hipSuccess) {
         return e;
     }
     uint32_t* sorted_keys = o.accel ? last_pass_keys(sb) : nullptr;
-    if ((e = launch_sort(segs, S, l.tiles, D == 3 ? 30 : 32, sb, o.sorted_indices, sorted_keys,
-                         stream)) != hipSuccess) {
+    if ((e = launch_sort(segs, S, l.tiles, bits, sb, o.sorted_indices, sorted_keys, stream)) != hipSuccess) {
         return e;
     }
     TreeOutputs to;
@@ -178,7 +185,8 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
 
 hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t S, int64_t m_uniform,
                           int64_t rows, int D, const float* scene_min, const float* scene_max,
-                          int64_t* order, uint32_t* codes_only, void* ws, hipStream_t stream) {
+                          SortBits bits, int64_t* order, uint32_t* codes_only, void* ws,
+                          hipStream_t stream) {
     const Layout l = make_layout(S, rows, D, false);
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l, S);
@@ -188,12 +196,12 @@ hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t 
                                                  stream);
     if (e != hipSuccess) return e;
     uint32_t* keys = codes_only ? codes_only : sb.keys_a;
-    if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys, sb.hist,
+    if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys, sb.hist, bits,
                            stream)) != hipSuccess) {
         return e;
     }
     if (codes_only) return hipSuccess;
-    return launch_sort(segs, S, l.tiles, D == 3 ? 30 : 32, sb, order, nullptr, stream);
+    return launch_sort(segs, S, l.tiles, bits, sb, order, nullptr, stream);
 }
 
 bool aligned(const void* p) { return reinterpret_cast<uintptr_t>(p) % kAlign == 0; }
@@ -349,7 +357,7 @@ int tbvh_sort_queries_workspace_size(int64_t B, int64_t M, int D, size_t* bytes)
 }
 
 static int sort_batched(const char* op, const float* queries, int64_t B, int64_t M, int D,
-                        const float* scene_min, const float* scene_max, int64_t* order,
+                        const float* scene_min, const float* scene_max, bool schedule, int64_t* order,
                         uint32_t* codes, void* workspace, size_t workspace_bytes, void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
@@ -361,8 +369,9 @@ static int sort_batched(const char* op, const float* queries, int64_t B, int64_t
     }
     const Layout l = make_layout(B, B * M, D, false);
     if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    TBVH_TRY(op, run_query_sort(queries, nullptr, B, M, B * M, D, scene_min, scene_max, order, codes,
-                                workspace, static_cast<hipStream_t>(stream_ptr)));
+    TBVH_TRY(op, run_query_sort(queries, nullptr, B, M, B * M, D, scene_min, scene_max,
+                                schedule ? schedule_sort(D) : full_sort(D), order, codes, workspace,
+                                static_cast<hipStream_t>(stream_ptr)));
     return ok();
 }
 
@@ -370,15 +379,23 @@ int tbvh_sort_queries(const float* queries, int64_t B, int64_t M, int D, const f
                       const float* scene_max, int64_t* order, void* workspace,
                       size_t workspace_bytes, void* stream_ptr) {
     if (!order && M > 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_sort_queries: null input or output pointer");
-    return sort_batched("tbvh_sort_queries", queries, B, M, D, scene_min, scene_max, order, nullptr,
-                        workspace, workspace_bytes, stream_ptr);
+    return sort_batched("tbvh_sort_queries", queries, B, M, D, scene_min, scene_max, false, order,
+                        nullptr, workspace, workspace_bytes, stream_ptr);
+}
+
+int tbvh_schedule_queries(const float* queries, int64_t B, int64_t M, int D, const float* scene_min,
+                          const float* scene_max, int64_t* order, void* workspace,
+                          size_t workspace_bytes, void* stream_ptr) {
+    if (!order && M > 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_schedule_queries: null input or output pointer");
+    return sort_batched("tbvh_schedule_queries", queries, B, M, D, scene_min, scene_max, true, order,
+                        nullptr, workspace, workspace_bytes, stream_ptr);
 }
 
 int tbvh_morton_codes(const float* rows, int64_t B, int64_t M, int D, const float* scene_min,
                       const float* scene_max, uint32_t* codes, void* workspace,
                       size_t workspace_bytes, void* stream_ptr) {
     if (!codes && M > 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "tbvh_morton_codes: null input or output pointer");
-    return sort_batched("tbvh_morton_codes", rows, B, M, D, scene_min, scene_max, nullptr, codes,
+    return sort_batched("tbvh_morton_codes", rows, B, M, D, scene_min, scene_max, false, nullptr, codes,
                         workspace, workspace_bytes, stream_ptr);
 }
 
@@ -392,11 +409,10 @@ int tbvh_sort_queries_ragged_workspace_size(int64_t B, int64_t total_q, int D, s
     return ok();
 }
 
-int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets, int64_t B,
-                             int64_t total_q, int D, const float* scene_min,
-                             const float* scene_max, int64_t* order, void* workspace,
-                             size_t workspace_bytes, void* stream_ptr) {
-    const char* op = "tbvh_sort_queries_ragged";
+static int sort_ragged(const char* op, const float* queries, const int64_t* query_offsets, int64_t B,
+                       int64_t total_q, int D, const float* scene_min, const float* scene_max,
+                       bool schedule, int64_t* order, void* workspace, size_t workspace_bytes,
+                       void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
     if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
     if (total_q > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
@@ -406,9 +422,26 @@ int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets,
     }
     const Layout l = make_layout(B, total_q, D, false);
     if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
-    TBVH_TRY(op, run_query_sort(queries, query_offsets, B, 0, total_q, D, scene_min, scene_max, order,
-                                nullptr, workspace, static_cast<hipStream_t>(stream_ptr)));
+    TBVH_TRY(op, run_query_sort(queries, query_offsets, B, 0, total_q, D, scene_min, scene_max,
+                                schedule ? schedule_sort(D) : full_sort(D), order, nullptr, workspace,
+                                static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets, int64_t B,
+                             int64_t total_q, int D, const float* scene_min,
+                             const float* scene_max, int64_t* order, void* workspace,
+                             size_t workspace_bytes, void* stream_ptr) {
+    return sort_ragged("tbvh_sort_queries_ragged", queries, query_offsets, B, total_q, D, scene_min,
+                       scene_max, false, order, workspace, workspace_bytes, stream_ptr);
+}
+
+int tbvh_schedule_queries_ragged(const float* queries, const int64_t* query_offsets, int64_t B,
+                                 int64_t total_q, int D, const float* scene_min,
+                                 const float* scene_max, int64_t* order, void* workspace,
+                                 size_t workspace_bytes, void* stream_ptr) {
+    return sort_ragged("tbvh_schedule_queries_ragged", queries, query_offsets, B, total_q, D,
+                       scene_min, scene_max, true, order, workspace, workspace_bytes, stream_ptr);
 }
 
 // ---------------------------------------------------------------------------

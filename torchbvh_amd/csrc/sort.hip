@@ -205,11 +205,11 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const Segment* __res
 
 }  // namespace
 
-hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles, int key_bits,
+hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles, SortBits bits,
                        const SortBuffers& b, int64_t* order, uint32_t* sorted_keys,
                        hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
-    const int passes = (key_bits + kRadixBits - 1) / kRadixBits;
+    const int passes = bits.passes();
     const int Si = static_cast<int>(S);
     uint32_t* kin = b.keys_a;
     uint32_t* vin = b.vals_a;
@@ -226,7 +226,7 @@ hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles, int key_bi
         pass.status = b.status + static_cast<int64_t>(p) * tiles * kRadix;
         pass.ticket = b.tickets + p;
         pass.abort = b.tickets + kMaxSortPasses;
-        pass.shift = p * kRadixBits;
+        pass.shift = bits.first_bit + p * kRadixBits;
         const bool first = p == 0;
         const bool last = p == passes - 1;
         if (last) pass.keys_out = sorted_keys;

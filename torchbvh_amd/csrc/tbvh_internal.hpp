@@ -126,16 +126,27 @@ hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_
                          int64_t tiles_bound, float* partials, uint32_t* seg_done,
                          float* scene_min, float* scene_max, hipStream_t stream);
 
-// Morton codes of every row against its segment's bounds, plus every sort
-// pass's per-segment digit histogram (`hist`, zeroed beforehand).
+// Digit range of a sort: 8-bit digits at bits first_bit, first_bit + 8, ...
+// below end_bit (so passes = ceil((end_bit - first_bit) / 8) <= 4).
+struct SortBits {
+    int first_bit;
+    int end_bit;
+    int passes() const { return (end_bit - first_bit + kRadixBits - 1) / kRadixBits; }
+};
+
+// Morton codes of every row against its segment's bounds, plus the
+// per-segment digit histogram of every pass of `bits` (`hist`, zeroed
+// beforehand).
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles_bound, const float* scene_min, const float* scene_max,
-                         uint32_t* keys, uint32_t* hist, hipStream_t stream);
+                         uint32_t* keys, uint32_t* hist, SortBits bits, hipStream_t stream);
 
-// Stable LSD sort of (key, local index) per segment; writes int64 local
-// indices in key order into `order` and, if `sorted_keys` is non-null, the
-// keys in that order.  Input keys are in buf.keys_a (clobbered).
-hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles_bound, int key_bits,
+// Stable LSD sort of (key, local index) per segment on the digits of
+// `bits`; writes int64 local indices in key order into `order` and, if
+// `sorted_keys` is non-null, the keys in that order (an even number of
+// passes leaves them in buf.keys_a).  Input keys are in buf.keys_a
+// (clobbered).
+hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles_bound, SortBits bits,
                        const SortBuffers& buf, int64_t* order, uint32_t* sorted_keys,
                        hipStream_t stream);
 
