@@ -230,3 +230,56 @@ def test_build_million_points_many_tiles():
     reduction, bit-exact against the oracle."""
     rng = np.random.default_rng(2024)
     check_single_build(rng.random((1_000_000, 3), dtype=np.float32))
+
+
+def _check_accel_boxes(points: np.ndarray, accel: torch.Tensor, sorted_idx: np.ndarray, dim: int) -> int:
+    """Walks the accel from the root: each record's child refs determine the
+    children's point ranges (a bucket ref names its range; an internal child
+    of a node covering [lo, hi] with index g covers [lo, g] on the left,
+    [g + 1, hi] on the right); every stored child box must equal the exact
+    min/max of its points.  Returns the number of records checked."""
+    n = points.shape[0]
+    width = 4 * dim + 4
+    off = (n * 16 + 255) // 256 * 256
+    recs = accel.cpu().numpy()[off:off + (n - 1) * width * 4].view(np.float32).reshape(-1, width)
+    refs = recs[:, 4 * dim:4 * dim + 2].copy().view(np.int32)
+    sp = points[sorted_idx]  # Morton order
+    stack = [(0, 0, n - 1)]
+    checked = 0
+    while stack:
+        node, lo, hi = stack.pop()
+        lref, rref = int(refs[node, 0]), int(refs[node, 1])
+        if lref < 0:
+            split = (lref & 0x0FFFFFFF) + ((lref >> 28) & 7)
+        else:
+            split = lref
+        ranges = ((lo, split), (split + 1, hi))
+        for c, (a, b) in enumerate(ranges):
+            box = recs[node, c * 2 * dim:(c + 1) * 2 * dim]
+            want = np.concatenate((sp[a:b + 1].min(0), sp[a:b + 1].max(0)))
+            assert np.array_equal(box.view(np.uint32), want.astype(np.float32).view(np.uint32)), \
+                f"record {node} child {c} range [{a}, {b}]"
+            ref = (lref, rref)[c]
+            if ref >= 0:
+                stack.append((ref, a, b))
+            else:
+                assert (ref & 0x0FFFFFFF) == a and ((ref >> 28) & 7) + 1 == b - a + 1
+        checked += 1
+    return checked
+
+
+@pytest.mark.parametrize("case", ["uniform3", "clustered3", "uniform2", "duplicates3"])
+def test_accel_records_hold_exact_child_boxes(case):
+    rng = np.random.default_rng({"uniform3": 71, "clustered3": 72, "uniform2": 73, "duplicates3": 74}[case])
+    if case == "uniform3":
+        p = rng.random((150_000, 3), dtype=np.float32)
+    elif case == "uniform2":
+        p = rng.random((60_000, 2), dtype=np.float32)
+    elif case == "clustered3":
+        c = rng.random((8, 3), dtype=np.float32)
+        p = (c[rng.integers(0, 8, 80_000)] + 0.02 * rng.standard_normal((80_000, 3))).astype(np.float32)
+    else:
+        p = rng.integers(0, 6, (20_000, 3)).astype(np.float32)
+    h = tb.build_bvh(dev(p))
+    checked = _check_accel_boxes(p, h._aux["accel"], h["sorted_indices"].cpu().numpy(), p.shape[1])
+    assert checked > p.shape[0] // 8

@@ -30,14 +30,25 @@
 namespace tbvh {
 namespace {
 
-// Number of differing-prefix bits between sorted positions i and j of one
-// cloud, on the 64-bit key (code << 32 | position); -1 outside the cloud.
-__device__ __forceinline__ int prefix_len(const uint32_t* codes, int n, int i, int j) {
-    if (j < 0 || j >= n) return -1;
-    const uint64_t a = (static_cast<uint64_t>(codes[i]) << 32) | static_cast<uint32_t>(i);
-    const uint64_t b = (static_cast<uint64_t>(codes[j]) << 32) | static_cast<uint32_t>(j);
-    return __clzll(static_cast<long long>(a ^ b));
-}
+// Sorted codes of one cloud, read from an LDS window where it covers the
+// position and from global memory elsewhere.
+struct CodeView {
+    const uint32_t* codes;  // cloud's codes (global)
+    const uint32_t* win;    // LDS window, cloud-local positions [w_lo, w_hi)
+    int w_lo, w_hi;
+    int n;
+    __device__ __forceinline__ uint32_t at(int j) const {
+        return (j >= w_lo && j < w_hi) ? win[j - w_lo] : codes[j];
+    }
+    // Length of the common prefix of the 64-bit keys (code << 32 | position)
+    // at positions i and j; -1 outside the cloud.
+    __device__ __forceinline__ int prefix_len(int i, uint32_t ci, int j) const {
+        if (j < 0 || j >= n) return -1;
+        const uint64_t a = (static_cast<uint64_t>(ci) << 32) | static_cast<uint32_t>(i);
+        const uint64_t b = (static_cast<uint64_t>(at(j)) << 32) | static_cast<uint32_t>(j);
+        return __clzll(static_cast<long long>(a ^ b));
+    }
+};
 
 template <int D>
 __device__ __forceinline__ void merge_row(float* box, const float* row) {
@@ -114,37 +125,70 @@ __global__ __launch_bounds__(kBlock) void accel_points_kernel(
 }
 
 // Pass 2: radix-tree internal nodes (Karras 2012, section 4), one thread per
-// node; nodes inside a bucket are not referenced and write nothing.
+// node; nodes inside a bucket are not referenced and write nothing.  The
+// block first stages the sorted codes around its nodes in LDS (most nodes
+// span few positions, so most of the searches' reads stay there; measured
+// -5% in 3-D, -16% in 2-D).  Child boxes come from the implicit tree's node
+// AABBs (reading the points directly measured slower, even for 16-point
+// ranges: more bytes through L2).
+constexpr int kCodeHalo = 256;
+constexpr int kCodeWindow = 2 * kBlock + 2 * kCodeHalo;
 template <int D>
 __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
-    const Segment* __restrict__ segs, int S, int64_t total_internal,
+    const Segment* __restrict__ segs, int S, int64_t total_internal, int64_t total_points,
     const uint32_t* __restrict__ all_codes, const float* __restrict__ node_aabbs,
     float* __restrict__ records) {
     constexpr int R = 4 * D + 4;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    __shared__ uint32_t s_codes[kCodeWindow];
+    __shared__ int64_t s_w0;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kBlock;
+    const int64_t r = r0 + threadIdx.x;
+    auto rec_first = [&](int c) { return segs[c].start - c; };
+    if (threadIdx.x == 0) {
+        // Record r belongs to cloud s at global code position r + s.
+        const int sa = find_segment(rec_first, S, r0);
+        const int64_t p0 = r0 + sa - kCodeHalo;
+        s_w0 = p0 < 0 ? 0 : p0;
+    }
+    __syncthreads();
+    const int64_t w0 = s_w0;
+    for (int k = threadIdx.x; k < kCodeWindow; k += kBlock) {
+        const int64_t gp = w0 + k;
+        s_codes[k] = gp < total_points ? all_codes[gp] : 0u;
+    }
+    __syncthreads();
     if (r >= total_internal) return;
-    const int s = find_segment([&](int c) { return segs[c].start - c; }, S, r);
+    const int s = find_segment(rec_first, S, r);
     const Segment g = segs[s];
     const int n = g.n;
     const int i = static_cast<int>(r - (g.start - s));
     if (i >= n - 1) return;
-    const uint32_t* c = all_codes + g.start;
+    // The window in positions of this cloud, clipped to it.
+    CodeView cv;
+    cv.codes = all_codes + g.start;
+    cv.n = n;
+    const int64_t lo = w0 - g.start;
+    const int64_t hi = w0 + kCodeWindow - g.start;
+    cv.win = s_codes + (lo > 0 ? 0 : -lo);
+    cv.w_lo = static_cast<int>(lo > 0 ? lo : 0);
+    cv.w_hi = static_cast<int>(hi < n ? (hi > 0 ? hi : 0) : n);
+    const uint32_t ci = cv.at(i);
 
-    const int dir = prefix_len(c, n, i, i + 1) - prefix_len(c, n, i, i - 1) > 0 ? 1 : -1;
-    const int dmin = prefix_len(c, n, i, i - dir);
+    const int dir = cv.prefix_len(i, ci, i + 1) - cv.prefix_len(i, ci, i - 1) > 0 ? 1 : -1;
+    const int dmin = cv.prefix_len(i, ci, i - dir);
     int lmax = 2;
-    while (prefix_len(c, n, i, i + lmax * dir) > dmin) lmax <<= 1;
+    while (cv.prefix_len(i, ci, i + lmax * dir) > dmin) lmax <<= 1;
     int l = 0;
     for (int t = lmax >> 1; t >= 1; t >>= 1) {
-        if (prefix_len(c, n, i, i + (l + t) * dir) > dmin) l += t;
+        if (cv.prefix_len(i, ci, i + (l + t) * dir) > dmin) l += t;
     }
     const int j = i + l * dir;
-    const int dnode = prefix_len(c, n, i, j);
+    const int dnode = cv.prefix_len(i, ci, j);
     int split = 0;
     int t = l;
     do {
         t = (t + 1) >> 1;
-        if (prefix_len(c, n, i, i + (split + t) * dir) > dnode) split += t;
+        if (cv.prefix_len(i, ci, i + (split + t) * dir) > dnode) split += t;
     } while (t > 1);
     const int gamma = i + split * dir + (dir < 0 ? dir : 0);
     const int first = min(i, j);
@@ -199,10 +243,10 @@ hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* seg
     const int Si = static_cast<int>(S);
     if (D == 3) {
         accel_nodes_kernel<3><<<grid_for(total - S), kBlock, 0, stream>>>(
-            segs, Si, total - S, sorted_codes, node_aabbs, records);
+            segs, Si, total - S, total, sorted_codes, node_aabbs, records);
     } else {
         accel_nodes_kernel<2><<<grid_for(total - S), kBlock, 0, stream>>>(
-            segs, Si, total - S, sorted_codes, node_aabbs, records);
+            segs, Si, total - S, total, sorted_codes, node_aabbs, records);
     }
     return hipGetLastError();
 }
