@@ -341,11 +341,28 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Implicit tree, level-synchronous passes
 // ---------------------------------------------------------------------------
+// Copies this group's nodes of one level (w LDS slots starting at local
+// index w - 1, of which the real ones are a prefix) to their rows, which are
+// contiguous in storage: every thread stores consecutive floats.
+template <int D>
+__device__ __forceinline__ void store_level(const float* s_box, float* nodes, int vl, int L, int lvl, int w,
+                                            int gl) {
+    const int j0 = gl * w;
+    const int real = tree::real_at_level(vl, L, lvl) - j0;
+    const int cnt = real < w ? real : w;
+    if (cnt <= 0) return;
+    const int64_t row0 = tree::memory_index(vl, L, tree::level_first(lvl) + j0);
+    float* dst = nodes + row0 * 2 * D;
+    const float* src = s_box + (w - 1) * 2 * D;
+    for (int f = threadIdx.x; f < cnt * 2 * D; f += kBlock) dst[f] = src[f];
+}
+
 // Work-group `gl` of pass p owns 2^up consecutive nodes of level lvl_in
-// (leaves for p == 0) and produces the `up` levels above them in LDS,
-// writing every real node it forms.  Nodes of a level are contiguous in
-// storage, so each level's writes are coalesced rows of 2D floats.  The same
-// thread that writes a node writes its traversal-array entries (left/right
+// (leaves for p == 0) and produces the `up` levels above them in LDS.  Nodes
+// of a level are contiguous in storage and in LDS, so each level is stored
+// by the whole group with consecutive floats per thread (one level is
+// stored while the next is formed: they occupy disjoint LDS ranges).  The
+// thread that forms a node writes its traversal-array entries (left/right
 // child rows, leaf rank) and, for leaves, the accel's float4 point.
 template <int D, bool kFromPoints>
 __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restrict__ points,
@@ -387,8 +404,6 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                     dst[d] = v;
                     dst[D + d] = v;
                 }
-#pragma unroll
-                for (int c = 0; c < 2 * D; ++c) nodes[row * 2 * D + c] = dst[c];
                 if (arrays) {
                     out.left[arr0 + row] = -1;
                     out.right[arr0 + row] = -1;
@@ -410,6 +425,9 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
     }
     __syncthreads();
     for (int step = 1; step <= up; ++step) {
+        // The level below, complete since the last barrier (the input level
+        // of a later pass is already stored).
+        if (kFromPoints || step > 1) store_level<D>(s_box, nodes, vl, L, lvl_in - step + 1, width >> (step - 1), gl);
         const int w = width >> step;
         if (tid < w) {
             const int lvl = lvl_in - step;
@@ -427,8 +445,6 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                     dst[D + d] = right_real ? fmaxf(a[D + d], b[D + d]) : a[D + d];
                 }
                 const int64_t row = tree::memory_index(vl, L, heap);
-#pragma unroll
-                for (int c = 0; c < 2 * D; ++c) nodes[row * 2 * D + c] = dst[c];
                 if (arrays) {
                     const int left_row = tree::memory_index(vl, L, 2 * heap + 1);
                     out.left[arr0 + row] = left_row;
@@ -439,6 +455,7 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
         }
         __syncthreads();
     }
+    if (kFromPoints || up > 0) store_level<D>(s_box, nodes, vl, L, lvl_in - up, width >> up, gl);
 }
 
 inline unsigned grid_for(int64_t items) {
