@@ -186,6 +186,17 @@ int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices,
              int D, int k,
              int64_t* out_indices, float* out_distances, void* stream);
 
+/* Spatial-output form.  Replaces `query_knn_batched_cached_bounds_spatial`
+ * (torchbvh/csrc/bindings.cpp:199, knn_query.cu:448-461, used by
+ * `_mls.py:169`): same search, but output row [b, m] holds the result of
+ * query order[b, m] (the launch order, which is the Morton order the MLS
+ * kernels consume) instead of query m.  `order` is required. */
+int tbvh_knn_spatial(const float* node_aabbs, const int64_t* sorted_indices,
+                     const float* queries, const int64_t* order,
+                     int64_t B, int64_t M, int64_t num_leaves, int64_t num_real_nodes,
+                     int D, int k,
+                     int64_t* out_indices, float* out_distances, void* stream);
+
 /* Ragged form over the packed outputs of tbvh_build_ragged.  point_offsets,
  * node_offsets and query_offsets are device int64 [B+1]; `order` (local query
  * indices from tbvh_sort_queries_ragged) may be NULL.  Every cloud must hold
@@ -225,6 +236,10 @@ int tbvh_accel_build_ragged(const float* points, const int64_t* offsets,
 int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order,
                    int64_t B, int64_t M, int64_t num_leaves, int D, int k,
                    int64_t* out_indices, float* out_distances, void* stream);
+/* Spatial-output form of tbvh_knn_accel (see tbvh_knn_spatial). */
+int tbvh_knn_accel_spatial(const void* accel, const float* queries, const int64_t* order,
+                           int64_t B, int64_t M, int64_t num_leaves, int D, int k,
+                           int64_t* out_indices, float* out_distances, void* stream);
 int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets,
                           int64_t total_points, const float* queries,
                           const int64_t* query_offsets, const int64_t* order,

@@ -162,3 +162,14 @@ def test_build_with_accel_argument_errors():
     assert L.tbvh_build_ragged_with_accel(FAKE, FAKE, 2, 100, 3, *([FAKE] * 8), 10, FAKE,
                                           FAKE, 1 << 20, None) == 1
     assert "total_nodes" in _err(L)
+
+
+def test_spatial_knn_requires_an_order():
+    L = _native.load()
+    nr = _native.real_node_count(100)
+    assert L.tbvh_knn_spatial(FAKE, FAKE, FAKE, None, 1, 10, 100, nr, 3, 4, FAKE, FAKE, None) == 1
+    assert "null" in _err(L)
+    assert L.tbvh_knn_accel_spatial(FAKE, FAKE, None, 1, 10, 100, 3, 4, FAKE, FAKE, None) == 1
+    assert "null" in _err(L)
+    assert L.tbvh_knn_accel_spatial(FAKE, FAKE, FAKE, 1, 10, 100, 3, 5, FAKE, FAKE, None) == 1
+    assert "k must be" in _err(L)

@@ -273,3 +273,29 @@ def test_ragged_indices_are_local():
         s = idx[3 * b:3 * b + 3]
         assert int(s.min()) >= 0 and int(s.max()) < c
     assert torch.all(dist[:, 0] == 0)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 16, 32])
+@pytest.mark.parametrize("use_accel", [True, False])
+def test_spatial_output_is_ordered_output_in_launch_order(dim, k, use_accel):
+    """`query_knn_batched_cached_bounds_spatial` (knn_query.cu:147-148,
+    448-461): row [b, m] holds the result of query order[b, m]."""
+    rng = np.random.default_rng(300 + dim * 10 + k)
+    p = rng.random((3, 2000, dim), dtype=np.float32)
+    q = rng.random((3, 777, dim), dtype=np.float32)
+    h = tb.build_bvh(dev(p))
+    qd = dev(q)
+    order = _C.morton_sort_queries_narrow(qd, h["scene_min"], h["scene_max"])
+    args = (h["node_aabbs"], h["sorted_indices"], qd, order, h["num_leaves"], h["num_real_nodes"], dim, k)
+    accel = h._aux["accel"] if use_accel else None
+    si, sd = _C.query_knn_batched_cached_bounds_spatial(*args, accel=accel)
+    oi, od = _C.query_knn_batched_cached_bounds_ordered(*args, accel=accel)
+    perm = order.unsqueeze(-1).expand(-1, -1, k)
+    assert torch.equal(si, torch.gather(oi, 1, perm))
+    assert torch.equal(sd, torch.gather(od, 1, perm))
+    o = order.cpu().numpy()
+    for b in range(3):
+        ei, ed = oracle.knn(p[b], q[b][o[b]], k)
+        assert_same_int(si[b].cpu().numpy(), ei, f"batch {b} indices")
+        assert_same_f32(sd[b].cpu().numpy(), ed, f"batch {b} distances")

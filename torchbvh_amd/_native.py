@@ -64,6 +64,7 @@ def _declare(L) -> None:
     L.tbvh_schedule_queries_ragged.argtypes = L.tbvh_sort_queries_ragged.argtypes
     L.tbvh_morton_codes.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_knn.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    L.tbvh_knn_spatial.argtypes = L.tbvh_knn.argtypes
     L.tbvh_knn_ragged.argtypes = (
         [_vp] * 7 + [_i64, _i64, _int, _int, _vp, _vp, _vp]
     )
@@ -74,6 +75,7 @@ def _declare(L) -> None:
         [_vp] * 6 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
     )
     L.tbvh_knn_accel.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    L.tbvh_knn_accel_spatial.argtypes = L.tbvh_knn_accel.argtypes
     L.tbvh_knn_accel_ragged.argtypes = (
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp]
     )
@@ -85,7 +87,7 @@ def _declare(L) -> None:
         "tbvh_schedule_queries", "tbvh_schedule_queries_ragged",
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
-        "tbvh_knn_accel", "tbvh_knn_accel_ragged",
+        "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
     ):
         getattr(L, name).restype = _int
 
@@ -417,7 +419,7 @@ class _NativeOps:
 
     @staticmethod
     def _knn(op, node_aabbs, sorted_indices, query_points, query_order, num_leaves,
-             num_real_nodes, dim, k, accel=None):
+             num_real_nodes, dim, k, accel=None, spatial=False):
         _require(dim in (2, 3), op, "D must be 2 or 3")
         _require_device_f32(op, query_points, "query_points")
         _require(query_points.dim() == 3 and query_points.size(2) == dim, op,
@@ -447,11 +449,13 @@ class _NativeOps:
         with torch.cuda.device(dev):
             if accel is not None:
                 _require(accel.is_cuda and accel.device == dev, op, "accel must be on the queries' device")
-                _check(L.tbvh_knn_accel(
+                fn = L.tbvh_knn_accel_spatial if spatial else L.tbvh_knn_accel
+                _check(fn(
                     _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
                     int(dim), int(k), _ptr(indices), _ptr(distances), _stream(dev)))
             else:
-                _check(L.tbvh_knn(
+                fn = L.tbvh_knn_spatial if spatial else L.tbvh_knn
+                _check(fn(
                     _ptr(node_aabbs), _ptr(sorted_indices), _ptr(query_points), _ptr(query_order),
                     B, M, int(num_leaves), int(num_real_nodes), int(dim), int(k),
                     _ptr(indices), _ptr(distances), _stream(dev)))
@@ -473,6 +477,18 @@ class _NativeOps:
         (identical results)."""
         return cls._knn("query_knn_batched_cached_bounds_ordered", node_aabbs, sorted_indices,
                         query_points, query_order, num_leaves, num_real_nodes, dim, k, accel)
+
+    @classmethod
+    def query_knn_batched_cached_bounds_spatial(cls, node_aabbs, sorted_indices, query_points,
+                                                query_order, num_leaves, num_real_nodes, dim, k,
+                                                *, accel=None):
+        """Reference binding `query_knn_batched_cached_bounds_spatial`
+        (bindings.cpp:199): as the ordered traversal, but row [b, m] of the
+        output holds query query_order[b, m] (launch order)."""
+        op = "query_knn_batched_cached_bounds_spatial"
+        _require(query_order is not None, op, "query_order is required")
+        return cls._knn(op, node_aabbs, sorted_indices, query_points, query_order, num_leaves,
+                        num_real_nodes, dim, k, accel, spatial=True)
 
     @staticmethod
     def query_knn_ragged(node_aabbs, sorted_indices, point_offsets, node_offsets, query_points,

@@ -447,11 +447,10 @@ int tbvh_schedule_queries_ragged(const float* queries, const int64_t* query_offs
 // ---------------------------------------------------------------------------
 // k-NN
 // ---------------------------------------------------------------------------
-int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices, const float* queries,
-             const int64_t* order, int64_t B, int64_t M, int64_t num_leaves,
-             int64_t num_real_nodes, int D, int k, int64_t* out_indices, float* out_distances,
-             void* stream_ptr) {
-    const char* op = "tbvh_knn";
+static int knn_batched(const char* op, const float* node_aabbs, const int64_t* sorted_indices,
+                       const float* queries, const int64_t* order, int64_t B, int64_t M,
+                       int64_t num_leaves, int64_t num_real_nodes, int D, int k, bool spatial,
+                       int64_t* out_indices, float* out_distances, void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
     if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
@@ -465,7 +464,7 @@ int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices, const float
     if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
     if (B > kMaxRows / num_leaves) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
     if (M == 0) return ok();
-    if (!node_aabbs || !sorted_indices || !queries || !out_indices || !out_distances) {
+    if (!node_aabbs || !sorted_indices || !queries || !out_indices || !out_distances || (spatial && !order)) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }
     KnnArgs a{};
@@ -480,8 +479,26 @@ int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices, const float
     a.num_real_nodes = static_cast<int32_t>(num_real_nodes);
     a.out_indices = out_indices;
     a.out_distances = out_distances;
+    a.spatial_output = spatial;
     TBVH_TRY(op, launch_knn(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices, const float* queries,
+             const int64_t* order, int64_t B, int64_t M, int64_t num_leaves,
+             int64_t num_real_nodes, int D, int k, int64_t* out_indices, float* out_distances,
+             void* stream_ptr) {
+    return knn_batched("tbvh_knn", node_aabbs, sorted_indices, queries, order, B, M, num_leaves,
+                       num_real_nodes, D, k, false, out_indices, out_distances, stream_ptr);
+}
+
+int tbvh_knn_spatial(const float* node_aabbs, const int64_t* sorted_indices, const float* queries,
+                     const int64_t* order, int64_t B, int64_t M, int64_t num_leaves,
+                     int64_t num_real_nodes, int D, int k, int64_t* out_indices,
+                     float* out_distances, void* stream_ptr) {
+    return knn_batched("tbvh_knn_spatial", node_aabbs, sorted_indices, queries, order, B, M,
+                       num_leaves, num_real_nodes, D, k, true, out_indices, out_distances,
+                       stream_ptr);
 }
 
 int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
@@ -597,10 +614,10 @@ int tbvh_accel_build_ragged(const float* points, const int64_t* offsets, const i
     return ok();
 }
 
-int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order, int64_t B,
-                   int64_t M, int64_t num_leaves, int D, int k, int64_t* out_indices,
-                   float* out_distances, void* stream_ptr) {
-    const char* op = "tbvh_knn_accel";
+static int knn_accel_batched(const char* op, const void* accel, const float* queries,
+                             const int64_t* order, int64_t B, int64_t M, int64_t num_leaves, int D,
+                             int k, bool spatial, int64_t* out_indices, float* out_distances,
+                             void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
     if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
@@ -611,7 +628,7 @@ int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order
     if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
     if (B > kMaxRows / num_leaves) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
     if (M == 0) return ok();
-    if (!accel || !queries || !out_indices || !out_distances) {
+    if (!accel || !queries || !out_indices || !out_distances || (spatial && !order)) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }
     KnnArgs a{};
@@ -625,8 +642,23 @@ int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order
     a.out_distances = out_distances;
     a.accel = accel;
     a.total_points = B * num_leaves;
+    a.spatial_output = spatial;
     TBVH_TRY(op, launch_knn_accel(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order, int64_t B,
+                   int64_t M, int64_t num_leaves, int D, int k, int64_t* out_indices,
+                   float* out_distances, void* stream_ptr) {
+    return knn_accel_batched("tbvh_knn_accel", accel, queries, order, B, M, num_leaves, D, k, false,
+                             out_indices, out_distances, stream_ptr);
+}
+
+int tbvh_knn_accel_spatial(const void* accel, const float* queries, const int64_t* order, int64_t B,
+                           int64_t M, int64_t num_leaves, int D, int k, int64_t* out_indices,
+                           float* out_distances, void* stream_ptr) {
+    return knn_accel_batched("tbvh_knn_accel_spatial", accel, queries, order, B, M, num_leaves, D, k,
+                             true, out_indices, out_distances, stream_ptr);
 }
 
 int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets, int64_t total_points,

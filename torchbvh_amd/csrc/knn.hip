@@ -140,8 +140,10 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
         nd = __uint_as_float(static_cast<uint32_t>(e));
     }
 
-    int64_t* oi = a.out_indices + row * K;
-    float* od = a.out_distances + row * K;
+    // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
+    const int64_t out_row = a.spatial_output ? qbase + local : row;
+    int64_t* oi = a.out_indices + out_row * K;
+    float* od = a.out_distances + out_row * K;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
         oi[i] = static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(best[i])));
@@ -373,8 +375,10 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
         stack.pop(nd, ref);
     }
 
-    int64_t* oi = a.out_indices + row * K;
-    float* od = a.out_distances + row * K;
+    // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
+    const int64_t out_row = a.spatial_output ? qbase + local : row;
+    int64_t* oi = a.out_indices + out_row * K;
+    float* od = a.out_distances + out_row * K;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
         oi[i] = static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(best[i])));

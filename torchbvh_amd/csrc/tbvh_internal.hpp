@@ -201,6 +201,7 @@ struct KnnArgs {
     float* out_distances;
     const void* accel;             // accelerated traversal only
     int64_t total_points;          // accelerated traversal only
+    bool spatial_output;           // write row `launch position` instead of `query index`
 };
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
