@@ -161,6 +161,22 @@ int tbvh_schedule_queries_ragged(const float* queries, const int64_t* query_offs
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* ---- routed query ordering -------------------------------------------------------------
+ * Replaces `morton_sort_routed_queries_batched` (torchbvh/csrc/bindings.cpp:196,
+ * morton_sort.cu:82-120, 288-329; used by `_conditional.py:164`): every query
+ * [b, m] has a route (bool as one byte; true selects the first of two BVHs)
+ * and is encoded against that route's bounds; `order` [B, M] int64 is the
+ * stable order of the composite key (route << code_bits | code), i.e. each
+ * cloud's false-route queries in Morton order, then its true-route queries. */
+int tbvh_sort_routed_queries_workspace_size(int64_t B, int64_t M, int D,
+                                            size_t* bytes);
+int tbvh_sort_routed_queries(const float* queries, const uint8_t* routes,
+                             int64_t B, int64_t M, int D,
+                             const float* true_min, const float* true_max,
+                             const float* false_min, const float* false_max,
+                             int64_t* order,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- diagnostic: Morton codes ------------------------------------------------------
  * No counterpart in the reference's FFI (its codes stay inside
  * `narrow_morton_sort_batched`, bvh_build.cu:551-600, and
@@ -245,6 +261,30 @@ int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets,
                           const int64_t* query_offsets, const int64_t* order,
                           int64_t B, int64_t total_q, int D, int k,
                           int64_t* out_indices, float* out_distances, void* stream);
+
+/* ---- routed k-NN (spatial output) --------------------------------------------------
+ * Replaces `query_knn_routed_batched_cached_bounds_spatial`
+ * (torchbvh/csrc/bindings.cpp:200, knn_query.cu:183-327, 463-539; used by `_conditional.py:181`):
+ * query [b, order[b, m]] searches the true-route tree if routes[b, query] is
+ * non-zero, else the false-route tree, whose indices are reported after the
+ * true cloud's (+ true_num_leaves); output row [b, m] (launch order).  Both
+ * clouds need at least k points.  Same candidate rule as tbvh_knn. */
+int tbvh_knn_routed_spatial(const float* true_node_aabbs, const int64_t* true_sorted_indices,
+                            const float* false_node_aabbs, const int64_t* false_sorted_indices,
+                            const float* queries, const uint8_t* routes, const int64_t* order,
+                            int64_t B, int64_t M,
+                            int64_t true_num_leaves, int64_t true_num_real_nodes,
+                            int64_t false_num_leaves, int64_t false_num_real_nodes,
+                            int D, int k,
+                            int64_t* out_indices, float* out_distances, void* stream);
+/* Same over the two clouds' acceleration structures (no counterpart in the
+ * reference; identical results). */
+int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_accel,
+                                  const float* queries, const uint8_t* routes,
+                                  const int64_t* order, int64_t B, int64_t M,
+                                  int64_t true_num_leaves, int64_t false_num_leaves,
+                                  int D, int k,
+                                  int64_t* out_indices, float* out_distances, void* stream);
 
 #ifdef __cplusplus
 }

@@ -189,6 +189,35 @@ def schedule_order(queries, scene_min, scene_max) -> np.ndarray:
     return stable_argsort((codes >> np.uint64(bits - 16)).astype(np.uint32))
 
 
+def routed_order(queries, routes, true_min, true_max, false_min, false_max) -> np.ndarray:
+    """Routed query order of one cloud (torchbvh/csrc/morton_sort.cu:82-120,
+    240-286): each query encoded against its route's bounds, composite key
+    route << code_bits | code, stable order."""
+    q = _f32(queries)
+    r = np.asarray(routes, dtype=bool)
+    bits = 30 if q.shape[1] == 3 else 32
+    ct = morton_codes(q, true_min, true_max).astype(np.uint64)
+    cf = morton_codes(q, false_min, false_max).astype(np.uint64)
+    key = np.where(r, ct | (np.uint64(1) << np.uint64(bits)), cf)
+    return np.argsort(key, kind="stable").astype(np.int64)
+
+
+def knn_routed(true_points, false_points, queries, routes, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """Routed k-NN of one cloud (torchbvh/csrc/knn_query.cu:183-327): a query
+    with a true route searches the true points, else the false points, whose
+    indices follow the true cloud's (+ len(true_points)); rows in query order."""
+    q = _f32(queries)
+    r = np.asarray(routes, dtype=bool)
+    idx = np.empty((q.shape[0], k), np.int64)
+    dist = np.empty((q.shape[0], k), np.float32)
+    if r.any():
+        idx[r], dist[r] = knn(true_points, q[r], k)
+    if (~r).any():
+        i, d = knn(false_points, q[~r], k)
+        idx[~r], dist[~r] = i + len(true_points), d
+    return idx, dist
+
+
 def knn_brute(points, queries, k: int) -> tuple[np.ndarray, np.ndarray]:
     p = _f32(points)
     q = _f32(queries)

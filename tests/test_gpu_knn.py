@@ -299,3 +299,49 @@ def test_spatial_output_is_ordered_output_in_launch_order(dim, k, use_accel):
         ei, ed = oracle.knn(p[b], q[b][o[b]], k)
         assert_same_int(si[b].cpu().numpy(), ei, f"batch {b} indices")
         assert_same_f32(sd[b].cpu().numpy(), ed, f"batch {b} distances")
+
+
+def _routed_case(dim, B, nt, nf, m, seed, frac=0.5):
+    rng = np.random.default_rng(seed)
+    tp = rng.random((B, nt, dim), dtype=np.float32)
+    fp = (rng.random((B, nf, dim), dtype=np.float32) * 2.0 - 0.5).astype(np.float32)
+    q = (rng.random((B, m, dim), dtype=np.float32) * 1.4 - 0.2).astype(np.float32)
+    routes = rng.random((B, m)) < frac
+    routes[0, :] = True    # a cloud whose queries all take the true route
+    if B > 1:
+        routes[1, :] = False  # ... and one whose queries all take the false route
+    return tp, fp, q, routes
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("m", [1, 300, 5000])
+def test_routed_order_bit_exact(dim, m):
+    tp, fp, q, routes = _routed_case(dim, 3, 500, 400, m, 410 + m + dim)
+    ht, hf = tb.build_bvh(dev(tp)), tb.build_bvh(dev(fp))
+    order = _C.morton_sort_routed_queries_batched(dev(q), dev(routes), ht["scene_min"], ht["scene_max"],
+                                                  hf["scene_min"], hf["scene_max"]).cpu().numpy()
+    tmin, tmax = ht["scene_min"].cpu().numpy(), ht["scene_max"].cpu().numpy()
+    fmin, fmax = hf["scene_min"].cpu().numpy(), hf["scene_max"].cpu().numpy()
+    for b in range(3):
+        want = oracle.routed_order(q[b], routes[b], tmin[b], tmax[b], fmin[b], fmax[b])
+        assert_same_int(order[b], want, f"cloud {b} routed order")
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("k", [4, 16, 32])
+@pytest.mark.parametrize("use_accel", [True, False])
+def test_routed_knn_spatial_matches_oracle(dim, k, use_accel):
+    tp, fp, q, routes = _routed_case(dim, 3, 900, 700, 640, 520 + dim * 10 + k)
+    ht, hf = tb.build_bvh(dev(tp)), tb.build_bvh(dev(fp))
+    qd, rd = dev(q), dev(routes)
+    order = _C.morton_sort_routed_queries_batched(qd, rd, ht["scene_min"], ht["scene_max"],
+                                                  hf["scene_min"], hf["scene_max"])
+    kw = {"true_accel": ht._aux["accel"], "false_accel": hf._aux["accel"]} if use_accel else {}
+    idx, dist = _C.query_knn_routed_batched_cached_bounds_spatial(
+        ht["node_aabbs"], ht["sorted_indices"], hf["node_aabbs"], hf["sorted_indices"], qd, rd, order,
+        ht["num_leaves"], ht["num_real_nodes"], hf["num_leaves"], hf["num_real_nodes"], dim, k, **kw)
+    o = order.cpu().numpy()
+    for b in range(3):
+        ei, ed = oracle.knn_routed(tp[b], fp[b], q[b][o[b]], routes[b][o[b]], k)
+        assert_same_int(idx[b].cpu().numpy(), ei, f"cloud {b} indices")
+        assert_same_f32(dist[b].cpu().numpy(), ed, f"cloud {b} distances")

@@ -164,6 +164,34 @@ def test_schedule_order_is_stable_sort_on_top_16_code_bits(dim):
     assert not np.array_equal(got, oracle.query_order(q, lo, hi))  # coarser than the full order
 
 
+@pytest.mark.parametrize("dim", [2, 3])
+def test_routed_order_is_stable_sort_on_route_then_code(dim):
+    """Pinned by its definition through a plain Python sort on (route, code of
+    the route's bounds, query index); 2-D needs the 33rd key bit."""
+    rng = np.random.default_rng(81 + dim)
+    q = rng.random((2500, dim), dtype=np.float32)
+    routes = rng.random(2500) < 0.4
+    tlo, thi = np.zeros(dim, np.float32), np.ones(dim, np.float32)
+    flo, fhi = np.full(dim, -1.0, np.float32), np.full(dim, 2.0, np.float32)
+    ct = oracle.morton_codes(q, tlo, thi).astype(np.int64)
+    cf = oracle.morton_codes(q, flo, fhi).astype(np.int64)
+    want = sorted(range(len(q)), key=lambda i: (int(routes[i]), ct[i] if routes[i] else cf[i], i))
+    got = oracle.routed_order(q, routes, tlo, thi, flo, fhi)
+    assert_same_int(got, np.array(want, np.int64), "routed order")
+
+
+def test_routed_knn_offsets_false_route_indices():
+    rng = np.random.default_rng(91)
+    tp = rng.random((300, 3), dtype=np.float32)
+    fp = rng.random((200, 3), dtype=np.float32) + 5.0
+    q = np.concatenate((tp[:5], fp[:5])).astype(np.float32)
+    routes = np.array([True] * 5 + [False] * 5)
+    idx, dist = oracle.knn_routed(tp, fp, q, routes, 4)
+    assert_same_int(idx[:5, 0], np.arange(5), "true self")
+    assert_same_int(idx[5:, 0], 300 + np.arange(5), "false self, offset")
+    assert (dist[:, 0] == 0).all()
+
+
 def test_bounds_match_numpy_and_seed_semantics():
     rng = np.random.default_rng(9)
     p = rng.standard_normal((1000, 3)).astype(np.float32)

@@ -62,6 +62,16 @@ def _declare(L) -> None:
     )
     L.tbvh_schedule_queries.argtypes = L.tbvh_sort_queries.argtypes
     L.tbvh_schedule_queries_ragged.argtypes = L.tbvh_sort_queries_ragged.argtypes
+    L.tbvh_sort_routed_queries_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_sort_routed_queries.argtypes = (
+        [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    )
+    L.tbvh_knn_routed_spatial.argtypes = (
+        [_vp] * 7 + [_i64] * 6 + [_int, _int, _vp, _vp, _vp]
+    )
+    L.tbvh_knn_accel_routed_spatial.argtypes = (
+        [_vp] * 5 + [_i64] * 4 + [_int, _int, _vp, _vp, _vp]
+    )
     L.tbvh_morton_codes.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_knn.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
     L.tbvh_knn_spatial.argtypes = L.tbvh_knn.argtypes
@@ -88,6 +98,8 @@ def _declare(L) -> None:
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
         "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
+        "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
+        "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
     ):
         getattr(L, name).restype = _int
 
@@ -489,6 +501,89 @@ class _NativeOps:
         _require(query_order is not None, op, "query_order is required")
         return cls._knn(op, node_aabbs, sorted_indices, query_points, query_order, num_leaves,
                         num_real_nodes, dim, k, accel, spatial=True)
+
+    @staticmethod
+    def morton_sort_routed_queries_batched(queries: torch.Tensor, routes: torch.Tensor,
+                                           true_scene_min: torch.Tensor, true_scene_max: torch.Tensor,
+                                           false_scene_min: torch.Tensor,
+                                           false_scene_max: torch.Tensor) -> torch.Tensor:
+        """Reference binding `morton_sort_routed_queries_batched`
+        (morton_sort.cu:288-329): stable order of (route, Morton code against
+        the route's bounds) per cloud."""
+        op = "morton_sort_routed_queries_batched"
+        _require_device_f32(op, queries, "queries")
+        _require(queries.dim() == 3 and queries.size(2) in (2, 3), op, "queries must have shape (B, M, D)")
+        _require(routes.is_cuda and routes.is_contiguous() and routes.dtype == torch.bool, op,
+                 "routes must be contiguous CUDA bool")
+        _require(routes.dim() == 2 and tuple(routes.shape) == tuple(queries.shape[:2]), op,
+                 "routes must have shape (B, M)")
+        B, M, D = (int(s) for s in queries.shape)
+        for t in (true_scene_min, true_scene_max, false_scene_min, false_scene_max):
+            _require_device_f32(op, t, "scene bounds")
+            _require(tuple(t.shape) == (B, D), op, "each scene bound must have shape (B, D)")
+        dev = queries.device
+        for t in (routes, true_scene_min, true_scene_max, false_scene_min, false_scene_max):
+            _require(t.device == dev, op, "all inputs must share a device")
+        L = load()
+        order = torch.empty((B, M), dtype=torch.int64, device=dev)
+        if M == 0:
+            return order
+        with torch.cuda.device(dev):
+            ws = _workspace(_size(L.tbvh_sort_routed_queries_workspace_size, B, M, D), dev)
+            _check(L.tbvh_sort_routed_queries(
+                _ptr(queries), _ptr(routes), B, M, D, _ptr(true_scene_min), _ptr(true_scene_max),
+                _ptr(false_scene_min), _ptr(false_scene_max), _ptr(order), _ptr(ws), ws.numel(),
+                _stream(dev)))
+        return order
+
+    @staticmethod
+    def query_knn_routed_batched_cached_bounds_spatial(
+            true_node_aabbs, true_sorted_indices, false_node_aabbs, false_sorted_indices, query_points,
+            routes, query_order, true_num_leaves, true_num_real_nodes, false_num_leaves,
+            false_num_real_nodes, dim, k, *, true_accel=None, false_accel=None):
+        """Reference binding `query_knn_routed_batched_cached_bounds_spatial`
+        (knn_query.cu:463-539): routed search, output rows in launch order,
+        false-route indices offset by true_num_leaves.  With both accels the
+        accelerated traversal (identical results)."""
+        op = "query_knn_routed_batched_cached_bounds_spatial"
+        _require(dim in (2, 3), op, "D must be 2 or 3")
+        _require_device_f32(op, query_points, "query_points")
+        _require(query_points.dim() == 3 and query_points.size(2) == dim, op,
+                 "query_points must have shape (B, M, D)")
+        B, M = int(query_points.size(0)), int(query_points.size(1))
+        _require(routes.is_cuda and routes.is_contiguous() and routes.dtype == torch.bool
+                 and tuple(routes.shape) == (B, M), op, "routes must be contiguous CUDA bool (B, M)")
+        _require_device_i64(op, query_order, "query_order")
+        _require(tuple(query_order.shape) == (B, M), op, "query_order must have shape (B, M)")
+        for nodes, nr, name in ((true_node_aabbs, true_num_real_nodes, "true_node_aabbs"),
+                                (false_node_aabbs, false_num_real_nodes, "false_node_aabbs")):
+            _require_device_f32(op, nodes, name)
+            _require(tuple(nodes.shape) == (B, nr, 2 * dim), op, f"{name} has incompatible shape")
+        for srt, n, name in ((true_sorted_indices, true_num_leaves, "true_sorted_indices"),
+                             (false_sorted_indices, false_num_leaves, "false_sorted_indices")):
+            _require_device_i64(op, srt, name)
+            _require(tuple(srt.shape) == (B, n), op, f"{name} has incompatible shape")
+        _require(true_num_leaves >= k and false_num_leaves >= k, op, "both source counts must be >= k")
+        dev = query_points.device
+        indices = torch.empty((B, M, k), dtype=torch.int64, device=dev)
+        distances = torch.empty((B, M, k), dtype=torch.float32, device=dev)
+        if M == 0:
+            return indices, distances
+        L = load()
+        with torch.cuda.device(dev):
+            if true_accel is not None and false_accel is not None:
+                _check(L.tbvh_knn_accel_routed_spatial(
+                    _ptr(true_accel), _ptr(false_accel), _ptr(query_points), _ptr(routes),
+                    _ptr(query_order), B, M, int(true_num_leaves), int(false_num_leaves), int(dim),
+                    int(k), _ptr(indices), _ptr(distances), _stream(dev)))
+            else:
+                _check(L.tbvh_knn_routed_spatial(
+                    _ptr(true_node_aabbs), _ptr(true_sorted_indices), _ptr(false_node_aabbs),
+                    _ptr(false_sorted_indices), _ptr(query_points), _ptr(routes), _ptr(query_order),
+                    B, M, int(true_num_leaves), int(true_num_real_nodes), int(false_num_leaves),
+                    int(false_num_real_nodes), int(dim), int(k), _ptr(indices), _ptr(distances),
+                    _stream(dev)))
+        return indices, distances
 
     @staticmethod
     def query_knn_ragged(node_aabbs, sorted_indices, point_offsets, node_offsets, query_points,

@@ -445,6 +445,97 @@ int tbvh_schedule_queries_ragged(const float* queries, const int64_t* query_offs
 }
 
 // ---------------------------------------------------------------------------
+// Routed query ordering
+// ---------------------------------------------------------------------------
+namespace {
+
+struct RoutedLayout {
+    size_t part, gathered, offsets, gmin, gmax, sorted_local, total;
+};
+
+RoutedLayout make_routed_layout(int64_t B, int64_t M, int D) {
+    const int64_t rows = B * M;
+    const size_t sort_a = make_layout(B, rows, D, false).total;
+    const size_t sort_b = make_layout(2 * B, rows, D, false).total;
+    RoutedLayout r;
+    size_t at = align_up(sort_a > sort_b ? sort_a : sort_b);
+    r.part = at; at = align_up(at + static_cast<size_t>(rows) * 8);
+    r.gathered = at; at = align_up(at + static_cast<size_t>(rows) * D * 4);
+    r.offsets = at; at = align_up(at + static_cast<size_t>(2 * B + 1) * 8);
+    r.gmin = at; at = align_up(at + static_cast<size_t>(2 * B) * D * 4);
+    r.gmax = at; at = align_up(at + static_cast<size_t>(2 * B) * D * 4);
+    r.sorted_local = at; at = align_up(at + static_cast<size_t>(rows) * 8);
+    r.total = at;
+    return r;
+}
+
+hipError_t run_routed_sort(const float* queries, const uint8_t* routes, int64_t B, int64_t M, int D,
+                           const float* true_min, const float* true_max, const float* false_min,
+                           const float* false_max, int64_t* order, void* ws, hipStream_t stream) {
+    const int64_t rows = B * M;
+    const RoutedLayout r = make_routed_layout(B, M, D);
+    int64_t* part = carve<int64_t>(ws, r.part);
+    float* gathered = carve<float>(ws, r.gathered);
+    int64_t* group_offsets = carve<int64_t>(ws, r.offsets);
+    float* gmin = carve<float>(ws, r.gmin);
+    float* gmax = carve<float>(ws, r.gmax);
+    int64_t* sorted_local = carve<int64_t>(ws, r.sorted_local);
+    // 1. Stable partition of every cloud by route (one 8-bit pass on 0/1).
+    const Layout l = make_layout(B, rows, D, false);
+    Segment* segs = carve<Segment>(ws, l.segs);
+    const SortBuffers sb = sort_buffers(ws, l, B);
+    hipError_t e = launch_plan_uniform(segs, B, M, false, sb.hist, l.clear_words, stream);
+    if (e != hipSuccess) return e;
+    if ((e = launch_route_keys(routes, segs, B, l.tiles, sb.keys_a, sb.hist, stream)) != hipSuccess) return e;
+    if ((e = launch_sort(segs, B, l.tiles, SortBits{0, kRadixBits}, sb, part, nullptr, stream)) != hipSuccess) {
+        return e;
+    }
+    // 2. Partitioned queries as 2B segments (false group, true group per cloud).
+    if ((e = launch_route_gather(queries, part, sb.hist, B, M, D, true_min, true_max, false_min, false_max,
+                                 gathered, group_offsets, gmin, gmax, stream)) != hipSuccess) {
+        return e;
+    }
+    // 3. Morton order within every group, against the group's route bounds.
+    if ((e = run_query_sort(gathered, group_offsets, 2 * B, 0, rows, D, gmin, gmax, full_sort(D), sorted_local,
+                            nullptr, ws, stream)) != hipSuccess) {
+        return e;
+    }
+    // 4. Back to query indices.
+    return launch_route_finish(part, sorted_local, group_offsets, B, M, order, stream);
+}
+
+}  // namespace
+
+int tbvh_sort_routed_queries_workspace_size(int64_t B, int64_t M, int D, size_t* bytes) {
+    const char* op = "tbvh_sort_routed_queries_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    *bytes = make_routed_layout(B, M, D).total;
+    return ok();
+}
+
+int tbvh_sort_routed_queries(const float* queries, const uint8_t* routes, int64_t B, int64_t M, int D,
+                             const float* true_min, const float* true_max, const float* false_min,
+                             const float* false_max, int64_t* order, void* workspace,
+                             size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_sort_routed_queries";
+    if (int r = check_dim(op, D)) return r;
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (M == 0) return ok();
+    if (M > kMaxCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: at most 2^30 queries per cloud", op);
+    if (!queries || !routes || !true_min || !true_max || !false_min || !false_max || !order) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    if (int r = check_workspace(op, workspace, workspace_bytes, make_routed_layout(B, M, D).total)) return r;
+    TBVH_TRY(op, run_routed_sort(queries, routes, B, M, D, true_min, true_max, false_min, false_max, order,
+                                 workspace, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
 // k-NN
 // ---------------------------------------------------------------------------
 static int knn_batched(const char* op, const float* node_aabbs, const int64_t* sorted_indices,
@@ -688,6 +779,93 @@ int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets, int64
     a.accel = accel;
     a.total_points = total_points;
     TBVH_TRY(op, launch_knn_accel(a, D, k, true, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Routed k-NN (spatial output)
+// ---------------------------------------------------------------------------
+static int check_routed(const char* op, int64_t B, int64_t M, int64_t true_n, int64_t false_n, int64_t max_n,
+                        int D, int k) {
+    if (int r = check_dim(op, D)) return r;
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
+    if (true_n < 1 || true_n > max_n || false_n < 1 || false_n > max_n) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: leaf counts out of range", op);
+    }
+    if (true_n < k || false_n < k) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: both source counts must be >= k", op);
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    if (B > kMaxRows / (true_n + false_n)) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total point count must fit in signed int32", op);
+    }
+    return TBVH_OK;
+}
+
+int tbvh_knn_routed_spatial(const float* true_node_aabbs, const int64_t* true_sorted_indices,
+                            const float* false_node_aabbs, const int64_t* false_sorted_indices,
+                            const float* queries, const uint8_t* routes, const int64_t* order, int64_t B,
+                            int64_t M, int64_t true_num_leaves, int64_t true_num_real_nodes,
+                            int64_t false_num_leaves, int64_t false_num_real_nodes, int D, int k,
+                            int64_t* out_indices, float* out_distances, void* stream_ptr) {
+    const char* op = "tbvh_knn_routed_spatial";
+    if (int r = check_routed(op, B, M, true_num_leaves, false_num_leaves, kMaxCloud, D, k)) return r;
+    if (true_num_real_nodes != tree::real_node_count(static_cast<int>(true_num_leaves)) ||
+        false_num_real_nodes != tree::real_node_count(static_cast<int>(false_num_leaves))) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_real_nodes does not match num_leaves", op);
+    }
+    if (M == 0) return ok();
+    if (!true_node_aabbs || !true_sorted_indices || !false_node_aabbs || !false_sorted_indices || !queries ||
+        !routes || !order || !out_indices || !out_distances) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    KnnArgs a{};
+    a.node_aabbs = true_node_aabbs;
+    a.sorted_indices = true_sorted_indices;
+    a.node_aabbs2 = false_node_aabbs;
+    a.sorted_indices2 = false_sorted_indices;
+    a.queries = queries;
+    a.order = order;
+    a.routes = routes;
+    a.B = B;
+    a.M = M;
+    a.total_q = B * M;
+    a.num_leaves = static_cast<int32_t>(true_num_leaves);
+    a.num_real_nodes = static_cast<int32_t>(true_num_real_nodes);
+    a.num_leaves2 = static_cast<int32_t>(false_num_leaves);
+    a.num_real_nodes2 = static_cast<int32_t>(false_num_real_nodes);
+    a.out_indices = out_indices;
+    a.out_distances = out_distances;
+    a.spatial_output = true;
+    TBVH_TRY(op, launch_knn(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_accel, const float* queries,
+                                  const uint8_t* routes, const int64_t* order, int64_t B, int64_t M,
+                                  int64_t true_num_leaves, int64_t false_num_leaves, int D, int k,
+                                  int64_t* out_indices, float* out_distances, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_routed_spatial";
+    if (int r = check_routed(op, B, M, true_num_leaves, false_num_leaves, kMaxAccelCloud, D, k)) return r;
+    if (M == 0) return ok();
+    if (!true_accel || !false_accel || !queries || !routes || !order || !out_indices || !out_distances) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    KnnArgs a{};
+    a.queries = queries;
+    a.order = order;
+    a.routes = routes;
+    a.B = B;
+    a.M = M;
+    a.total_q = B * M;
+    a.num_leaves = static_cast<int32_t>(true_num_leaves);
+    a.num_leaves2 = static_cast<int32_t>(false_num_leaves);
+    a.accel = true_accel;
+    a.accel2 = false_accel;
+    a.total_points = B * true_num_leaves;
+    a.out_indices = out_indices;
+    a.out_distances = out_distances;
+    a.spatial_output = true;
+    TBVH_TRY(op, launch_knn_accel(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
     return ok();
 }
 

@@ -82,8 +82,21 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
     const int64_t qi = kOrdered ? a.order[qbase + local] : local;
     if (qi < 0 || qi >= qcount) return;  // a corrupt order never indexes out of range
     const int64_t row = qbase + qi;
-    const float* nodes = a.node_aabbs + nstart * 2 * D;
-    const int64_t* sorted = a.sorted_indices + pstart;
+    const float* node_base = a.node_aabbs;
+    const int64_t* sorted_base = a.sorted_indices;
+    int64_t index_offset = 0;
+    if (!kRagged && a.routes != nullptr && a.routes[row] == 0) {
+        // False route (knn_query.cu:205-217): the second tree, indices after
+        // the first tree's points.
+        index_offset = n;
+        n = a.num_leaves2;
+        pstart = seg * static_cast<int64_t>(n);
+        nstart = seg * static_cast<int64_t>(a.num_real_nodes2);
+        node_base = a.node_aabbs2;
+        sorted_base = a.sorted_indices2;
+    }
+    const float* nodes = node_base + nstart * 2 * D;
+    const int64_t* sorted = sorted_base + pstart;
 
     float q[D];
 #pragma unroll
@@ -146,7 +159,8 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
     float* od = a.out_distances + out_row * K;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-        oi[i] = static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(best[i])));
+        const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+        oi[i] = idx >= 0 ? idx + index_offset : idx;
         od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
     }
 }
@@ -276,9 +290,20 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     const int64_t qi = kOrdered ? a.order[qbase + local] : local;
     if (qi < 0 || qi >= qcount) return;
     const int64_t row = qbase + qi;
-    const float4* pts = static_cast<const float4*>(a.accel) + pstart;
-    const float* recs = reinterpret_cast<const float*>(static_cast<const char*>(a.accel) +
-                                                       accel_points_bytes(a.total_points)) +
+    const void* accel = a.accel;
+    int64_t total_points = a.total_points;
+    int64_t index_offset = 0;
+    if (!kRagged && a.routes != nullptr && a.routes[row] == 0) {
+        // False route: the second structure, indices after the first's points.
+        index_offset = n;
+        n = a.num_leaves2;
+        pstart = seg * static_cast<int64_t>(n);
+        accel = a.accel2;
+        total_points = a.B * static_cast<int64_t>(n);
+    }
+    const float4* pts = static_cast<const float4*>(accel) + pstart;
+    const float* recs = reinterpret_cast<const float*>(static_cast<const char*>(accel) +
+                                                       accel_points_bytes(total_points)) +
                         (pstart - seg) * R;
 
     float q[D];
@@ -381,7 +406,8 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     float* od = a.out_distances + out_row * K;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-        oi[i] = static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(best[i])));
+        const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+        oi[i] = idx >= 0 ? idx + index_offset : idx;
         od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
     }
 }

@@ -183,6 +183,18 @@ hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* seg
                               int64_t total, const uint32_t* sorted_codes, void* accel,
                               hipStream_t stream);
 
+// Routed query ordering (route.hip): route digits + per-cloud histogram;
+// partitioned queries, 2B group segments and bounds; final query order.
+hipError_t launch_route_keys(const uint8_t* routes, const Segment* segs, int64_t S, int64_t tiles,
+                             uint32_t* keys, uint32_t* hist, hipStream_t stream);
+hipError_t launch_route_gather(const float* queries, const int64_t* part, const uint32_t* hist, int64_t B,
+                               int64_t M, int D, const float* true_min, const float* true_max,
+                               const float* false_min, const float* false_max, float* gathered,
+                               int64_t* group_offsets, float* group_min, float* group_max,
+                               hipStream_t stream);
+hipError_t launch_route_finish(const int64_t* part, const int64_t* sorted_local, const int64_t* group_offsets,
+                               int64_t B, int64_t M, int64_t* order, hipStream_t stream);
+
 // k-NN traversal.
 struct KnnArgs {
     const float* node_aabbs;
@@ -202,6 +214,14 @@ struct KnnArgs {
     const void* accel;             // accelerated traversal only
     int64_t total_points;          // accelerated traversal only
     bool spatial_output;           // write row `launch position` instead of `query index`
+    // Routed traversal (batched only): a query whose route is false searches
+    // the second structure and its indices are offset by num_leaves.
+    const uint8_t* routes;         // null: not routed
+    const float* node_aabbs2;      // implicit tree of the false route
+    const int64_t* sorted_indices2;
+    const void* accel2;            // accel of the false route
+    int32_t num_leaves2;
+    int32_t num_real_nodes2;
 };
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
