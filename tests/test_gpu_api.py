@@ -299,3 +299,66 @@ def test_quickstart_config1_end_to_end():
     ei, ed = oracle.knn(w["points"].numpy(), w["queries"].numpy(), 4)
     assert_same_int(neighbors.cpu().numpy(), ei, "cfg1 indices")
     assert_same_f32(distances_sq.cpu().numpy(), ed, "cfg1 distances")
+
+
+def _displaced_inputs(B=2, N=24, H=3, D=3, C=4, seed=20500):
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand((B, N, D), generator=g)
+    pos = pos + 8.0 * torch.arange(B, dtype=torch.float32).view(B, 1, 1)
+    q = pos[:, :, None, :] + 0.015 * torch.randn((B, N, H, D), generator=g)
+    values = torch.randn((B, N, H, C), generator=g)
+    return pos.to(DEV).contiguous(), q.to(DEV).contiguous(), values.to(DEV).contiguous()
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_query_displaced_knn_matches_flattened_batched_query(dim):
+    """tests/test_displaced_query.py:88-150: local indices, ascending
+    distances, positions of the returned points; identical to one batched
+    query over the flattened heads."""
+    pos, q, _ = _displaced_inputs(B=3, N=28, H=2, D=dim)
+    idx, d2, npos = tb.query_displaced_knn(pos, q, 4)
+    assert idx.shape == (3, 28, 2, 4) and d2.shape == (3, 28, 2, 4) and npos.shape == (3, 28, 2, 4, dim)
+    assert int(idx.min()) >= 0 and int(idx.max()) < 28
+    assert torch.all(d2[..., :-1] <= d2[..., 1:])
+    b = torch.arange(3, device=DEV).view(3, 1, 1, 1)
+    assert torch.equal(npos, pos[b, idx])
+    fi, fd = tb.query_knn(tb.build_bvh(pos), q.reshape(3, 56, dim), 4)
+    assert torch.equal(idx, fi.reshape(3, 28, 2, 4)) and torch.equal(d2, fd.reshape(3, 28, 2, 4))
+    i2, dd2 = tb.query_displaced_knn(pos, q, 4, return_positions=False)
+    assert torch.equal(i2, idx) and torch.equal(dd2, d2)
+    with pytest.raises(ValueError, match="k must be"):
+        tb.query_displaced_knn(pos, q, 5)
+
+
+def test_gather_neighbor_values_uses_matching_head_only():
+    values = torch.arange(2 * 5 * 3 * 2, dtype=torch.float32, device=DEV).reshape(2, 5, 3, 2)
+    idx = torch.tensor([4, 0, 2, 1], device=DEV).expand(2, 5, 3, 4).contiguous()
+    out = tb.gather_neighbor_values(values, idx)
+    assert out.shape == (2, 5, 3, 4, 2)
+    for b in range(2):
+        for h in range(3):
+            assert torch.equal(out[b, :, h], values[b, idx[b, :, h], h])
+    with pytest.raises(ValueError, match="local source indices"):
+        tb.gather_neighbor_values(values, idx + 5)
+
+
+def test_interpolate_displaced_weighted_mean_and_exact_hits():
+    """Weighted mean w = 1/(d2 + 1e-12) normalised; exact hits average."""
+    pos, q, values = _displaced_inputs(B=2, N=20, H=3, D=3, C=5, seed=7)
+    q[:, :, 0] = pos  # head 0 hits its own point exactly
+    out = tb.interpolate_displaced(pos, q, values, 4)
+    idx, d2 = tb.query_displaced_knn(pos, q, 4, return_positions=False)
+    nv = tb.gather_neighbor_values(values, idx)
+    w = torch.reciprocal(d2 + 1e-12)
+    w = w / w.sum(-1, keepdim=True).clamp(min=1e-12)
+    want = torch.zeros_like(values)
+    for r in range(4):
+        want = want + nv[..., r, :] * w[..., r].unsqueeze(-1)
+    exact = d2 <= 1e-12
+    ex = torch.zeros_like(values)
+    for r in range(4):
+        ex = ex + nv[..., r, :] * exact[..., r].float().unsqueeze(-1)
+    ex = ex / exact.float().sum(-1, keepdim=True).clamp(min=1.0)
+    want = torch.where(exact.any(-1, keepdim=True), ex, want)
+    assert torch.equal(out, want)
+    assert exact[:, :, 0, 0].all()  # head 0's nearest neighbour is its own point

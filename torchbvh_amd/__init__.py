@@ -12,6 +12,7 @@ from ._bvh_class import BVH
 from ._constants import SUPPORTED_DIMS, SUPPORTED_K
 from ._geometry import PointGeometry
 from ._handles import BVHHandle, BatchedBVHHandle, RaggedBVHHandle, destroy_bvh
+from ._multihead import gather_neighbor_values, interpolate_displaced, query_displaced_knn
 from ._native import _C
 from ._query import build_bvh, query_knn
 
@@ -26,6 +27,9 @@ __all__ = [
     "build_bvh",
     "destroy_bvh",
     "query_knn",
+    "query_displaced_knn",
+    "gather_neighbor_values",
+    "interpolate_displaced",
     "SUPPORTED_K",
     "SUPPORTED_DIMS",
 ]
