@@ -119,6 +119,34 @@ int tbvh_build_ragged_with_accel(const float* points, const int64_t* offsets,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* ---- primitive build ----------------------------------------------------------
+ * Replaces `build_primitive_bvh_batched` (torchbvh/csrc/bindings.cpp:159-160,
+ * torchbvh/csrc/bvh_build.cu:60-93, 757-821; used by `_ray.py:195`):
+ * `primitives` is [B, F, V, D] float32, (V, D) = (2, 2) segments or (3, 3)
+ * triangles.  Leaves are the primitives' vertex boxes; each cloud's bounds
+ * are the min / max of those boxes' corners; the Morton codes are of the
+ * centres (vertex sum / V) against those bounds.  Outputs as tbvh_build,
+ * with F in place of N.  The sort is stable (the reference's is not: the
+ * orders agree wherever centre codes are distinct). */
+int tbvh_build_primitives_workspace_size(int64_t B, int64_t F, int V, int D, size_t* bytes);
+int tbvh_build_primitives(const float* primitives, int64_t B, int64_t F, int V, int D,
+                          float* node_aabbs, int64_t* sorted_indices,
+                          float* scene_min, float* scene_max,
+                          int32_t* left_child_mem, int32_t* right_child_mem,
+                          int32_t* mem_to_leaf,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- point ordering -----------------------------------------------------------
+ * Replaces `morton_sort_points_batched` (torchbvh/csrc/bindings.cpp:194,
+ * torchbvh/csrc/bvh_build.cu:723-740; used by `_fps.py:112, 190`): each
+ * cloud's bounds, 30/32-bit Morton codes against them and the stable order,
+ * `sorted_indices` [B, N] int64 (cloud-local) -- the `sorted_indices` of
+ * tbvh_build without the tree. */
+int tbvh_morton_sort_points_workspace_size(int64_t B, int64_t N, int D, size_t* bytes);
+int tbvh_morton_sort_points(const float* points, int64_t B, int64_t N, int D,
+                            int64_t* sorted_indices,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- query ordering -----------------------------------------------------------
  * Replaces `morton_sort_queries_narrow` (torchbvh/csrc/morton_sort.cu:212-287):
  * Morton codes of the queries against the BVH's scene bounds, stable sort,

@@ -51,6 +51,8 @@ def lib():
         L.orc_bounds.argtypes = [_f32p, c_i64, c_int, _f32p, _f32p]
         L.orc_stable_argsort.argtypes = [_u32p, c_i64, _i64p]
         L.orc_build.argtypes = [_f32p, c_int, c_int, _f32p, _i64p, _f32p, _f32p, _i32p, _i32p, _i32p]
+        L.orc_build_primitives.argtypes = [_f32p, c_int, c_int, c_int, _f32p, _i64p, _f32p, _f32p, _i32p,
+                                           _i32p, _i32p, _f32p]
         L.orc_knn_brute.argtypes = [_f32p, c_i64, _f32p, c_i64, c_int, c_int, _i64p, _f32p]
         L.orc_knn_bvh.argtypes = [_f32p, _i64p, c_int, _f32p, c_i64, c_int, c_int, _i64p, _f32p]
         L.orc_point_dist.argtypes = [_f32p, _f32p, c_int]
@@ -187,6 +189,30 @@ def schedule_order(queries, scene_min, scene_max) -> np.ndarray:
     bits = 30 if q.shape[1] == 3 else 32
     codes = morton_codes(q, scene_min, scene_max).astype(np.uint64)
     return stable_argsort((codes >> np.uint64(bits - 16)).astype(np.uint32))
+
+
+def build_primitives(primitives) -> dict:
+    """Primitive build of one sample ((n, V, D): 2-D segments or 3-D
+    triangles; torchbvh/csrc/bvh_build.cu:60-93, 757-821), with the centres."""
+    p = _f32(primitives)
+    n, V, D = p.shape
+    nr = real_node_count(n)
+    out = {
+        "node_aabbs": np.empty((nr, 2 * D), np.float32),
+        "sorted_indices": np.empty(n, np.int64),
+        "scene_min": np.empty(D, np.float32),
+        "scene_max": np.empty(D, np.float32),
+        "left_child_mem": np.empty(nr, np.int32),
+        "right_child_mem": np.empty(nr, np.int32),
+        "mem_to_leaf": np.empty(nr, np.int32),
+        "centers": np.empty((n, D), np.float32),
+    }
+    lib().orc_build_primitives(p, n, V, D, out["node_aabbs"], out["sorted_indices"], out["scene_min"],
+                               out["scene_max"], out["left_child_mem"], out["right_child_mem"],
+                               out["mem_to_leaf"], out["centers"])
+    out.update(num_leaves=n, num_real_nodes=nr, leaf_level=leaf_level(n), virtual_leaves=virtual_leaves(n),
+               dim=D)
+    return out
 
 
 def routed_order(queries, routes, true_min, true_max, false_min, false_max) -> np.ndarray:

@@ -146,14 +146,10 @@ void orc_stable_argsort(const uint32_t* keys, int64_t n, int64_t* perm) {
  * whose right child is virtual copies its left child), :361-398
  * (traversal arrays).  One cloud of n points.
  * ---------------------------------------------------------------------- */
-void orc_build(const float* pts, int n, int D, float* node_aabbs, int64_t* sorted,
-               float* scene_lo, float* scene_hi, int32_t* left, int32_t* right, int32_t* leaf) {
-    orc_bounds(pts, n, D, scene_lo, scene_hi);
-    uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
-    orc_morton_codes(pts, n, D, scene_lo, scene_hi, codes);
-    orc_stable_argsort(codes, n, sorted);
-    free(codes);
-
+/* Node AABBs and traversal arrays over `sorted` leaves whose boxes are
+ * leaf_boxes[sorted[j]] (2D floats each, by original index). */
+static void build_nodes(const float* leaf_boxes, int n, int D, const int64_t* sorted, float* node_aabbs,
+                        int32_t* left, int32_t* right, int32_t* leaf) {
     const int L = orc_leaf_level(n);
     const int W = 2 * D;
     const int first_leaf = (1 << L) - 1;
@@ -165,8 +161,7 @@ void orc_build(const float* pts, int n, int D, float* node_aabbs, int64_t* sorte
             float* box = node_aabbs + (int64_t)orc_memory_index(n, i) * W;
             const int row = orc_memory_index(n, i);
             if (level == L) {
-                const float* p = pts + sorted[i - first_leaf] * D;
-                for (int d = 0; d < D; ++d) { box[d] = p[d]; box[D + d] = p[d]; }
+                memcpy(box, leaf_boxes + sorted[i - first_leaf] * W, sizeof(float) * (size_t)W);
                 left[row] = -1;
                 right[row] = -1;
                 leaf[row] = i - first_leaf;
@@ -189,6 +184,60 @@ void orc_build(const float* pts, int n, int D, float* node_aabbs, int64_t* sorte
             }
         }
     }
+}
+
+void orc_build(const float* pts, int n, int D, float* node_aabbs, int64_t* sorted,
+               float* scene_lo, float* scene_hi, int32_t* left, int32_t* right, int32_t* leaf) {
+    orc_bounds(pts, n, D, scene_lo, scene_hi);
+    uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    orc_morton_codes(pts, n, D, scene_lo, scene_hi, codes);
+    orc_stable_argsort(codes, n, sorted);
+    free(codes);
+    /* leaf = the point's degenerate box */
+    float* boxes = (float*)malloc(sizeof(float) * (size_t)n * 2 * D);
+    for (int j = 0; j < n; ++j)
+        for (int d = 0; d < D; ++d) boxes[(int64_t)j * 2 * D + d] = boxes[(int64_t)j * 2 * D + D + d] = pts[(int64_t)j * D + d];
+    build_nodes(boxes, n, D, sorted, node_aabbs, left, right, leaf);
+    free(boxes);
+}
+
+/* ------------------------------------------------------------------------
+ * Primitive build — torchbvh/csrc/bvh_build.cu:61-93 (per primitive: vertex
+ * min/max box and centre = sequential vertex sum / V), :789-791 (scene
+ * bounds = min of the boxes' lower corners, max of their upper corners),
+ * :793-800 (Morton codes of the centres, sorted; here stably, ties by
+ * primitive index), :801-811 (node AABBs with the primitive boxes as
+ * leaves).  One sample of n primitives of V vertices in D dimensions.
+ * ---------------------------------------------------------------------- */
+void orc_build_primitives(const float* prims, int n, int V, int D, float* node_aabbs, int64_t* sorted,
+                          float* scene_lo, float* scene_hi, int32_t* left, int32_t* right, int32_t* leaf,
+                          float* centers_out) {
+    const int W = 2 * D;
+    float* boxes = (float*)malloc(sizeof(float) * (size_t)n * W);
+    for (int d = 0; d < D; ++d) { scene_lo[d] = INFINITY; scene_hi[d] = -INFINITY; }
+    for (int j = 0; j < n; ++j) {
+        const float* p = prims + (int64_t)j * V * D;
+        for (int d = 0; d < D; ++d) {
+            float lo = p[d], hi = p[d], sum = p[d];
+            for (int v = 1; v < V; ++v) {
+                const float x = p[v * D + d];
+                lo = fminf(lo, x);
+                hi = fmaxf(hi, x);
+                sum += x;
+            }
+            centers_out[(int64_t)j * D + d] = sum / (float)V;
+            boxes[(int64_t)j * W + d] = lo;
+            boxes[(int64_t)j * W + D + d] = hi;
+            scene_lo[d] = fminf(scene_lo[d], lo);
+            scene_hi[d] = fmaxf(scene_hi[d], hi);
+        }
+    }
+    uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    orc_morton_codes(centers_out, n, D, scene_lo, scene_hi, codes);
+    orc_stable_argsort(codes, n, sorted);
+    free(codes);
+    build_nodes(boxes, n, D, sorted, node_aabbs, left, right, leaf);
+    free(boxes);
 }
 
 /* ------------------------------------------------------------------------

@@ -173,3 +173,32 @@ def test_spatial_knn_requires_an_order():
     assert "null" in _err(L)
     assert L.tbvh_knn_accel_spatial(FAKE, FAKE, FAKE, 1, 10, 100, 3, 5, FAKE, FAKE, None) == 1
     assert "k must be" in _err(L)
+
+
+def test_primitive_build_and_point_sort_argument_errors():
+    L = _native.load()
+    size = ctypes.c_size_t()
+    # Only 2-D segments and 3-D triangles.
+    for V, D in ((3, 2), (2, 3), (4, 3), (1, 1)):
+        assert L.tbvh_build_primitives_workspace_size(1, 10, V, D, ctypes.byref(size)) == 1
+        assert "expected 2-D segments or 3-D triangles" in _err(L)
+    assert L.tbvh_build_primitives_workspace_size(0, 10, 3, 3, ctypes.byref(size)) == 1
+    assert L.tbvh_build_primitives_workspace_size(2, 1000, 3, 3, ctypes.byref(size)) == 0
+    need = size.value
+    # The centres and leaf boxes are workspace: more than the point build's.
+    point_size = ctypes.c_size_t()
+    assert L.tbvh_build_workspace_size(2, 1000, 3, ctypes.byref(point_size)) == 0
+    assert need >= point_size.value + 2 * 1000 * 9 * 4
+    outs = [FAKE] * 7
+    assert L.tbvh_build_primitives(None, 2, 1000, 3, 3, *outs, FAKE, need, None) == 1
+    assert "null" in _err(L)
+    assert L.tbvh_build_primitives(FAKE, 2, 1000, 3, 3, *outs, FAKE, need - 1, None) == 2
+    assert L.tbvh_build_primitives(FAKE, 2, 1000, 3, 3, *outs, ctypes.c_void_p(0x100010), need,
+                                   None) == 1
+    assert "aligned" in _err(L)
+    # Point ordering: bounds live in the workspace after the build layout.
+    assert L.tbvh_morton_sort_points_workspace_size(2, 1000, 4, ctypes.byref(size)) == 1
+    assert L.tbvh_morton_sort_points_workspace_size(2, 1000, 3, ctypes.byref(size)) == 0
+    assert size.value > point_size.value
+    assert L.tbvh_morton_sort_points(FAKE, 2, 1000, 3, None, FAKE, size.value, None) == 1
+    assert L.tbvh_morton_sort_points(FAKE, 2, 1000, 3, FAKE, FAKE, size.value - 1, None) == 2

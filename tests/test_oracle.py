@@ -210,7 +210,7 @@ def test_bounds_match_numpy_and_seed_semantics():
 def check_build(points: np.ndarray) -> dict:
     n, D = points.shape
     b = oracle.build(points)
-    L, real, rank = brute_tree(n)
+    L, real, _ = brute_tree(n)
     nr = int(real.sum())
     nodes = b["node_aabbs"]
     assert nodes.shape == (nr, 2 * D)
@@ -223,15 +223,24 @@ def check_build(points: np.ndarray) -> dict:
     codes = oracle.morton_codes(points, lo, hi)
     assert_same_int(b["sorted_indices"], np.argsort(codes, kind="stable"), "sorted_indices")
     sp = points[b["sorted_indices"]]
+    check_tree(b, sp, sp)
+    return b
+
+
+def check_tree(b: dict, leaf_lo: np.ndarray, leaf_hi: np.ndarray) -> None:
+    """Every real node's box is the union of its leaf range's boxes (leaf
+    boxes in sorted order); traversal arrays follow the heap."""
+    n, D = leaf_lo.shape
+    L, real, rank = brute_tree(n)
+    nodes = b["node_aabbs"]
     first_leaf = (1 << L) - 1
     for i in np.nonzero(real)[0]:
         level = int(i + 1).bit_length() - 1
         span = 1 << (L - level)
         a = (i - ((1 << level) - 1)) * span
-        leaves = sp[a:min(a + span, n)]
         box = nodes[rank[i]]
-        assert_same_f32(box[:D], leaves.min(0), f"node {i} lo")
-        assert_same_f32(box[D:], leaves.max(0), f"node {i} hi")
+        assert_same_f32(box[:D], leaf_lo[a:min(a + span, n)].min(0), f"node {i} lo")
+        assert_same_f32(box[D:], leaf_hi[a:min(a + span, n)].max(0), f"node {i} hi")
         row = rank[i]
         if i >= first_leaf:
             assert b["left_child_mem"][row] == -1 and b["right_child_mem"][row] == -1
@@ -240,7 +249,6 @@ def check_build(points: np.ndarray) -> dict:
             assert b["left_child_mem"][row] == rank[2 * i + 1]
             assert b["right_child_mem"][row] == (rank[2 * i + 2] if real[2 * i + 2] else -1)
             assert b["mem_to_leaf"][row] == -1
-    return b
 
 
 @pytest.mark.parametrize("case", range(len(pathological_clouds())))
@@ -268,6 +276,76 @@ def test_build_random(n, dim):
 def test_build_degenerate_extent_is_constant():
     b = check_build(np.array([[7.0, -3.0]] * 3, np.float32))
     assert np.all(b["node_aabbs"] == np.array([7.0, -3.0, 7.0, -3.0], np.float32))
+
+
+# ---------------------------------------------------------------------------
+# Primitive build: numpy boxes / centres / bounds, brute-force node boxes,
+# and the reduction to the point build for degenerate primitives
+# ---------------------------------------------------------------------------
+def check_build_primitives(prims: np.ndarray) -> dict:
+    n, V, D = prims.shape
+    b = oracle.build_primitives(prims)
+    L, real, _ = brute_tree(n)
+    assert b["node_aabbs"].shape == (int(real.sum()), 2 * D) and b["leaf_level"] == L
+    box_lo, box_hi = prims.min(1), prims.max(1)
+    centers = prims[:, 0, :].copy()
+    for v in range(1, V):
+        centers = centers + prims[:, v, :]  # float32, vertex order
+    centers = centers / np.float32(V)
+    assert_same_f32(b["centers"], centers, "centers")
+    lo, hi = box_lo.min(0), box_hi.max(0)
+    assert_same_f32(b["scene_min"], lo, "scene_min")
+    assert_same_f32(b["scene_max"], hi, "scene_max")
+    codes = oracle.morton_codes(centers, lo, hi)
+    assert_same_int(b["sorted_indices"], np.argsort(codes, kind="stable"), "sorted_indices")
+    order = b["sorted_indices"]
+    check_tree(b, box_lo[order], box_hi[order])
+    return b
+
+
+def random_primitives(rng, n: int, V: int, D: int, spread: float = 0.05) -> np.ndarray:
+    """Primitives around random anchors in [-2, 2]^D, edges up to `spread`."""
+    anchor = rng.random((n, 1, D), dtype=np.float32) * 4 - 2
+    return (anchor + (rng.random((n, V, D), dtype=np.float32) - 0.5) * spread).astype(np.float32)
+
+
+@pytest.mark.parametrize("V,D", [(2, 2), (3, 3)])
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 16, 17, 37, 1000])
+def test_build_primitives_random(n, V, D):
+    check_build_primitives(random_primitives(np.random.default_rng(100 * n + D), n, V, D))
+
+
+@pytest.mark.parametrize("V,D", [(2, 2), (3, 3)])
+def test_build_primitives_long_overlapping_edges(V, D):
+    # Boxes spanning most of the scene: node boxes are far from the centres'.
+    rng = np.random.default_rng(7 + D)
+    check_build_primitives((rng.random((300, V, D), dtype=np.float32) * 4 - 2).astype(np.float32))
+
+
+@pytest.mark.parametrize("V,D", [(2, 2), (3, 3)])
+def test_build_primitives_degenerate_reduce_to_point_build(V, D):
+    # Every vertex equal, on a 1/64 grid: the vertex sum is exact, so the
+    # centre is the point and each leaf box is the point's; the primitive
+    # build must then equal the (separately pinned) point build field by field.
+    rng = np.random.default_rng(21 + D)
+    pts = (rng.integers(-128, 128, (513, D)) / 64.0).astype(np.float32)
+    prims = np.repeat(pts[:, None, :], V, axis=1)
+    pb, b = check_build_primitives(prims), oracle.build(pts)
+    for key in ("node_aabbs", "scene_min", "scene_max"):
+        assert_same_f32(pb[key], b[key], key)
+    for key in ("sorted_indices", "left_child_mem", "right_child_mem", "mem_to_leaf"):
+        assert_same_int(pb[key], b[key], key)
+
+
+def test_build_primitives_bounds_take_box_corners_not_centres():
+    # Two segments whose centres coincide: scene bounds still cover the
+    # vertices, and both leaves carry their own boxes.
+    prims = np.array([[[0.0, 0.0], [2.0, 2.0]], [[0.0, 2.0], [2.0, 0.0]]], np.float32)
+    b = check_build_primitives(prims)
+    assert_same_f32(b["scene_min"], np.zeros(2, np.float32), "scene_min")
+    assert_same_f32(b["scene_max"], np.full(2, 2.0, np.float32), "scene_max")
+    assert_same_f32(b["centers"], np.ones((2, 2), np.float32), "centers")
+    assert_same_int(b["sorted_indices"], np.array([0, 1]), "equal codes keep input order")
 
 
 # ---------------------------------------------------------------------------

@@ -54,6 +54,12 @@ def _declare(L) -> None:
     L.tbvh_build_ragged_with_accel.argtypes = (
         [_vp, _vp, _i64, _i64, _int] + [_vp] * 8 + [_i64, _vp, _vp, ctypes.c_size_t, _vp]
     )
+    L.tbvh_build_primitives_workspace_size.argtypes = [_i64, _i64, _int, _int, _szp]
+    L.tbvh_build_primitives.argtypes = (
+        [_vp, _i64, _i64, _int, _int] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]
+    )
+    L.tbvh_morton_sort_points_workspace_size.argtypes = [_i64, _i64, _int, _szp]
+    L.tbvh_morton_sort_points.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_sort_queries_workspace_size.argtypes = [_i64, _i64, _int, _szp]
     L.tbvh_sort_queries.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_sort_queries_ragged_workspace_size.argtypes = [_i64, _i64, _int, _szp]
@@ -100,6 +106,8 @@ def _declare(L) -> None:
         "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
         "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
+        "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
+        "tbvh_morton_sort_points_workspace_size", "tbvh_morton_sort_points",
     ):
         getattr(L, name).restype = _int
 
@@ -249,6 +257,72 @@ class _NativeOps:
         if with_accel:
             out["accel"] = accel
         return out
+
+    @staticmethod
+    def build_primitive_bvh_batched(primitives: torch.Tensor) -> dict:
+        """Batched BVH over segments (B, F, 2, 2) or triangles (B, F, 3, 3):
+        leaves are the primitives' vertex boxes, ordered by the Morton codes
+        of their centres (bvh_build.cu:757-821).  Same payload as the point
+        build, with F leaves per cloud."""
+        op = "build_primitive_bvh_batched"
+        _require_device_f32(op, primitives, "primitives")
+        _require(primitives.dim() == 4, op, "primitives must have shape (B, F, V, D)")
+        _require(primitives.size(0) >= 1, op, "batch size must be at least 1")
+        _require(primitives.size(1) >= 1, op, "each sample must contain at least one primitive")
+        B, F, V, D = (int(s) for s in primitives.shape)
+        _require((V, D) in ((2, 2), (3, 3)), op, "expected 2-D segments or 3-D triangles")
+        L = load()
+        dev = primitives.device
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_build_primitives_workspace_size, B, F, V, D)
+            nr = real_node_count(F)
+            node_aabbs = torch.empty((B, nr, 2 * D), dtype=torch.float32, device=dev)
+            sorted_indices = torch.empty((B, F), dtype=torch.int64, device=dev)
+            scene_min = torch.empty((B, D), dtype=torch.float32, device=dev)
+            scene_max = torch.empty((B, D), dtype=torch.float32, device=dev)
+            left = torch.empty(nr, dtype=torch.int32, device=dev)
+            right = torch.empty(nr, dtype=torch.int32, device=dev)
+            leaf = torch.empty(nr, dtype=torch.int32, device=dev)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_build_primitives(
+                _ptr(primitives), B, F, V, D, _ptr(node_aabbs), _ptr(sorted_indices),
+                _ptr(scene_min), _ptr(scene_max), _ptr(left), _ptr(right), _ptr(leaf),
+                _ptr(ws), ws.numel(), _stream(dev)))
+        return {
+            "node_aabbs": node_aabbs,
+            "sorted_indices": sorted_indices,
+            "scene_min": scene_min,
+            "scene_max": scene_max,
+            "batch_size": B,
+            "num_leaves": F,
+            "num_real_nodes": nr,
+            "leaf_level": leaf_level(F),
+            "virtual_leaves": virtual_leaves(F),
+            "dim": D,
+            "left_child_mem": left,
+            "right_child_mem": right,
+            "mem_to_leaf": leaf,
+        }
+
+    @staticmethod
+    def morton_sort_points_batched(points: torch.Tensor) -> torch.Tensor:
+        """Cloud-local Morton order of every cloud's points against its own
+        bounds (bvh_build.cu:723-740), as `sorted_indices` of the build."""
+        op = "morton_sort_points_batched"
+        _require(isinstance(points, torch.Tensor) and points.is_cuda and points.is_contiguous()
+                 and points.dtype == torch.float32, op, "points must be contiguous CUDA float32")
+        _require(points.dim() == 3 and points.size(0) >= 1 and points.size(1) >= 1
+                 and points.size(2) in (2, 3), op, "points must have shape (B, N, 2|3)")
+        L = load()
+        B, N, D = (int(s) for s in points.shape)
+        dev = points.device
+        with torch.cuda.device(dev):
+            ws_bytes = _size(L.tbvh_morton_sort_points_workspace_size, B, N, D)
+            order = torch.empty((B, N), dtype=torch.int64, device=dev)
+            ws = _workspace(ws_bytes, dev)
+            _check(L.tbvh_morton_sort_points(_ptr(points), B, N, D, _ptr(order), _ptr(ws), ws.numel(),
+                                             _stream(dev)))
+        return order
 
     @staticmethod
     def build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor,

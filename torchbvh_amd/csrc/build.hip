@@ -273,6 +273,93 @@ __global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Primitive preparation (primitive BVH)
+// ---------------------------------------------------------------------------
+// One work-group per tile of 4096 primitives (V vertices of D floats):
+// each primitive's vertex box and centre (sequential vertex sum / V,
+// bvh_build.cu:61-93), and the cloud's bounds as min of the boxes' lower
+// corners and max of their upper corners (bvh_build.cu:789-791, a reduction
+// with no seed values, so +-inf start it), finished by the last tile.
+template <int D, int V>
+__global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __restrict__ prims,
+                                                                const Segment* __restrict__ segs, int S,
+                                                                float* __restrict__ centers,
+                                                                float* __restrict__ boxes,
+                                                                float* __restrict__ partials,
+                                                                uint32_t* __restrict__ seg_done,
+                                                                float* __restrict__ scene_min,
+                                                                float* __restrict__ scene_max) {
+    __shared__ int s_seg;
+    __shared__ int s_last;
+    __shared__ float s_red[kBlock / kWave][2 * D];
+    __shared__ float s_out[2 * D];
+    const int64_t t = blockIdx.x;
+    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
+                                     S, t, &s_seg);
+    const Segment g = segs[s];
+    const int lt = static_cast<int>(t - g.tile_first);
+    if (lt >= g.tiles) return;
+    const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
+    const int count = min(kSortTile, g.n - lt * kSortTile);
+    float lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) { lo[d] = INFINITY; hi[d] = -INFINITY; }
+    for (int j = threadIdx.x; j < count; j += kBlock) {
+        const int64_t row = row0 + j;
+        const float* p = prims + row * V * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            float b_lo = p[d], b_hi = p[d], sum = p[d];
+#pragma unroll
+            for (int v = 1; v < V; ++v) {
+                const float x = p[v * D + d];
+                b_lo = fminf(b_lo, x);
+                b_hi = fmaxf(b_hi, x);
+                sum += x;
+            }
+            centers[row * D + d] = sum / static_cast<float>(V);
+            boxes[row * 2 * D + d] = b_lo;
+            boxes[row * 2 * D + D + d] = b_hi;
+            lo[d] = fminf(lo[d], b_lo);
+            hi[d] = fmaxf(hi[d], b_hi);
+        }
+    }
+    block_box<D>(lo, hi, s_red, s_out);
+    if (g.tiles == 1) {
+        if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
+        else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
+        return;
+    }
+    if (threadIdx.x < 2 * D) {
+        partials[t * 2 * D + threadIdx.x] = s_out[threadIdx.x];
+        __threadfence();
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prior = __hip_atomic_fetch_add(seg_done + s, 1u, __ATOMIC_ACQ_REL,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prior == static_cast<uint32_t>(g.tiles - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+#pragma unroll
+    for (int d = 0; d < D; ++d) { lo[d] = INFINITY; hi[d] = -INFINITY; }
+    for (int j = threadIdx.x; j < g.tiles; j += kBlock) {
+        const float* p = partials + (static_cast<int64_t>(g.tile_first) + j) * 2 * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            lo[d] = fminf(lo[d], p[d]);
+            hi[d] = fmaxf(hi[d], p[D + d]);
+        }
+    }
+    __syncthreads();
+    block_box<D>(lo, hi, s_red, s_out);
+    if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
+    else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
+}
+
+// ---------------------------------------------------------------------------
 // Morton codes + all sort passes' digit histograms
 // ---------------------------------------------------------------------------
 // One work-group per tile.  Digit counts of the sort passes are gathered
@@ -397,12 +484,19 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
             if constexpr (kFromPoints) {
                 // Clamped so a corrupt permutation cannot read outside the cloud.
                 const int64_t idx = min(max(sorted[g.start + j], int64_t(0)), int64_t(g.n - 1));
-                const float* pt = points + (g.start + idx) * D;
+                if (out.leaf_boxes) {
+                    // Primitive BVH: the leaf is the primitive's box.
+                    const float* box = out.leaf_boxes + (g.start + idx) * 2 * D;
 #pragma unroll
-                for (int d = 0; d < D; ++d) {
-                    const float v = pt[d];
-                    dst[d] = v;
-                    dst[D + d] = v;
+                    for (int c = 0; c < 2 * D; ++c) dst[c] = box[c];
+                } else {
+                    const float* pt = points + (g.start + idx) * D;
+#pragma unroll
+                    for (int d = 0; d < D; ++d) {
+                        const float v = pt[d];
+                        dst[d] = v;
+                        dst[D + d] = v;
+                    }
                 }
                 if (arrays) {
                     out.left[arr0 + row] = -1;
@@ -496,6 +590,24 @@ hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_
         bounds_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, partials, seg_done, scene_min, scene_max);
     } else {
         bounds_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, partials, seg_done, scene_min, scene_max);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment* segs, int64_t S,
+                                 int64_t tiles, float* centers, float* boxes, float* partials,
+                                 uint32_t* seg_done, float* scene_min, float* scene_max,
+                                 hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>(tiles);
+    const int Si = static_cast<int>(S);
+    if (D == 3 && V == 3) {
+        primitive_prep_kernel<3, 3><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials,
+                                                                 seg_done, scene_min, scene_max);
+    } else if (D == 2 && V == 2) {
+        primitive_prep_kernel<2, 2><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials,
+                                                                 seg_done, scene_min, scene_max);
+    } else {
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

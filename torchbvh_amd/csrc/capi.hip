@@ -53,11 +53,12 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 // clears them in one sweep.
 struct Layout {
     size_t segs = 0, partials = 0, keys_a = 0, keys_b = 0, vals_a = 0, vals_b = 0;
-    size_t clear = 0, total = 0;
+    size_t clear = 0, centers = 0, boxes = 0, total = 0;
     int64_t tiles = 0, clear_words = 0;
 };
 
-Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials) {
+// `with_primitives` adds the primitive build's centres and leaf boxes.
+Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials, bool with_primitives = false) {
     Layout l;
     l.tiles = tiles_bound(rows, S);
     l.clear_words = sort_clear_words(S, l.tiles);
@@ -69,6 +70,9 @@ Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials) {
     l.vals_a = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.vals_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.clear = at; at = align_up(at + static_cast<size_t>(l.clear_words) * 4);
+    const size_t prim_floats = with_primitives ? static_cast<size_t>(rows) * D : 0;
+    l.centers = at; at = align_up(at + prim_floats * sizeof(float));
+    l.boxes = at; at = align_up(at + 2 * prim_floats * sizeof(float));
     l.total = at;
     return l;
 }
@@ -127,10 +131,11 @@ int full_key_bits(int D) { return D == 3 ? 30 : 32; }
 SortBits full_sort(int D) { return SortBits{0, full_key_bits(D)}; }
 SortBits schedule_sort(int D) { return SortBits{full_key_bits(D) - 16, full_key_bits(D)}; }
 
-// Everything one build call launches, in order: plan (+ clear), bounds,
-// Morton (+ all pass histograms), four sort passes, implicit-tree passes
-// (+ traversal arrays, + accel points) and, when `accel` is given, the
-// accel's radix-tree records.
+// Everything one build call launches, in order: plan (+ clear), bounds
+// (primitive builds: boxes, centres and bounds), Morton (+ all pass
+// histograms), four sort passes, implicit-tree passes (+ traversal arrays,
+// + accel points) and, when `accel` is given, the accel's radix-tree
+// records.  `sort_only` stops after the sort.
 struct BuildOut {
     float* node_aabbs;
     int64_t* sorted_indices;
@@ -141,11 +146,14 @@ struct BuildOut {
     int32_t* leaf;
     int64_t* node_offsets;  // ragged only
     void* accel;            // optional
+    bool sort_only = false;
 };
 
+// `V` > 0: `points` holds primitives of V vertices each, and the leaves are
+// their boxes; the Morton codes are the centres' against the boxes' bounds.
 hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int64_t n_uniform,
-                     int64_t rows, int D, const BuildOut& o, void* ws, hipStream_t stream) {
-    const Layout l = make_layout(S, rows, D, true);
+                     int64_t rows, int D, const BuildOut& o, void* ws, hipStream_t stream, int V = 0) {
+    const Layout l = make_layout(S, rows, D, true, V > 0);
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l, S);
     const bool ragged = offsets != nullptr;
@@ -155,8 +163,18 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
                                                 stream);
     if (e != hipSuccess) return e;
     float* partials = carve<float>(ws, l.partials);
-    if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, sb.seg_done, o.scene_min,
-                           o.scene_max, stream)) != hipSuccess) {
+    const float* boxes = nullptr;
+    if (V > 0) {
+        float* centers = carve<float>(ws, l.centers);
+        float* leaf_boxes = carve<float>(ws, l.boxes);
+        if ((e = launch_primitive_prep(points, D, V, segs, S, l.tiles, centers, leaf_boxes, partials,
+                                       sb.seg_done, o.scene_min, o.scene_max, stream)) != hipSuccess) {
+            return e;
+        }
+        points = centers;
+        boxes = leaf_boxes;
+    } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, sb.seg_done, o.scene_min,
+                                  o.scene_max, stream)) != hipSuccess) {
         return e;
     }
     const SortBits bits = full_sort(D);
@@ -168,12 +186,14 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
     if ((e = launch_sort(segs, S, l.tiles, bits, sb, o.sorted_indices, sorted_keys, stream)) != hipSuccess) {
         return e;
     }
+    if (o.sort_only) return hipSuccess;
     TreeOutputs to;
     to.left = o.left;
     to.right = o.right;
     to.leaf = o.leaf;
     to.arrays_packed = ragged;
     to.accel_points = o.accel ? static_cast<float4*>(o.accel) : nullptr;
+    to.leaf_boxes = boxes;
     const int64_t max_n = ragged ? (rows < kMaxCloud ? rows : kMaxCloud) : n_uniform;
     if ((e = launch_tree(points, D, segs, S, rows, max_n, o.sorted_indices, o.node_aabbs, to,
                          stream)) != hipSuccess) {
@@ -341,6 +361,77 @@ int tbvh_build_ragged_with_accel(const float* points, const int64_t* offsets, in
                      right_child_mem, mem_to_leaf, node_offsets, accel};
     return build_ragged("tbvh_build_ragged_with_accel", points, offsets, B, total, D, o, total_nodes,
                         workspace, workspace_bytes, stream_ptr);
+}
+
+// ---------------------------------------------------------------------------
+// Primitive build and point ordering
+// ---------------------------------------------------------------------------
+static int check_primitive_shape(const char* op, int64_t B, int64_t F, int V, int D) {
+    if (!((V == 2 && D == 2) || (V == 3 && D == 3))) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: expected 2-D segments or 3-D triangles", op);
+    }
+    return check_batched_extent(op, B, F);
+}
+
+int tbvh_build_primitives_workspace_size(int64_t B, int64_t F, int V, int D, size_t* bytes) {
+    const char* op = "tbvh_build_primitives_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_primitive_shape(op, B, F, V, D)) return r;
+    *bytes = make_layout(B, B * F, D, true, true).total;
+    return ok();
+}
+
+int tbvh_build_primitives(const float* primitives, int64_t B, int64_t F, int V, int D, float* node_aabbs,
+                          int64_t* sorted_indices, float* scene_min, float* scene_max,
+                          int32_t* left_child_mem, int32_t* right_child_mem, int32_t* mem_to_leaf,
+                          void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_build_primitives";
+    if (int r = check_primitive_shape(op, B, F, V, D)) return r;
+    if (!primitives || !node_aabbs || !sorted_indices || !scene_min || !scene_max || !left_child_mem ||
+        !right_child_mem || !mem_to_leaf) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const Layout l = make_layout(B, B * F, D, true, true);
+    if (int r = check_workspace(op, workspace, workspace_bytes, l.total)) return r;
+    const BuildOut o{node_aabbs, sorted_indices, scene_min, scene_max, left_child_mem,
+                     right_child_mem, mem_to_leaf, nullptr, nullptr};
+    TBVH_TRY(op, run_build(primitives, nullptr, B, F, B * F, D, o, workspace,
+                           static_cast<hipStream_t>(stream_ptr), V));
+    return ok();
+}
+
+// The point ordering needs the clouds' bounds only in the workspace: they
+// sit after the build layout.
+static size_t point_sort_bytes(int64_t B, int64_t N, int D, size_t* bounds_at) {
+    const size_t at = make_layout(B, B * N, D, true).total;
+    if (bounds_at) *bounds_at = at;
+    return at + align_up(2 * static_cast<size_t>(B) * D * sizeof(float));
+}
+
+int tbvh_morton_sort_points_workspace_size(int64_t B, int64_t N, int D, size_t* bytes) {
+    const char* op = "tbvh_morton_sort_points_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: bytes is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    *bytes = point_sort_bytes(B, N, D, nullptr);
+    return ok();
+}
+
+int tbvh_morton_sort_points(const float* points, int64_t B, int64_t N, int D, int64_t* sorted_indices,
+                            void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_morton_sort_points";
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    if (!points || !sorted_indices) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    size_t bounds_at = 0;
+    if (int r = check_workspace(op, workspace, workspace_bytes, point_sort_bytes(B, N, D, &bounds_at))) return r;
+    float* scene_min = carve<float>(workspace, bounds_at);
+    float* scene_max = scene_min + B * D;
+    BuildOut o{nullptr, sorted_indices, scene_min, scene_max, nullptr, nullptr, nullptr, nullptr, nullptr};
+    o.sort_only = true;
+    TBVH_TRY(op, run_build(points, nullptr, B, N, B * N, D, o, workspace,
+                           static_cast<hipStream_t>(stream_ptr)));
+    return ok();
 }
 
 // ---------------------------------------------------------------------------

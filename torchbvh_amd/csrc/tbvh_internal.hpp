@@ -134,6 +134,13 @@ struct SortBits {
     int passes() const { return (end_bit - first_bit + kRadixBits - 1) / kRadixBits; }
 };
 
+// Primitive BVH input: every primitive's box and centre, and each cloud's
+// bounds over the boxes (seg_done / partials as in launch_bounds).
+hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment* segs, int64_t S,
+                                 int64_t tiles, float* centers, float* boxes, float* partials,
+                                 uint32_t* seg_done, float* scene_min, float* scene_max,
+                                 hipStream_t stream);
+
 // Morton codes of every row against its segment's bounds, plus the
 // per-segment digit histogram of every pass of `bits` (`hist`, zeroed
 // beforehand).
@@ -157,6 +164,7 @@ struct TreeOutputs {
     int32_t* leaf;
     bool arrays_packed;    // ragged: per-segment arrays at node_start; batched: segment 0 only
     float4* accel_points;  // Morton-ordered float4 points for the accel (null: not written)
+    const float* leaf_boxes = nullptr;  // primitive BVH: [rows, 2D] leaf boxes (null: point leaves)
 };
 
 // Implicit-tree node AABBs (all passes), optionally the traversal arrays and
