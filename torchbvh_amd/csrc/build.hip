@@ -1,5 +1,5 @@
 // BVH build kernels: segment planning, per-cloud bounds, Morton codes (with
-// every sort pass's digit histograms), implicit-tree node AABBs, fused with
+// the first sort digit's tile counts), implicit-tree node AABBs, fused with
 // the traversal arrays and the accel's Morton-ordered points.
 //
 // Reference behaviour followed (torchbvh/csrc/bvh_build.cu):
@@ -137,15 +137,6 @@ __global__ __launch_bounds__(kBlock) void plan_offsets_kernel(Segment* segs, con
         }
     }
     if (node_offsets && threadIdx.x == 0) node_offsets[S] = carry_nodes;
-}
-
-// Segment owning work item `x` of a per-segment range table, found by one
-// thread and broadcast through LDS.
-template <typename F>
-__device__ __forceinline__ int block_find_segment(F firsts, int S, int64_t x, int* s_seg) {
-    if (threadIdx.x == 0) *s_seg = find_segment(firsts, S, x);
-    __syncthreads();
-    return *s_seg;
 }
 
 // ---------------------------------------------------------------------------
@@ -360,31 +351,34 @@ __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// Morton codes + all sort passes' digit histograms
+// Morton codes + the first sort digit's tile counts
 // ---------------------------------------------------------------------------
-// One work-group per tile.  Digit counts of the sort passes are gathered
-// with LDS atomics, then added to the segment's global histograms with one
-// device atomic per non-zero bin.
+// One work-group per tile (the sort's tiles).  Digit counts are gathered
+// with LDS atomics and stored digit-major; surplus tiles store zeros.
 template <int D>
 __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict__ points,
                                                         const Segment* __restrict__ segs, int S,
                                                         const float* __restrict__ scene_min,
                                                         const float* __restrict__ scene_max,
                                                         uint32_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ hist,
-                                                        int first_bit, int passes) {
+                                                        uint32_t* __restrict__ tile_hist, int64_t tstride,
+                                                        int first_bit) {
+    static_assert(kBlock == kRadix, "one thread per digit");
     __shared__ int s_seg;
-    __shared__ uint32_t s_hist[kMaxSortPasses][kRadix];
+    __shared__ uint32_t s_hist[kRadix];
     __shared__ float s_pts[kSortTile * D];
     const int64_t t = blockIdx.x;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
                                      S, t, &s_seg);
     const Segment g = segs[s];
     const int lt = static_cast<int>(t - g.tile_first);
-    if (lt >= g.tiles) return;
+    if (lt >= g.tiles) {
+        if (tile_hist) tile_hist[threadIdx.x * tstride + t] = 0u;
+        return;
+    }
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
-    for (int i = threadIdx.x; i < kMaxSortPasses * kRadix; i += kBlock) (&s_hist[0][0])[i] = 0u;
+    s_hist[threadIdx.x] = 0u;
     // Stage the tile's points in LDS with coalesced loads.
     constexpr int kF = kSortTile * D / kBlock;
     const int nf = count * D;
@@ -411,18 +405,10 @@ __global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict_
         for (int d = 0; d < D; ++d) p[d] = s_pts[j * D + d];
         const uint32_t code = morton::encode<D>(p, lo, hi);
         keys[row0 + j] = code;
-#pragma unroll
-        for (int pass = 0; pass < kMaxSortPasses; ++pass) {
-            if (pass < passes) {
-                atomicAdd(&s_hist[pass][(code >> (first_bit + pass * kRadixBits)) & (kRadix - 1)], 1u);
-            }
-        }
+        if (tile_hist) atomicAdd(&s_hist[(code >> first_bit) & (kRadix - 1)], 1u);
     }
     __syncthreads();
-    for (int pass = 0; pass < passes; ++pass) {
-        const uint32_t c = s_hist[pass][threadIdx.x];
-        if (c) atomicAdd(hist + (static_cast<int64_t>(pass) * S + s) * kRadix + threadIdx.x, c);
-    }
+    if (tile_hist) tile_hist[threadIdx.x * tstride + t] = s_hist[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
@@ -614,16 +600,15 @@ hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment
 
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S, int64_t tiles,
                          const float* scene_min, const float* scene_max, uint32_t* keys,
-                         uint32_t* hist, SortBits bits, hipStream_t stream) {
+                         uint32_t* tile_hist, int64_t tstride, SortBits bits, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
-    const int passes = bits.passes();
     if (D == 3) {
-        morton_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist,
-                                                      bits.first_bit, passes);
+        morton_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
+                                                      tstride, bits.first_bit);
     } else {
-        morton_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, hist,
-                                                      bits.first_bit, passes);
+        morton_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
+                                                      tstride, bits.first_bit);
     }
     return hipGetLastError();
 }

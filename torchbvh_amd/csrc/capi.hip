@@ -48,20 +48,20 @@ constexpr int64_t kMaxRows = 2147483647;  // INT32_MAX
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-// Workspace carve-out shared by build and query sort.  The histogram,
-// look-back status and ticket words are contiguous: the planning kernel
-// clears them in one sweep.
+// Workspace carve-out shared by build and query sort.  Only the bounds
+// counters (`clear`) need zeroing; the planning kernel clears them.
 struct Layout {
     size_t segs = 0, partials = 0, keys_a = 0, keys_b = 0, vals_a = 0, vals_b = 0;
-    size_t clear = 0, centers = 0, boxes = 0, total = 0;
-    int64_t tiles = 0, clear_words = 0;
+    size_t tile_hist = 0, tile_scan = 0, clear = 0, centers = 0, boxes = 0, total = 0;
+    int64_t tiles = 0, tstride = 0, clear_words = 0;
 };
 
 // `with_primitives` adds the primitive build's centres and leaf boxes.
 Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials, bool with_primitives = false) {
     Layout l;
     l.tiles = tiles_bound(rows, S);
-    l.clear_words = sort_clear_words(S, l.tiles);
+    l.tstride = tile_stride(l.tiles);
+    l.clear_words = sort_clear_words(S);
     size_t at = 0;
     l.segs = at; at = align_up(at + static_cast<size_t>(S) * sizeof(Segment));
     l.partials = at; at = align_up(at + (with_partials ? static_cast<size_t>(l.tiles) * 2 * D * sizeof(float) : 0));
@@ -69,6 +69,8 @@ Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials, bool with
     l.keys_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.vals_a = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.vals_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
+    l.tile_hist = at; at = align_up(at + static_cast<size_t>(kRadix) * l.tstride * 4);
+    l.tile_scan = at; at = align_up(at + static_cast<size_t>(kRadix) * l.tstride * 4);
     l.clear = at; at = align_up(at + static_cast<size_t>(l.clear_words) * 4);
     const size_t prim_floats = with_primitives ? static_cast<size_t>(rows) * D : 0;
     l.centers = at; at = align_up(at + prim_floats * sizeof(float));
@@ -82,16 +84,16 @@ T* carve(void* ws, size_t off) {
     return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-SortBuffers sort_buffers(void* ws, const Layout& l, int64_t S) {
+SortBuffers sort_buffers(void* ws, const Layout& l) {
     SortBuffers b;
     b.keys_a = carve<uint32_t>(ws, l.keys_a);
     b.keys_b = carve<uint32_t>(ws, l.keys_b);
     b.vals_a = carve<uint32_t>(ws, l.vals_a);
     b.vals_b = carve<uint32_t>(ws, l.vals_b);
-    b.hist = carve<uint32_t>(ws, l.clear);
-    b.status = b.hist + static_cast<int64_t>(kMaxSortPasses) * S * kRadix;
-    b.tickets = b.status + static_cast<int64_t>(kMaxSortPasses) * l.tiles * kRadix;
-    b.seg_done = b.tickets + kMaxSortPasses + 1;
+    b.tile_hist = carve<uint32_t>(ws, l.tile_hist);
+    b.tile_scan = carve<uint32_t>(ws, l.tile_scan);
+    b.seg_done = carve<uint32_t>(ws, l.clear);
+    b.tstride = l.tstride;
     return b;
 }
 
@@ -132,10 +134,11 @@ SortBits full_sort(int D) { return SortBits{0, full_key_bits(D)}; }
 SortBits schedule_sort(int D) { return SortBits{full_key_bits(D) - 16, full_key_bits(D)}; }
 
 // Everything one build call launches, in order: plan (+ clear), bounds
-// (primitive builds: boxes, centres and bounds), Morton (+ all pass
-// histograms), four sort passes, implicit-tree passes (+ traversal arrays,
-// + accel points) and, when `accel` is given, the accel's radix-tree
-// records.  `sort_only` stops after the sort.
+// (primitive builds: boxes, centres and bounds), Morton (+ the first
+// digit's tile counts), four sort passes (count, scan, scatter),
+// implicit-tree passes (+ traversal arrays, + accel points) and, when
+// `accel` is given, the accel's radix-tree records.  `sort_only` stops
+// after the sort.
 struct BuildOut {
     float* node_aabbs;
     int64_t* sorted_indices;
@@ -155,11 +158,11 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
                      int64_t rows, int D, const BuildOut& o, void* ws, hipStream_t stream, int V = 0) {
     const Layout l = make_layout(S, rows, D, true, V > 0);
     Segment* segs = carve<Segment>(ws, l.segs);
-    const SortBuffers sb = sort_buffers(ws, l, S);
+    const SortBuffers sb = sort_buffers(ws, l);
     const bool ragged = offsets != nullptr;
-    hipError_t e = ragged ? launch_plan_offsets(segs, offsets, S, true, o.node_offsets, sb.hist,
+    hipError_t e = ragged ? launch_plan_offsets(segs, offsets, S, true, o.node_offsets, sb.seg_done,
                                                 l.clear_words, stream)
-                          : launch_plan_uniform(segs, S, n_uniform, true, sb.hist, l.clear_words,
+                          : launch_plan_uniform(segs, S, n_uniform, true, sb.seg_done, l.clear_words,
                                                 stream);
     if (e != hipSuccess) return e;
     float* partials = carve<float>(ws, l.partials);
@@ -178,8 +181,8 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
         return e;
     }
     const SortBits bits = full_sort(D);
-    if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.hist,
-                           bits, stream)) != hipSuccess) {
+    if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.tile_hist,
+                           sb.tstride, bits, stream)) != hipSuccess) {
         return e;
     }
     uint32_t* sorted_keys = o.accel ? last_pass_keys(sb) : nullptr;
@@ -209,15 +212,15 @@ hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t 
                           hipStream_t stream) {
     const Layout l = make_layout(S, rows, D, false);
     Segment* segs = carve<Segment>(ws, l.segs);
-    const SortBuffers sb = sort_buffers(ws, l, S);
-    hipError_t e = offsets ? launch_plan_offsets(segs, offsets, S, false, nullptr, sb.hist,
+    const SortBuffers sb = sort_buffers(ws, l);
+    hipError_t e = offsets ? launch_plan_offsets(segs, offsets, S, false, nullptr, sb.seg_done,
                                                  l.clear_words, stream)
-                           : launch_plan_uniform(segs, S, m_uniform, false, sb.hist, l.clear_words,
+                           : launch_plan_uniform(segs, S, m_uniform, false, sb.seg_done, l.clear_words,
                                                  stream);
     if (e != hipSuccess) return e;
     uint32_t* keys = codes_only ? codes_only : sb.keys_a;
-    if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys, sb.hist, bits,
-                           stream)) != hipSuccess) {
+    if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys,
+                           codes_only ? nullptr : sb.tile_hist, sb.tstride, bits, stream)) != hipSuccess) {
         return e;
     }
     if (codes_only) return hipSuccess;
@@ -574,15 +577,18 @@ hipError_t run_routed_sort(const float* queries, const uint8_t* routes, int64_t 
     // 1. Stable partition of every cloud by route (one 8-bit pass on 0/1).
     const Layout l = make_layout(B, rows, D, false);
     Segment* segs = carve<Segment>(ws, l.segs);
-    const SortBuffers sb = sort_buffers(ws, l, B);
-    hipError_t e = launch_plan_uniform(segs, B, M, false, sb.hist, l.clear_words, stream);
+    const SortBuffers sb = sort_buffers(ws, l);
+    hipError_t e = launch_plan_uniform(segs, B, M, false, sb.seg_done, l.clear_words, stream);
     if (e != hipSuccess) return e;
-    if ((e = launch_route_keys(routes, segs, B, l.tiles, sb.keys_a, sb.hist, stream)) != hipSuccess) return e;
+    if ((e = launch_route_keys(routes, segs, B, l.tiles, sb.keys_a, sb.tile_hist, sb.tstride, stream)) !=
+        hipSuccess) {
+        return e;
+    }
     if ((e = launch_sort(segs, B, l.tiles, SortBits{0, kRadixBits}, sb, part, nullptr, stream)) != hipSuccess) {
         return e;
     }
     // 2. Partitioned queries as 2B segments (false group, true group per cloud).
-    if ((e = launch_route_gather(queries, part, sb.hist, B, M, D, true_min, true_max, false_min, false_max,
+    if ((e = launch_route_gather(queries, part, segs, sb.tile_scan, B, M, D, true_min, true_max, false_min, false_max,
                                  gathered, group_offsets, gmin, gmax, stream)) != hipSuccess) {
         return e;
     }

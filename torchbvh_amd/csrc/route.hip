@@ -17,48 +17,48 @@
 namespace tbvh {
 namespace {
 
-// Route digits (0/1) of every query and their per-cloud histogram.
+// Route digits (0/1) of every query and each tile's digit counts (the
+// sort's first-pass input: [digit][tile], zero beyond digit 1 and for
+// surplus tiles).
 __global__ __launch_bounds__(kBlock) void route_keys_kernel(const uint8_t* __restrict__ routes,
                                                             const Segment* __restrict__ segs, int S,
                                                             uint32_t* __restrict__ keys,
-                                                            uint32_t* __restrict__ hist) {
+                                                            uint32_t* __restrict__ tile_hist,
+                                                            int64_t tstride) {
+    static_assert(kBlock == kRadix, "one thread per digit");
     __shared__ int s_seg;
-    __shared__ uint32_t s_count[2];
+    __shared__ uint32_t s_ones;
     const int64_t t = blockIdx.x;
-    if (threadIdx.x == 0) {
-        s_seg = find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); }, S, t);
-        s_count[0] = 0u;
-        s_count[1] = 0u;
-    }
-    __syncthreads();
-    const int s = s_seg;
+    if (threadIdx.x == 0) s_ones = 0u;
+    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
+                                     S, t, &s_seg);
     const Segment g = segs[s];
     const int lt = static_cast<int>(t - g.tile_first);
-    if (lt >= g.tiles) return;
-    const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
-    const int count = min(kSortTile, g.n - lt * kSortTile);
-    uint32_t ones = 0;
-    for (int j = threadIdx.x; j < count; j += kBlock) {
-        const uint32_t r = routes[row0 + j] != 0 ? 1u : 0u;
-        keys[row0 + j] = r;
-        ones += r;
+    int count = 0;
+    if (lt < g.tiles) {
+        const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
+        count = min(kSortTile, g.n - lt * kSortTile);
+        uint32_t ones = 0;
+        for (int j = threadIdx.x; j < count; j += kBlock) {
+            const uint32_t r = routes[row0 + j] != 0 ? 1u : 0u;
+            keys[row0 + j] = r;
+            ones += r;
+        }
+        ones = wave_sum(ones);
+        if (lane_id() == 0) atomicAdd(&s_ones, ones);
     }
-    ones = wave_sum(ones);
-    if (lane_id() == 0) atomicAdd(&s_count[1], ones);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t c1 = s_count[1];
-        const uint32_t c0 = static_cast<uint32_t>(count) - c1;
-        if (c0) atomicAdd(hist + static_cast<int64_t>(s) * kRadix + 0, c0);
-        if (c1) atomicAdd(hist + static_cast<int64_t>(s) * kRadix + 1, c1);
-    }
+    const uint32_t c1 = s_ones;
+    const uint32_t c = threadIdx.x == 0 ? static_cast<uint32_t>(count) - c1 : (threadIdx.x == 1 ? c1 : 0u);
+    tile_hist[threadIdx.x * tstride + t] = c;
 }
 
 // Queries in partitioned order, the 2B group segments and their bounds.
 template <int D>
 __global__ __launch_bounds__(kBlock) void route_gather_kernel(
-    const float* __restrict__ queries, const int64_t* __restrict__ part, const uint32_t* __restrict__ hist,
-    int64_t B, int64_t M, const float* __restrict__ true_min, const float* __restrict__ true_max,
+    const float* __restrict__ queries, const int64_t* __restrict__ part, const Segment* __restrict__ segs,
+    const uint32_t* __restrict__ tile_scan, int64_t B, int64_t M, const float* __restrict__ true_min,
+    const float* __restrict__ true_max,
     const float* __restrict__ false_min, const float* __restrict__ false_max, float* __restrict__ gathered,
     int64_t* __restrict__ group_offsets, float* __restrict__ group_min, float* __restrict__ group_max) {
     const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -68,7 +68,10 @@ __global__ __launch_bounds__(kBlock) void route_gather_kernel(
 #pragma unroll
     for (int d = 0; d < D; ++d) gathered[j * D + d] = queries[(b * M + m) * D + d];
     if (j - b * M == 0) {
-        const int64_t c0 = hist[b * kRadix + 0];  // false queries of cloud b
+        // False queries of cloud b: digit 0's count over the cloud's tiles
+        // (row 0 of the route sort's tile scan).
+        const Segment g = segs[b];
+        const int64_t c0 = tile_scan[g.tile_first + g.tiles] - tile_scan[g.tile_first];
         group_offsets[2 * b] = b * M;
         group_offsets[2 * b + 1] = b * M + c0;
         if (b == B - 1) group_offsets[2 * B] = B * M;
@@ -104,25 +107,26 @@ inline unsigned grid_for(int64_t items) { return static_cast<unsigned>((items + 
 }  // namespace
 
 hipError_t launch_route_keys(const uint8_t* routes, const Segment* segs, int64_t S, int64_t tiles,
-                             uint32_t* keys, uint32_t* hist, hipStream_t stream) {
+                             uint32_t* keys, uint32_t* tile_hist, int64_t tstride, hipStream_t stream) {
     route_keys_kernel<<<static_cast<unsigned>(tiles), kBlock, 0, stream>>>(routes, segs, static_cast<int>(S),
-                                                                           keys, hist);
+                                                                           keys, tile_hist, tstride);
     return hipGetLastError();
 }
 
-hipError_t launch_route_gather(const float* queries, const int64_t* part, const uint32_t* hist, int64_t B,
+hipError_t launch_route_gather(const float* queries, const int64_t* part, const Segment* segs,
+                               const uint32_t* tile_scan, int64_t B,
                                int64_t M, int D, const float* true_min, const float* true_max,
                                const float* false_min, const float* false_max, float* gathered,
                                int64_t* group_offsets, float* group_min, float* group_max,
                                hipStream_t stream) {
     if (D == 3) {
         route_gather_kernel<3><<<grid_for(B * M), kBlock, 0, stream>>>(
-            queries, part, hist, B, M, true_min, true_max, false_min, false_max, gathered, group_offsets,
-            group_min, group_max);
+            queries, part, segs, tile_scan, B, M, true_min, true_max, false_min, false_max, gathered,
+            group_offsets, group_min, group_max);
     } else {
         route_gather_kernel<2><<<grid_for(B * M), kBlock, 0, stream>>>(
-            queries, part, hist, B, M, true_min, true_max, false_min, false_max, gathered, group_offsets,
-            group_min, group_max);
+            queries, part, segs, tile_scan, B, M, true_min, true_max, false_min, false_max, gathered,
+            group_offsets, group_min, group_max);
     }
     return hipGetLastError();
 }

@@ -6,48 +6,35 @@
 // and equal keys keep ascending original (local) index — LSD passes of a
 // stable counting sort give exactly that.
 //
-// Design (gfx950): 8-bit digits, kSortTile = 4096 keys per tile, 256-thread
-// work-groups, tiles never straddle segments.  The Morton kernel accumulates
-// every pass's per-segment digit histogram, so each pass is one kernel
-// ("onesweep": Adinets & Merrill, 2022):
-//   1. the work-group takes the next tile ticket (tickets follow dispatch
-//      order, so every lower ticket belongs to a running or finished group);
-//   2. ranks its keys stably (wave64 ballot matching, striped order);
-//   3. publishes each digit's count, then looks back over earlier tiles of
-//      its segment, summing published counts until it meets an inclusive
-//      prefix, and publishes its own inclusive prefix;
-//   4. stages the tile in LDS in digit order and writes each digit run
-//      contiguously at segment start + digit start + prefix.
-// Status words pack flag and count in one 32-bit word and are read and
-// written with agent-scope atomics, so they are coherent across XCDs.  A
-// group publishes all its aggregates before it waits on anyone, so every
-// wait ends; the spin is also bounded and a shared abort flag ends all spins
-// at once should that bound ever be reached (the output is then invalid, but
-// the kernel exits).
+// Design (gfx950): 8-bit digits, kSortTile = 4096 keys per tile, tiles never
+// straddle segments.  Each pass is reduce-then-scan in three kernels, every
+// one of which reads only data published by an earlier kernel (plain cached
+// loads, no inter-work-group waiting):
+//   1. count: each tile's digit counts, digit-major [digit][tile] (for the
+//      first pass the key producer writes them: launch_morton /
+//      launch_route_keys);
+//   2. scan: one work-group per digit, exclusive scan along the tiles;
+//   3. scatter: each tile ranks its keys stably (wave64 ballot matching),
+//      takes its segment-relative digit offsets from the scan
+//      (scan[d][t] - scan[d][first tile of the segment]) and the segment's
+//      digit totals from the same array, stages the tile in LDS in digit
+//      order and writes each digit run contiguously.
+// Single-pass "onesweep" look-back was measured first: on MI355X its status
+// words must be agent-coherent, and their traffic beyond the per-XCD L2
+// cost 9-13 us of a 20-46 us pass (plus a contended ticket atomic).
 #include "tbvh_internal.hpp"
 
 namespace tbvh {
 namespace {
 
-// Work-group size of a sort pass: 8 waves share a 4096-key tile, so each
-// wave ranks 512 keys (measured on MI355X: ~10% faster per pass than 4
-// waves, no gain from 16).
+// Work-group size of the count and scatter kernels: 8 waves share a
+// 4096-key tile, so each wave ranks 512 keys.
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kItems = kSortTile / kThreads;  // keys per thread
 static_assert(kThreads >= kRadix && kSortTile % kThreads == 0, "sort tiling");
-constexpr uint32_t kFlagAggregate = 1u << 30;
-constexpr uint32_t kFlagPrefix = 2u << 30;
-constexpr uint32_t kCountMask = (1u << 30) - 1;
-constexpr int kSpinLimit = 1 << 20;
-
-__device__ __forceinline__ uint32_t load_status(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_status(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+constexpr int kScanThreads = 1024;
+constexpr int kScanItems = 4;
 
 // Lanes of the current wave holding the same digit as this lane (among
 // `valid` lanes).
@@ -62,10 +49,66 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
     return peers;
 }
 
+// Digit counts of one tile of `keys` (a pass after the first).  Surplus
+// tiles (past their segment's last) count nothing.
+__global__ __launch_bounds__(kThreads) void tile_count_kernel(const Segment* __restrict__ segs, int S,
+                                                              const uint32_t* __restrict__ keys, int shift,
+                                                              uint32_t* __restrict__ tile_hist,
+                                                              int64_t tstride) {
+    __shared__ int s_seg;
+    __shared__ uint32_t s_cnt[kRadix];
+    const int64_t t = blockIdx.x;
+    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
+                                     S, t, &s_seg);
+    if (threadIdx.x < kRadix) s_cnt[threadIdx.x] = 0u;
+    __syncthreads();
+    const Segment g = segs[s];
+    const int lt = static_cast<int>(t - g.tile_first);
+    if (lt < g.tiles) {
+        const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
+        const int count = min(kSortTile, g.n - lt * kSortTile);
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int pos = i * kThreads + threadIdx.x;
+            if (pos < count) atomicAdd(&s_cnt[(keys[row0 + pos] >> shift) & (kRadix - 1)], 1u);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < kRadix) tile_hist[threadIdx.x * tstride + t] = s_cnt[threadIdx.x];
+}
+
+// Exclusive scan of one digit's tile counts along the tiles (work-group
+// `digit`), in chunks of kScanThreads * kScanItems tiles.
+__global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(const uint32_t* __restrict__ tile_hist,
+                                                                 uint32_t* __restrict__ tile_scan,
+                                                                 int64_t tiles, int64_t tstride) {
+    __shared__ uint32_t s_scan[kScanThreads / kWave];
+    const uint32_t* in = tile_hist + blockIdx.x * tstride;
+    uint32_t* out = tile_scan + blockIdx.x * tstride;
+    uint32_t carry = 0;
+    for (int64_t base = 0; base < tiles; base += kScanThreads * kScanItems) {
+        const int64_t i0 = base + static_cast<int64_t>(threadIdx.x) * kScanItems;
+        uint32_t v[kScanItems];
+        uint32_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            v[k] = i0 + k < tiles ? in[i0 + k] : 0u;
+            sum += v[k];
+        }
+        uint32_t total = 0;
+        uint32_t run = carry + block_exclusive_sum<kScanThreads>(sum, s_scan, &total);
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            if (i0 + k < tiles) out[i0 + k] = run;
+            run += v[k];
+        }
+        carry += total;
+    }
+}
+
 template <bool kFirst, bool kLast>
-__global__ __launch_bounds__(kThreads) void onesweep_kernel(const Segment* __restrict__ segs, int S,
-                                                            int64_t tiles_total, SortPass pass) {
-    __shared__ int64_t s_tile;
+__global__ __launch_bounds__(kThreads) void scatter_kernel(const Segment* __restrict__ segs, int S,
+                                                           SortPass pass) {
     __shared__ int s_seg;
     __shared__ uint32_t s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
@@ -73,26 +116,14 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const Segment* __res
     __shared__ uint32_t s_start[kRadix];
     __shared__ uint32_t s_base[kRadix];
     __shared__ uint32_t s_scan[kWaves];
-    if (threadIdx.x == 0) {
-        const int64_t t = atomicAdd(pass.ticket, 1u);
-        s_tile = t;
-        s_seg = t < tiles_total
-                    ? find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); }, S, t)
-                    : 0;
-    }
+    const int64_t t = blockIdx.x;
+    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
+                                     S, t, &s_seg);
     for (int i = threadIdx.x; i < kWaves * kRadix; i += kThreads) (&s_cnt[0][0])[i] = 0u;
     __syncthreads();
-    const int64_t t = s_tile;
-    if (t >= tiles_total) return;
-    const Segment g = segs[s_seg];
+    const Segment g = segs[s];
     const int lt = static_cast<int>(t - g.tile_first);
-    uint32_t* status = pass.status + t * kRadix;
-    if (lt >= g.tiles) {
-        // A ticket past the segment's last tile (surplus grid): nothing to
-        // sort, but publish zero prefixes so no later tile can wait on it.
-        if (threadIdx.x < kRadix) store_status(status + threadIdx.x, kFlagPrefix);
-        return;
-    }
+    if (lt >= g.tiles) return;  // surplus tile
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
     const int shift = pass.shift;
@@ -112,6 +143,17 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const Segment* __res
             val[i] = valid ? pass.vals_in[row0 + pos] : 0u;
         }
     }
+    // Thread d < kRadix owns digit d.  Its scan entries depend only on the
+    // tile, so they are loaded together with the keys: the tiles of the
+    // segment before this one and the segment's total.
+    const int d = threadIdx.x;
+    uint32_t before_tiles = 0, seg_count = 0;
+    if (d < kRadix) {
+        const uint32_t* col = pass.tile_scan + d * pass.tstride;
+        const uint32_t seg0 = col[g.tile_first];
+        before_tiles = col[t] - seg0;
+        seg_count = col[g.tile_first + g.tiles] - seg0;
+    }
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const int pos = wave * kWave * kItems + i * kWave + lane;
@@ -127,9 +169,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const Segment* __res
     }
     __syncthreads();
 
-    // Thread d < kRadix owns digit d: tile count, publish, look back.
-    const int d = threadIdx.x;
-    uint32_t tile_count = 0, before_tiles = 0, seg_count = 0;
+    // The tile's count of digit d and the waves' offsets within it.
+    uint32_t tile_count = 0;
     if (d < kRadix) {
         uint32_t run = 0;
 #pragma unroll
@@ -139,33 +180,8 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const Segment* __res
             run += c;
         }
         tile_count = run;
-        if (lt == 0) {
-            store_status(status + d, kFlagPrefix | tile_count);
-        } else {
-            store_status(status + d, kFlagAggregate | tile_count);
-            for (int64_t j = t - 1;; --j) {
-                const uint32_t* other = pass.status + j * kRadix + d;
-                uint32_t v = load_status(other);
-                int spins = 0;
-                while ((v >> 30) == 0) {
-                    if (++spins > kSpinLimit) {
-                        store_status(pass.abort, 1u);
-                    }
-                    if ((spins & 63) == 0 && load_status(pass.abort) != 0u) {
-                        v = kFlagPrefix;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                    v = load_status(other);
-                }
-                before_tiles += v & kCountMask;
-                if ((v & ~kCountMask) == kFlagPrefix) break;
-            }
-            store_status(status + d, kFlagPrefix | ((before_tiles + tile_count) & kCountMask));
-        }
-        seg_count = pass.hist[static_cast<int64_t>(s_seg) * kRadix + d];
     }
-    // Digit starts of the segment from its global histogram; tile-local
+    // Digit starts of the segment from its digit totals; tile-local
     // digit starts from the tile counts (threads >= kRadix add zeros).
     const uint32_t digit_start = block_exclusive_sum<kThreads>(seg_count, s_scan);
     const uint32_t local_start = block_exclusive_sum<kThreads>(tile_count, s_scan);
@@ -216,28 +232,31 @@ hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles, SortBits b
     uint32_t* kout = b.keys_b;
     uint32_t* vout = b.vals_b;
     for (int p = 0; p < passes; ++p) {
+        const int shift = bits.first_bit + p * kRadixBits;
+        if (p > 0) {
+            tile_count_kernel<<<grid, kThreads, 0, stream>>>(segs, Si, kin, shift, b.tile_hist, b.tstride);
+        }
+        tile_scan_kernel<<<kRadix, kScanThreads, 0, stream>>>(b.tile_hist, b.tile_scan, tiles, b.tstride);
         SortPass pass;
         pass.keys_in = kin;
         pass.vals_in = vin;
         pass.keys_out = kout;
         pass.vals_out = vout;
         pass.idx_out = order;
-        pass.hist = b.hist + static_cast<int64_t>(p) * S * kRadix;
-        pass.status = b.status + static_cast<int64_t>(p) * tiles * kRadix;
-        pass.ticket = b.tickets + p;
-        pass.abort = b.tickets + kMaxSortPasses;
-        pass.shift = bits.first_bit + p * kRadixBits;
+        pass.tile_scan = b.tile_scan;
+        pass.tstride = b.tstride;
+        pass.shift = shift;
         const bool first = p == 0;
         const bool last = p == passes - 1;
         if (last) pass.keys_out = sorted_keys;
         if (first && last) {
-            onesweep_kernel<true, true><<<grid, kThreads, 0, stream>>>(segs, Si, tiles, pass);
+            scatter_kernel<true, true><<<grid, kThreads, 0, stream>>>(segs, Si, pass);
         } else if (first) {
-            onesweep_kernel<true, false><<<grid, kThreads, 0, stream>>>(segs, Si, tiles, pass);
+            scatter_kernel<true, false><<<grid, kThreads, 0, stream>>>(segs, Si, pass);
         } else if (last) {
-            onesweep_kernel<false, true><<<grid, kThreads, 0, stream>>>(segs, Si, tiles, pass);
+            scatter_kernel<false, true><<<grid, kThreads, 0, stream>>>(segs, Si, pass);
         } else {
-            onesweep_kernel<false, false><<<grid, kThreads, 0, stream>>>(segs, Si, tiles, pass);
+            scatter_kernel<false, false><<<grid, kThreads, 0, stream>>>(segs, Si, pass);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

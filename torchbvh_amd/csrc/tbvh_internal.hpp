@@ -71,46 +71,51 @@ __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* sc
     return before + incl - v;
 }
 
+// Segment owning work item `x` of a per-segment range table, found by one
+// thread and broadcast through LDS.
+template <typename F>
+__device__ __forceinline__ int block_find_segment(F firsts, int S, int64_t x, int* s_seg) {
+    if (threadIdx.x == 0) *s_seg = find_segment(firsts, S, x);
+    __syncthreads();
+    return *s_seg;
+}
+
 // ---------------------------------------------------------------------------
 // Launchers (host).  Every launcher enqueues on `stream` and returns the
 // launch status.
 // ---------------------------------------------------------------------------
-constexpr int kMaxSortPasses = 4;   // 32-bit keys, 8-bit digits
 
-// Sort scratch: ping-pong keys/values, per-pass digit histograms of every
-// segment ([pass][segment][digit]), per-pass look-back status words
-// ([pass][tile][digit]), per-pass tile tickets plus one abort word.
+// Sort scratch: ping-pong keys/values; the current pass's digit count of
+// every tile and its exclusive scan along the tiles, both digit-major
+// ([digit][tile], row stride `tstride`); the bounds counters.
 struct SortBuffers {
-    uint32_t* keys_a;   // input keys (Morton kernel output)
+    uint32_t* keys_a;     // input keys (Morton kernel output)
     uint32_t* keys_b;
     uint32_t* vals_a;
     uint32_t* vals_b;
-    uint32_t* hist;     // kMaxSortPasses * S * kRadix words
-    uint32_t* status;   // kMaxSortPasses * tiles_bound * kRadix words
-    uint32_t* tickets;  // kMaxSortPasses + 1 words
-    uint32_t* seg_done; // S words: bounds tiles finished per segment
+    uint32_t* tile_hist;  // kRadix * tstride words
+    uint32_t* tile_scan;  // kRadix * tstride words
+    uint32_t* seg_done;   // S words: bounds tiles finished per segment
+    int64_t tstride;      // >= tiles_bound, a multiple of 64
 };
 
-// One onesweep pass (device-side view).
+// Row stride of the digit-major tile arrays.
+inline int64_t tile_stride(int64_t tiles_bound) { return (tiles_bound + 63) / 64 * 64; }
+
+// One scatter pass (device-side view).
 struct SortPass {
     const uint32_t* keys_in;
     const uint32_t* vals_in;
     uint32_t* keys_out;
     uint32_t* vals_out;
     int64_t* idx_out;
-    const uint32_t* hist;   // this pass: [segment][digit]
-    uint32_t* status;       // this pass: [tile][digit]
-    uint32_t* ticket;
-    uint32_t* abort;
+    const uint32_t* tile_scan;  // [digit][tile], exclusive along tiles
+    int64_t tstride;
     int shift;
 };
 
-// Words the planning kernel clears: histograms, status words, tickets and
-// the bounds counters, contiguous from `hist` in that order.
-inline int64_t sort_clear_words(int64_t S, int64_t tiles) {
-    return static_cast<int64_t>(kMaxSortPasses) * S * kRadix +
-           static_cast<int64_t>(kMaxSortPasses) * tiles * kRadix + kMaxSortPasses + 1 + S;
-}
+// Words the planning kernel clears: the bounds counters (one per segment).
+inline int64_t sort_clear_words(int64_t S) { return S; }
 
 // Planning: fill the segment table and clear `clear_words` words at `clear`.
 hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, uint32_t* clear,
@@ -141,18 +146,20 @@ hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment
                                  uint32_t* seg_done, float* scene_min, float* scene_max,
                                  hipStream_t stream);
 
-// Morton codes of every row against its segment's bounds, plus the
-// per-segment digit histogram of every pass of `bits` (`hist`, zeroed
-// beforehand).
+// Morton codes of every row against its segment's bounds and, unless
+// `tile_hist` is null, every tile's count of the first sort digit (digit at
+// bits.first_bit; [digit][tile], row stride `tstride`, surplus tiles zero).
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles_bound, const float* scene_min, const float* scene_max,
-                         uint32_t* keys, uint32_t* hist, SortBits bits, hipStream_t stream);
+                         uint32_t* keys, uint32_t* tile_hist, int64_t tstride, SortBits bits,
+                         hipStream_t stream);
 
 // Stable LSD sort of (key, local index) per segment on the digits of
 // `bits`; writes int64 local indices in key order into `order` and, if
 // `sorted_keys` is non-null, the keys in that order (an even number of
 // passes leaves them in buf.keys_a).  Input keys are in buf.keys_a
-// (clobbered).
+// (clobbered); buf.tile_hist holds the first digit's tile counts (written
+// by the key producer, launch_morton or launch_route_keys).
 hipError_t launch_sort(const Segment* segs, int64_t S, int64_t tiles_bound, SortBits bits,
                        const SortBuffers& buf, int64_t* order, uint32_t* sorted_keys,
                        hipStream_t stream);
@@ -191,11 +198,13 @@ hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* seg
                               int64_t total, const uint32_t* sorted_codes, void* accel,
                               hipStream_t stream);
 
-// Routed query ordering (route.hip): route digits + per-cloud histogram;
-// partitioned queries, 2B group segments and bounds; final query order.
+// Routed query ordering (route.hip): route digits + their tile counts;
+// partitioned queries, 2B group segments and bounds (a cloud's false count
+// from the route sort's tile scan); final query order.
 hipError_t launch_route_keys(const uint8_t* routes, const Segment* segs, int64_t S, int64_t tiles,
-                             uint32_t* keys, uint32_t* hist, hipStream_t stream);
-hipError_t launch_route_gather(const float* queries, const int64_t* part, const uint32_t* hist, int64_t B,
+                             uint32_t* keys, uint32_t* tile_hist, int64_t tstride, hipStream_t stream);
+hipError_t launch_route_gather(const float* queries, const int64_t* part, const Segment* segs,
+                               const uint32_t* tile_scan, int64_t B,
                                int64_t M, int D, const float* true_min, const float* true_max,
                                const float* false_min, const float* false_max, float* gathered,
                                int64_t* group_offsets, float* group_min, float* group_max,
