@@ -75,37 +75,23 @@ __device__ inline void fill_segment(Segment& g, int64_t start, int n, bool with_
 }
 
 __global__ __launch_bounds__(kBlock) void plan_uniform_kernel(Segment* segs, int64_t S, int n,
-                                                              bool with_tree, uint32_t* clear,
-                                                              int64_t clear_words) {
+                                                              bool with_tree) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    const int64_t span = S > clear_words ? S : clear_words;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < span; i += stride) {
-        if (i < clear_words) clear[i] = 0u;
-        if (i < S) {
-            Segment g;
-            fill_segment(g, i * n, n, with_tree);
-            g.tile_first = static_cast<int32_t>(i * g.tiles);
-            g.node_start = i * g.nr;
-            for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(i * g.groups[p]);
-            segs[i] = g;
-        }
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < S; i += stride) {
+        Segment g;
+        fill_segment(g, i * n, n, with_tree);
+        g.tile_first = static_cast<int32_t>(i * g.tiles);
+        g.node_start = i * g.nr;
+        for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(i * g.groups[p]);
+        segs[i] = g;
     }
 }
 
-// Work-group 0 scans all segments in chunks of kBlock; the others clear.
+// One work-group scans all segments in chunks of kBlock.
 __global__ __launch_bounds__(kBlock) void plan_offsets_kernel(Segment* segs, const int64_t* offsets,
                                                               int64_t S, bool with_tree,
-                                                              int64_t* node_offsets, uint32_t* clear,
-                                                              int64_t clear_words) {
+                                                              int64_t* node_offsets) {
     __shared__ int64_t scratch[kBlock / kWave];
-    if (blockIdx.x > 0) {
-        const int64_t stride = static_cast<int64_t>(gridDim.x - 1) * kBlock;
-        for (int64_t i = static_cast<int64_t>(blockIdx.x - 1) * kBlock + threadIdx.x; i < clear_words;
-             i += stride) {
-            clear[i] = 0u;
-        }
-        return;
-    }
     int64_t carry_tiles = 0, carry_nodes = 0;
     int64_t carry_groups[kMaxTreePasses] = {0, 0, 0, 0};
     for (int64_t base = 0; base < S; base += kBlock) {
@@ -144,7 +130,7 @@ __global__ __launch_bounds__(kBlock) void plan_offsets_kernel(Segment* segs, con
 // ---------------------------------------------------------------------------
 // Block-wide min (c < D) / max (c >= D) of per-thread boxes; the result for
 // component c lands in out[c] for threads c < 2D.
-template <int D>
+template <int D, int kThreads = kBlock>
 __device__ __forceinline__ void block_box(float (&lo)[D], float (&hi)[D], float (*s_red)[2 * D],
                                           float* out) {
     const int wave = threadIdx.x / kWave;
@@ -161,21 +147,31 @@ __device__ __forceinline__ void block_box(float (&lo)[D], float (&hi)[D], float 
     if (threadIdx.x < 2 * D) {
         const int c = threadIdx.x;
         float v = s_red[0][c];
-        for (int w = 1; w < kBlock / kWave; ++w) v = c < D ? fminf(v, s_red[w][c]) : fmaxf(v, s_red[w][c]);
+        for (int w = 1; w < kThreads / kWave; ++w) v = c < D ? fminf(v, s_red[w][c]) : fmaxf(v, s_red[w][c]);
         out[c] = v;
     }
 }
 
+// Whole points as one load per lane (dwordx3 / dwordx2: a wave reads 64
+// consecutive points).
 template <int D>
-__global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict__ points,
-                                                        const Segment* __restrict__ segs, int S,
-                                                        float* __restrict__ partials,
-                                                        uint32_t* __restrict__ seg_done,
-                                                        float* __restrict__ scene_min,
-                                                        float* __restrict__ scene_max) {
+struct PointRow {
+    float v[D];
+};
+
+// Work-groups of the per-tile point kernels (bounds, Morton): 16 waves per
+// 4096-point tile, four points per thread.  (256 threads with 48 scalar
+// loads each ran at a third of the bandwidth: too few waves per CU to cover
+// the load latency.)
+constexpr int kTileThreads = 1024;
+constexpr int kTileRows = kSortTile / kTileThreads;
+
+template <int D>
+__global__ __launch_bounds__(kTileThreads) void bounds_kernel(const float* __restrict__ points,
+                                                              const Segment* __restrict__ segs, int S,
+                                                              float* __restrict__ partials) {
     __shared__ int s_seg;
-    __shared__ int s_last;
-    __shared__ float s_red[kBlock / kWave][2 * D];
+    __shared__ float s_red[kTileThreads / kWave][2 * D];
     __shared__ float s_out[2 * D];
     const int64_t t = blockIdx.x;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
@@ -185,70 +181,48 @@ __global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict_
     if (lt >= g.tiles) return;
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
-
-    // The tile's count*D floats are contiguous: thread t loads floats
-    // t, t + kBlock, ... (coalesced, all loads in flight at once).  Float f
-    // is component f % D; with kBlock = 256 the component of load i is
-    // (i * kBlock + t) % D, so accumulator a = (i * kBlock) % D is fixed at
-    // compile time and maps to component (a + t) % D.
-    constexpr int kF = kSortTile * D / kBlock;
-    const int nf = count * D;
-    const float* base = points + row0 * D;
-    float acc_lo[D], acc_hi[D];
+    const PointRow<D>* rows = reinterpret_cast<const PointRow<D>*>(points + row0 * D);
+    PointRow<D> r[kTileRows];
 #pragma unroll
-    for (int a = 0; a < D; ++a) { acc_lo[a] = kSeedLo; acc_hi[a] = kSeedHi; }
-    float v[kF];
-#pragma unroll
-    for (int i = 0; i < kF; ++i) {
-        const int f = i * kBlock + threadIdx.x;
-        v[i] = f < nf ? base[f] : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < kF; ++i) {
-        const int f = i * kBlock + threadIdx.x;
-        constexpr int kStep = kBlock % D;
-        const int a = (i * kStep) % D;
-        if (f < nf) {
-            acc_lo[a] = fminf(acc_lo[a], v[i]);
-            acc_hi[a] = fmaxf(acc_hi[a], v[i]);
-        }
+    for (int i = 0; i < kTileRows; ++i) {
+        const int j = i * kTileThreads + threadIdx.x;
+        if (j < count) r[i] = rows[j];
     }
     float lo[D], hi[D];
-    const int r = threadIdx.x % D;
-#pragma unroll
-    for (int c = 0; c < D; ++c) {
-        // accumulator holding component c: a with (a + r) % D == c
-        const int want = (c - r + D) % D;
-        lo[c] = acc_lo[0];
-        hi[c] = acc_hi[0];
-#pragma unroll
-        for (int a = 1; a < D; ++a) {
-            lo[c] = want == a ? acc_lo[a] : lo[c];
-            hi[c] = want == a ? acc_hi[a] : hi[c];
-        }
-    }
-    block_box<D>(lo, hi, s_red, s_out);
-    if (g.tiles == 1) {
-        // The whole cloud is this tile.
-        if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
-        else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
-        return;
-    }
-    if (threadIdx.x < 2 * D) {
-        partials[t * 2 * D + threadIdx.x] = s_out[threadIdx.x];
-        __threadfence();  // publish the partial before this tile is counted
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prior = __hip_atomic_fetch_add(seg_done + s, 1u, __ATOMIC_ACQ_REL,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prior == static_cast<uint32_t>(g.tiles - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // every other tile's partial is now visible
 #pragma unroll
     for (int d = 0; d < D; ++d) { lo[d] = kSeedLo; hi[d] = kSeedHi; }
+#pragma unroll
+    for (int i = 0; i < kTileRows; ++i) {
+        if (i * kTileThreads + static_cast<int>(threadIdx.x) < count) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                lo[d] = fminf(lo[d], r[i].v[d]);
+                hi[d] = fmaxf(hi[d], r[i].v[d]);
+            }
+        }
+    }
+    block_box<D, kTileThreads>(lo, hi, s_red, s_out);
+    if (threadIdx.x < 2 * D) partials[t * 2 * D + threadIdx.x] = s_out[threadIdx.x];
+}
+
+// Each cloud's bounds from its tiles' partial boxes (work-group = cloud),
+// seeded with (seed_lo, seed_hi).  A separate launch rather than "last tile
+// finishes": on MI355X the agent-scope release/acquire that pattern needs
+// writes back and invalidates the XCD's L2 once per tile, which measured
+// slower than the extra launch.
+template <int D>
+__global__ __launch_bounds__(kBlock) void bounds_final_kernel(const Segment* __restrict__ segs,
+                                                              const float* __restrict__ partials,
+                                                              float seed_lo, float seed_hi,
+                                                              float* __restrict__ scene_min,
+                                                              float* __restrict__ scene_max) {
+    __shared__ float s_red[kBlock / kWave][2 * D];
+    __shared__ float s_out[2 * D];
+    const int64_t s = blockIdx.x;
+    const Segment g = segs[s];
+    float lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) { lo[d] = seed_lo; hi[d] = seed_hi; }
     for (int j = threadIdx.x; j < g.tiles; j += kBlock) {
         const float* p = partials + (static_cast<int64_t>(g.tile_first) + j) * 2 * D;
 #pragma unroll
@@ -257,10 +231,9 @@ __global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict_
             hi[d] = fmaxf(hi[d], p[D + d]);
         }
     }
-    __syncthreads();  // s_red is reused
     block_box<D>(lo, hi, s_red, s_out);
-    if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
-    else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
+    if (threadIdx.x < D) scene_min[s * D + threadIdx.x] = s_out[threadIdx.x];
+    else if (threadIdx.x < 2 * D) scene_max[s * D + threadIdx.x - D] = s_out[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
@@ -268,20 +241,17 @@ __global__ __launch_bounds__(kBlock) void bounds_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // One work-group per tile of 4096 primitives (V vertices of D floats):
 // each primitive's vertex box and centre (sequential vertex sum / V,
-// bvh_build.cu:61-93), and the cloud's bounds as min of the boxes' lower
-// corners and max of their upper corners (bvh_build.cu:789-791, a reduction
-// with no seed values, so +-inf start it), finished by the last tile.
+// bvh_build.cu:61-93) and the tile's partial box; the cloud's bounds are
+// the min of the boxes' lower corners and max of their upper corners
+// (bvh_build.cu:789-791, a reduction with no seed values, so +-inf start
+// it), reduced by bounds_final_kernel.
 template <int D, int V>
 __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __restrict__ prims,
                                                                 const Segment* __restrict__ segs, int S,
                                                                 float* __restrict__ centers,
                                                                 float* __restrict__ boxes,
-                                                                float* __restrict__ partials,
-                                                                uint32_t* __restrict__ seg_done,
-                                                                float* __restrict__ scene_min,
-                                                                float* __restrict__ scene_max) {
+                                                                float* __restrict__ partials) {
     __shared__ int s_seg;
-    __shared__ int s_last;
     __shared__ float s_red[kBlock / kWave][2 * D];
     __shared__ float s_out[2 * D];
     const int64_t t = blockIdx.x;
@@ -316,38 +286,7 @@ __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __r
         }
     }
     block_box<D>(lo, hi, s_red, s_out);
-    if (g.tiles == 1) {
-        if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
-        else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
-        return;
-    }
-    if (threadIdx.x < 2 * D) {
-        partials[t * 2 * D + threadIdx.x] = s_out[threadIdx.x];
-        __threadfence();
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prior = __hip_atomic_fetch_add(seg_done + s, 1u, __ATOMIC_ACQ_REL,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prior == static_cast<uint32_t>(g.tiles - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-#pragma unroll
-    for (int d = 0; d < D; ++d) { lo[d] = INFINITY; hi[d] = -INFINITY; }
-    for (int j = threadIdx.x; j < g.tiles; j += kBlock) {
-        const float* p = partials + (static_cast<int64_t>(g.tile_first) + j) * 2 * D;
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            lo[d] = fminf(lo[d], p[d]);
-            hi[d] = fmaxf(hi[d], p[D + d]);
-        }
-    }
-    __syncthreads();
-    block_box<D>(lo, hi, s_red, s_out);
-    if (threadIdx.x < D) scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_out[threadIdx.x];
-    else if (threadIdx.x < 2 * D) scene_max[static_cast<int64_t>(s) * D + threadIdx.x - D] = s_out[threadIdx.x];
+    if (threadIdx.x < 2 * D) partials[t * 2 * D + threadIdx.x] = s_out[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
@@ -356,59 +295,52 @@ __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __r
 // One work-group per tile (the sort's tiles).  Digit counts are gathered
 // with LDS atomics and stored digit-major; surplus tiles store zeros.
 template <int D>
-__global__ __launch_bounds__(kBlock) void morton_kernel(const float* __restrict__ points,
-                                                        const Segment* __restrict__ segs, int S,
-                                                        const float* __restrict__ scene_min,
-                                                        const float* __restrict__ scene_max,
-                                                        uint32_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ tile_hist, int64_t tstride,
-                                                        int first_bit) {
-    static_assert(kBlock == kRadix, "one thread per digit");
+__global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __restrict__ points,
+                                                              const Segment* __restrict__ segs, int S,
+                                                              const float* __restrict__ scene_min,
+                                                              const float* __restrict__ scene_max,
+                                                              uint32_t* __restrict__ keys,
+                                                              uint32_t* __restrict__ tile_hist, int64_t tstride,
+                                                              int first_bit) {
+    static_assert(kTileThreads >= kRadix, "one thread per digit");
     __shared__ int s_seg;
     __shared__ uint32_t s_hist[kRadix];
-    __shared__ float s_pts[kSortTile * D];
     const int64_t t = blockIdx.x;
+    if (threadIdx.x < kRadix) s_hist[threadIdx.x] = 0u;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
                                      S, t, &s_seg);
     const Segment g = segs[s];
     const int lt = static_cast<int>(t - g.tile_first);
     if (lt >= g.tiles) {
-        if (tile_hist) tile_hist[threadIdx.x * tstride + t] = 0u;
+        if (tile_hist && threadIdx.x < kRadix) tile_hist[threadIdx.x * tstride + t] = 0u;
         return;
     }
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
     const int count = min(kSortTile, g.n - lt * kSortTile);
-    s_hist[threadIdx.x] = 0u;
-    // Stage the tile's points in LDS with coalesced loads.
-    constexpr int kF = kSortTile * D / kBlock;
-    const int nf = count * D;
-    const float* base = points + row0 * D;
-    float v[kF];
+    const PointRow<D>* rows = reinterpret_cast<const PointRow<D>*>(points + row0 * D);
+    PointRow<D> r[kTileRows];
 #pragma unroll
-    for (int i = 0; i < kF; ++i) {
-        const int f = i * kBlock + threadIdx.x;
-        v[i] = f < nf ? base[f] : 0.0f;
+    for (int i = 0; i < kTileRows; ++i) {
+        const int j = i * kTileThreads + threadIdx.x;
+        if (j < count) r[i] = rows[j];
     }
-#pragma unroll
-    for (int i = 0; i < kF; ++i) s_pts[i * kBlock + threadIdx.x] = v[i];
     float lo[D], hi[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         lo[d] = scene_min[static_cast<int64_t>(s) * D + d];
         hi[d] = scene_max[static_cast<int64_t>(s) * D + d];
     }
-    __syncthreads();
-
-    for (int j = threadIdx.x; j < count; j += kBlock) {
-        float p[D];
 #pragma unroll
-        for (int d = 0; d < D; ++d) p[d] = s_pts[j * D + d];
-        const uint32_t code = morton::encode<D>(p, lo, hi);
-        keys[row0 + j] = code;
-        if (tile_hist) atomicAdd(&s_hist[(code >> first_bit) & (kRadix - 1)], 1u);
+    for (int i = 0; i < kTileRows; ++i) {
+        const int j = i * kTileThreads + threadIdx.x;
+        if (j < count) {
+            const uint32_t code = morton::encode<D>(r[i].v, lo, hi);
+            keys[row0 + j] = code;
+            if (tile_hist) atomicAdd(&s_hist[(code >> first_bit) & (kRadix - 1)], 1u);
+        }
     }
     __syncthreads();
-    if (tile_hist) tile_hist[threadIdx.x * tstride + t] = s_hist[threadIdx.x];
+    if (tile_hist && threadIdx.x < kRadix) tile_hist[threadIdx.x * tstride + t] = s_hist[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
@@ -542,56 +474,57 @@ inline unsigned grid_for(int64_t items) {
     return static_cast<unsigned>((items + kBlock - 1) / kBlock);
 }
 
-// Grid for a clearing/planning launch over `items` words: enough groups to
-// stream the memory, capped (the kernels are grid-stride).
-inline unsigned clear_grid(int64_t items) {
+// Grid for a planning launch over `items` segments: enough groups to
+// stream the table, capped (the kernel is grid-stride).
+inline unsigned plan_grid(int64_t items) {
     const int64_t g = (items + kBlock * 4 - 1) / (kBlock * 4);
     return static_cast<unsigned>(g < 1 ? 1 : (g > 2048 ? 2048 : g));
 }
 
 }  // namespace
 
-hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, uint32_t* clear,
-                               int64_t clear_words, hipStream_t stream) {
-    plan_uniform_kernel<<<clear_grid(S > clear_words ? S : clear_words), kBlock, 0, stream>>>(
-        segs, S, static_cast<int>(n), tree, clear, clear_words);
+hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream) {
+    plan_uniform_kernel<<<plan_grid(S), kBlock, 0, stream>>>(segs, S, static_cast<int>(n), tree);
     return hipGetLastError();
 }
 
 hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
-                               int64_t* node_offsets, uint32_t* clear, int64_t clear_words,
-                               hipStream_t stream) {
-    const unsigned grid = 1 + (clear_words > 0 ? clear_grid(clear_words) : 0);
-    plan_offsets_kernel<<<grid, kBlock, 0, stream>>>(segs, offsets, S, tree, node_offsets, clear,
-                                                     clear_words);
+                               int64_t* node_offsets, hipStream_t stream) {
+    plan_offsets_kernel<<<1, kBlock, 0, stream>>>(segs, offsets, S, tree, node_offsets);
     return hipGetLastError();
 }
 
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
-                         int64_t tiles, float* partials, uint32_t* seg_done, float* scene_min,
-                         float* scene_max, hipStream_t stream) {
+                         int64_t tiles, float* partials, float* scene_min, float* scene_max,
+                         hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
     if (D == 3) {
-        bounds_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, partials, seg_done, scene_min, scene_max);
+        bounds_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, partials);
+        bounds_final_kernel<3><<<static_cast<unsigned>(S), kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi,
+                                                                                scene_min, scene_max);
     } else {
-        bounds_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, partials, seg_done, scene_min, scene_max);
+        bounds_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, partials);
+        bounds_final_kernel<2><<<static_cast<unsigned>(S), kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi,
+                                                                                scene_min, scene_max);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment* segs, int64_t S,
                                  int64_t tiles, float* centers, float* boxes, float* partials,
-                                 uint32_t* seg_done, float* scene_min, float* scene_max,
-                                 hipStream_t stream) {
+                                 float* scene_min, float* scene_max, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
+    const unsigned cgrid = static_cast<unsigned>(S);
     const int Si = static_cast<int>(S);
     if (D == 3 && V == 3) {
-        primitive_prep_kernel<3, 3><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials,
-                                                                 seg_done, scene_min, scene_max);
+        primitive_prep_kernel<3, 3><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials);
+        bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, INFINITY, -INFINITY, scene_min,
+                                                             scene_max);
     } else if (D == 2 && V == 2) {
-        primitive_prep_kernel<2, 2><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials,
-                                                                 seg_done, scene_min, scene_max);
+        primitive_prep_kernel<2, 2><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials);
+        bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, INFINITY, -INFINITY, scene_min,
+                                                             scene_max);
     } else {
         return hipErrorInvalidValue;
     }
@@ -604,11 +537,11 @@ hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
     if (D == 3) {
-        morton_kernel<3><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
-                                                      tstride, bits.first_bit);
+        morton_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys,
+                                                            tile_hist, tstride, bits.first_bit);
     } else {
-        morton_kernel<2><<<grid, kBlock, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
-                                                      tstride, bits.first_bit);
+        morton_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys,
+                                                            tile_hist, tstride, bits.first_bit);
     }
     return hipGetLastError();
 }

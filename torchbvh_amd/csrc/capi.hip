@@ -48,12 +48,12 @@ constexpr int64_t kMaxRows = 2147483647;  // INT32_MAX
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-// Workspace carve-out shared by build and query sort.  Only the bounds
-// counters (`clear`) need zeroing; the planning kernel clears them.
+// Workspace carve-out shared by build and query sort.  Every word is
+// written before it is read, so nothing is cleared.
 struct Layout {
     size_t segs = 0, partials = 0, keys_a = 0, keys_b = 0, vals_a = 0, vals_b = 0;
-    size_t tile_hist = 0, tile_scan = 0, clear = 0, centers = 0, boxes = 0, total = 0;
-    int64_t tiles = 0, tstride = 0, clear_words = 0;
+    size_t tile_hist = 0, tile_scan = 0, centers = 0, boxes = 0, total = 0;
+    int64_t tiles = 0, tstride = 0;
 };
 
 // `with_primitives` adds the primitive build's centres and leaf boxes.
@@ -61,7 +61,6 @@ Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials, bool with
     Layout l;
     l.tiles = tiles_bound(rows, S);
     l.tstride = tile_stride(l.tiles);
-    l.clear_words = sort_clear_words(S);
     size_t at = 0;
     l.segs = at; at = align_up(at + static_cast<size_t>(S) * sizeof(Segment));
     l.partials = at; at = align_up(at + (with_partials ? static_cast<size_t>(l.tiles) * 2 * D * sizeof(float) : 0));
@@ -71,7 +70,6 @@ Layout make_layout(int64_t S, int64_t rows, int D, bool with_partials, bool with
     l.vals_b = at; at = align_up(at + static_cast<size_t>(rows) * 4);
     l.tile_hist = at; at = align_up(at + static_cast<size_t>(kRadix) * l.tstride * 4);
     l.tile_scan = at; at = align_up(at + static_cast<size_t>(kRadix) * l.tstride * 4);
-    l.clear = at; at = align_up(at + static_cast<size_t>(l.clear_words) * 4);
     const size_t prim_floats = with_primitives ? static_cast<size_t>(rows) * D : 0;
     l.centers = at; at = align_up(at + prim_floats * sizeof(float));
     l.boxes = at; at = align_up(at + 2 * prim_floats * sizeof(float));
@@ -92,7 +90,6 @@ SortBuffers sort_buffers(void* ws, const Layout& l) {
     b.vals_b = carve<uint32_t>(ws, l.vals_b);
     b.tile_hist = carve<uint32_t>(ws, l.tile_hist);
     b.tile_scan = carve<uint32_t>(ws, l.tile_scan);
-    b.seg_done = carve<uint32_t>(ws, l.clear);
     b.tstride = l.tstride;
     return b;
 }
@@ -160,10 +157,8 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l);
     const bool ragged = offsets != nullptr;
-    hipError_t e = ragged ? launch_plan_offsets(segs, offsets, S, true, o.node_offsets, sb.seg_done,
-                                                l.clear_words, stream)
-                          : launch_plan_uniform(segs, S, n_uniform, true, sb.seg_done, l.clear_words,
-                                                stream);
+    hipError_t e = ragged ? launch_plan_offsets(segs, offsets, S, true, o.node_offsets, stream)
+                          : launch_plan_uniform(segs, S, n_uniform, true, stream);
     if (e != hipSuccess) return e;
     float* partials = carve<float>(ws, l.partials);
     const float* boxes = nullptr;
@@ -171,13 +166,13 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
         float* centers = carve<float>(ws, l.centers);
         float* leaf_boxes = carve<float>(ws, l.boxes);
         if ((e = launch_primitive_prep(points, D, V, segs, S, l.tiles, centers, leaf_boxes, partials,
-                                       sb.seg_done, o.scene_min, o.scene_max, stream)) != hipSuccess) {
+                                       o.scene_min, o.scene_max, stream)) != hipSuccess) {
             return e;
         }
         points = centers;
         boxes = leaf_boxes;
-    } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, sb.seg_done, o.scene_min,
-                                  o.scene_max, stream)) != hipSuccess) {
+    } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max,
+                                  stream)) != hipSuccess) {
         return e;
     }
     const SortBits bits = full_sort(D);
@@ -213,10 +208,8 @@ hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t 
     const Layout l = make_layout(S, rows, D, false);
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l);
-    hipError_t e = offsets ? launch_plan_offsets(segs, offsets, S, false, nullptr, sb.seg_done,
-                                                 l.clear_words, stream)
-                           : launch_plan_uniform(segs, S, m_uniform, false, sb.seg_done, l.clear_words,
-                                                 stream);
+    hipError_t e = offsets ? launch_plan_offsets(segs, offsets, S, false, nullptr, stream)
+                           : launch_plan_uniform(segs, S, m_uniform, false, stream);
     if (e != hipSuccess) return e;
     uint32_t* keys = codes_only ? codes_only : sb.keys_a;
     if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys,
@@ -578,7 +571,7 @@ hipError_t run_routed_sort(const float* queries, const uint8_t* routes, int64_t 
     const Layout l = make_layout(B, rows, D, false);
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l);
-    hipError_t e = launch_plan_uniform(segs, B, M, false, sb.seg_done, l.clear_words, stream);
+    hipError_t e = launch_plan_uniform(segs, B, M, false, stream);
     if (e != hipSuccess) return e;
     if ((e = launch_route_keys(routes, segs, B, l.tiles, sb.keys_a, sb.tile_hist, sb.tstride, stream)) !=
         hipSuccess) {
@@ -772,7 +765,7 @@ int tbvh_accel_build(const float* points, const int64_t* sorted_indices, const f
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     Segment* segs = carve<Segment>(workspace, 0);
     uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
-    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, nullptr, 0, stream));
+    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
     TBVH_TRY(op, launch_accel_points(points, sorted_indices, scene_min, scene_max, D, segs, B, total,
                                      codes, accel, stream));
     TBVH_TRY(op, launch_accel_nodes(node_aabbs, D, segs, B, total, codes, accel, stream));
@@ -795,7 +788,7 @@ int tbvh_accel_build_ragged(const float* points, const int64_t* offsets, const i
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     Segment* segs = carve<Segment>(workspace, 0);
     uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
-    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, nullptr, nullptr, 0, stream));
+    TBVH_TRY(op, launch_plan_offsets(segs, offsets, B, true, nullptr, stream));
     TBVH_TRY(op, launch_accel_points(points, sorted_indices, scene_min, scene_max, D, segs, B, total,
                                      codes, accel, stream));
     TBVH_TRY(op, launch_accel_nodes(node_aabbs, D, segs, B, total, codes, accel, stream));

@@ -87,7 +87,7 @@ __device__ __forceinline__ int block_find_segment(F firsts, int S, int64_t x, in
 
 // Sort scratch: ping-pong keys/values; the current pass's digit count of
 // every tile and its exclusive scan along the tiles, both digit-major
-// ([digit][tile], row stride `tstride`); the bounds counters.
+// ([digit][tile], row stride `tstride`).  Nothing needs clearing.
 struct SortBuffers {
     uint32_t* keys_a;     // input keys (Morton kernel output)
     uint32_t* keys_b;
@@ -95,7 +95,6 @@ struct SortBuffers {
     uint32_t* vals_b;
     uint32_t* tile_hist;  // kRadix * tstride words
     uint32_t* tile_scan;  // kRadix * tstride words
-    uint32_t* seg_done;   // S words: bounds tiles finished per segment
     int64_t tstride;      // >= tiles_bound, a multiple of 64
 };
 
@@ -114,22 +113,17 @@ struct SortPass {
     int shift;
 };
 
-// Words the planning kernel clears: the bounds counters (one per segment).
-inline int64_t sort_clear_words(int64_t S) { return S; }
-
-// Planning: fill the segment table and clear `clear_words` words at `clear`.
-hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, uint32_t* clear,
-                               int64_t clear_words, hipStream_t stream);
+// Planning: fill the segment table.
+hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream);
 hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
-                               int64_t* node_offsets, uint32_t* clear, int64_t clear_words,
-                               hipStream_t stream);
+                               int64_t* node_offsets, hipStream_t stream);
 
-// Per-cloud bounds: one work-group per tile writes a partial box; the last
-// tile of a cloud to finish (counted in `seg_done`, zeroed beforehand)
-// reduces the cloud's partials into scene_min/max.
+// Per-cloud bounds: one work-group per tile writes a partial box
+// (`partials`: 2D floats per tile), then one work-group per cloud reduces
+// them into scene_min/max.
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
-                         int64_t tiles_bound, float* partials, uint32_t* seg_done,
-                         float* scene_min, float* scene_max, hipStream_t stream);
+                         int64_t tiles_bound, float* partials, float* scene_min, float* scene_max,
+                         hipStream_t stream);
 
 // Digit range of a sort: 8-bit digits at bits first_bit, first_bit + 8, ...
 // below end_bit (so passes = ceil((end_bit - first_bit) / 8) <= 4).
@@ -140,11 +134,10 @@ struct SortBits {
 };
 
 // Primitive BVH input: every primitive's box and centre, and each cloud's
-// bounds over the boxes (seg_done / partials as in launch_bounds).
+// bounds over the boxes (partials as in launch_bounds).
 hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment* segs, int64_t S,
                                  int64_t tiles, float* centers, float* boxes, float* partials,
-                                 uint32_t* seg_done, float* scene_min, float* scene_max,
-                                 hipStream_t stream);
+                                 float* scene_min, float* scene_max, hipStream_t stream);
 
 // Morton codes of every row against its segment's bounds and, unless
 // `tile_hist` is null, every tile's count of the first sort digit (digit at
