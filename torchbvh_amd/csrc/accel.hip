@@ -25,76 +25,10 @@
 // cross-work-group synchronisation.
 #include <float.h>
 
-#include "tbvh_internal.hpp"
+#include "accel_tree.hpp"
 
 namespace tbvh {
 namespace {
-
-// Sorted codes of one cloud, read from an LDS window where it covers the
-// position and from global memory elsewhere.
-struct CodeView {
-    const uint32_t* codes;  // cloud's codes (global)
-    const uint32_t* win;    // LDS window, cloud-local positions [w_lo, w_hi)
-    int w_lo, w_hi;
-    int n;
-    __device__ __forceinline__ uint32_t at(int j) const {
-        return (j >= w_lo && j < w_hi) ? win[j - w_lo] : codes[j];
-    }
-    // Length of the common prefix of the 64-bit keys (code << 32 | position)
-    // at positions i and j; -1 outside the cloud.
-    __device__ __forceinline__ int prefix_len(int i, uint32_t ci, int j) const {
-        if (j < 0 || j >= n) return -1;
-        const uint64_t a = (static_cast<uint64_t>(ci) << 32) | static_cast<uint32_t>(i);
-        const uint64_t b = (static_cast<uint64_t>(at(j)) << 32) | static_cast<uint32_t>(j);
-        return __clzll(static_cast<long long>(a ^ b));
-    }
-};
-
-template <int D>
-__device__ __forceinline__ void merge_row(float* box, const float* row) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        box[d] = fminf(box[d], row[d]);
-        box[D + d] = fmaxf(box[D + d], row[D + d]);
-    }
-}
-
-// Exact box of sorted positions [a, b] (inclusive) from the implicit tree:
-// heap node h has 1-based index h + 1, leaves are [2^L, 2^(L+1)), and the
-// classic bottom-up cover visits O(log n) nodes whose ranges tile [a, b].
-template <int D>
-__device__ void range_box(const float* nodes, int vl, int L, int a, int b, float* box) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        box[d] = FLT_MAX;
-        box[D + d] = -FLT_MAX;
-    }
-    int64_t lo = static_cast<int64_t>(a) + (int64_t(1) << L);
-    int64_t hi = static_cast<int64_t>(b) + 1 + (int64_t(1) << L);
-    while (lo < hi) {
-        if (lo & 1) {
-            const int row = tree::memory_index(vl, L, static_cast<int>(lo - 1));
-            merge_row<D>(box, nodes + static_cast<int64_t>(row) * 2 * D);
-            ++lo;
-        }
-        if (hi & 1) {
-            --hi;
-            const int row = tree::memory_index(vl, L, static_cast<int>(hi - 1));
-            merge_row<D>(box, nodes + static_cast<int64_t>(row) * 2 * D);
-        }
-        lo >>= 1;
-        hi >>= 1;
-    }
-}
-
-__device__ __forceinline__ int32_t child_ref(int first, int last, int internal) {
-    const int count = last - first + 1;
-    if (count <= kAccelBucket) {
-        return static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(count - 1) << 28) |
-                                    static_cast<uint32_t>(first));
-    }
-    return internal;
-}
 
 // Pass 1: Morton-ordered points (float4) and their codes, one thread per point.
 template <int D>
@@ -131,7 +65,6 @@ __global__ __launch_bounds__(kBlock) void accel_points_kernel(
 // -5% in 3-D, -16% in 2-D).  Child boxes come from the implicit tree's node
 // AABBs (reading the points directly measured slower, even for 16-point
 // ranges: more bytes through L2).
-constexpr int kCodeHalo = 256;
 constexpr int kCodeWindow = 2 * kBlock + 2 * kCodeHalo;
 template <int D>
 __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
@@ -172,27 +105,8 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
     cv.win = s_codes + (lo > 0 ? 0 : -lo);
     cv.w_lo = static_cast<int>(lo > 0 ? lo : 0);
     cv.w_hi = static_cast<int>(hi < n ? (hi > 0 ? hi : 0) : n);
-    const uint32_t ci = cv.at(i);
-
-    const int dir = cv.prefix_len(i, ci, i + 1) - cv.prefix_len(i, ci, i - 1) > 0 ? 1 : -1;
-    const int dmin = cv.prefix_len(i, ci, i - dir);
-    int lmax = 2;
-    while (cv.prefix_len(i, ci, i + lmax * dir) > dmin) lmax <<= 1;
-    int l = 0;
-    for (int t = lmax >> 1; t >= 1; t >>= 1) {
-        if (cv.prefix_len(i, ci, i + (l + t) * dir) > dmin) l += t;
-    }
-    const int j = i + l * dir;
-    const int dnode = cv.prefix_len(i, ci, j);
-    int split = 0;
-    int t = l;
-    do {
-        t = (t + 1) >> 1;
-        if (cv.prefix_len(i, ci, i + (split + t) * dir) > dnode) split += t;
-    } while (t > 1);
-    const int gamma = i + split * dir + (dir < 0 ? dir : 0);
-    const int first = min(i, j);
-    const int last = max(i, j);
+    int first, last, gamma;
+    karras_node(cv, i, first, last, gamma);
     if (i != 0 && last - first + 1 <= kAccelBucket) return;
 
     const float* nodes = node_aabbs + g.node_start * 2 * D;
@@ -208,6 +122,81 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
     rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
     rec[4 * D + 2] = 0.0f;
     rec[4 * D + 3] = 0.0f;
+}
+
+// Records of the radix-tree nodes the fused first tree pass could not
+// finish (their range spans two of its work-groups).  A work-group takes
+// kSpanGroups consecutive first-pass groups and runs their listed nodes
+// back to back, so its lanes stay busy; search and child boxes from global
+// memory (the finished implicit tree).
+constexpr int kSpanGroups = 8;
+template <int D>
+__global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __restrict__ segs, int S,
+                                                            int64_t groups_bound,
+                                                            const uint32_t* __restrict__ sorted_codes,
+                                                            const uint32_t* __restrict__ span_list,
+                                                            const uint32_t* __restrict__ span_count,
+                                                            const float* __restrict__ node_aabbs,
+                                                            float* __restrict__ records) {
+    constexpr int R = 4 * D + 4;
+    __shared__ int s_seg[kSpanGroups];
+    __shared__ uint32_t s_base[kSpanGroups + 1];
+    __shared__ int64_t s_list0[kSpanGroups];
+    const int tid = threadIdx.x;
+    if (tid < kSpanGroups) {
+        const int64_t G = static_cast<int64_t>(blockIdx.x) * kSpanGroups + tid;
+        uint32_t cnt = 0;
+        int sg = 0;
+        int64_t list0 = 0;
+        if (G < groups_bound) {
+            sg = find_segment([&](int c) { return static_cast<int64_t>(segs[c].group_first[0]); }, S, G);
+            const Segment g = segs[sg];
+            const int gl = static_cast<int>(G - g.group_first[0]);
+            if (gl < g.groups[0]) {
+                const int width = 1 << (g.leaf_level < kSubtreeLevels ? g.leaf_level : kSubtreeLevels);
+                cnt = span_count[G];
+                list0 = (g.start - sg) + static_cast<int64_t>(gl) * width;
+            }
+        }
+        s_seg[tid] = sg;
+        s_list0[tid] = list0;
+        s_base[tid + 1] = cnt;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        s_base[0] = 0;
+        for (int k = 1; k <= kSpanGroups; ++k) s_base[k] += s_base[k - 1];
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < s_base[kSpanGroups]; e += kBlock) {
+        int k = 0;
+        while (e >= s_base[k + 1]) ++k;
+        const int sg = s_seg[k];
+        const Segment g = segs[sg];
+        const int i = static_cast<int>(span_list[s_list0[k] + (e - s_base[k])]);
+        if (i < 0 || i >= g.n - 1) continue;  // never for entries the tree pass wrote
+        CodeView cv;
+        cv.codes = sorted_codes + g.start;
+        cv.win = nullptr;
+        cv.w_lo = 0;
+        cv.w_hi = 0;
+        cv.n = g.n;
+        int first, last, gamma;
+        karras_node(cv, i, first, last, gamma);
+        const float* nodes = node_aabbs + g.node_start * 2 * D;
+        float* rec = records + ((g.start - sg) + i) * R;
+        float box[2 * D];
+        range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, box);
+#pragma unroll
+        for (int c = 0; c < 2 * D; ++c) rec[c] = box[c];
+        range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
+#pragma unroll
+        for (int c = 0; c < 2 * D; ++c) rec[2 * D + c] = box[c];
+        rec[4 * D] = __int_as_float(child_ref(first, gamma, gamma));
+        rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
+        rec[4 * D + 2] = 0.0f;
+        rec[4 * D + 3] = 0.0f;
+    }
 }
 
 inline unsigned grid_for(int64_t items) {
@@ -247,6 +236,23 @@ hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* seg
     } else {
         accel_nodes_kernel<2><<<grid_for(total - S), kBlock, 0, stream>>>(
             segs, Si, total - S, total, sorted_codes, node_aabbs, records);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_accel_span(const float* node_aabbs, int D, const Segment* segs, int64_t S, int64_t total,
+                             int64_t groups_bound, const uint32_t* sorted_codes, const uint32_t* span_list,
+                             const uint32_t* span_count, void* accel, hipStream_t stream) {
+    if (total - S <= 0) return hipSuccess;
+    float* records = reinterpret_cast<float*>(static_cast<char*>(accel) + accel_points_bytes(total));
+    const int Si = static_cast<int>(S);
+    const unsigned grid = static_cast<unsigned>((groups_bound + kSpanGroups - 1) / kSpanGroups);
+    if (D == 3) {
+        accel_span_kernel<3><<<grid, kBlock, 0, stream>>>(segs, Si, groups_bound, sorted_codes, span_list,
+                                                          span_count, node_aabbs, records);
+    } else {
+        accel_span_kernel<2><<<grid, kBlock, 0, stream>>>(segs, Si, groups_bound, sorted_codes, span_list,
+                                                          span_count, node_aabbs, records);
     }
     return hipGetLastError();
 }

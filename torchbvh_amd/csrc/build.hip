@@ -12,7 +12,7 @@
 // segments (clouds), so single, batched and ragged inputs share one launch
 // sequence, and the tree is built by level-synchronous LDS passes of
 // 2^kSubtreeLevels nodes per work-group with no global atomics.
-#include "tbvh_internal.hpp"
+#include "accel_tree.hpp"
 
 namespace tbvh {
 namespace {
@@ -377,7 +377,10 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                                                            TreeOutputs out) {
     __shared__ int s_seg;
     __shared__ float s_box[(2 * kSubtreeLeaves - 1) * 2 * D];
+    __shared__ uint32_t s_codes[kFromPoints ? kSubtreeLeaves + 2 * kCodeHalo : 1];
+    __shared__ uint32_t s_span;
     const int64_t grp = blockIdx.x;
+    if (threadIdx.x == 0) s_span = 0u;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].group_first[p]); },
                                      S, grp, &s_seg);
     const Segment g = segs[s];
@@ -392,6 +395,14 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
     const bool arrays = out.left != nullptr && (out.arrays_packed || s == 0);
     const int64_t arr0 = out.arrays_packed ? g.node_start : 0;
     const int tid = threadIdx.x;
+    // Fused accel: the sorted codes around this group's leaves, in LDS.
+    const bool fused_accel = kFromPoints && out.sorted_codes != nullptr;
+    const int g0 = gl * width;
+    const int w_lo = max(g0 - kCodeHalo, 0);
+    const int w_hi = min(g0 + width + kCodeHalo, g.n);
+    if (fused_accel) {
+        for (int k = tid; k < w_hi - w_lo; k += kBlock) s_codes[k] = out.sorted_codes[g.start + w_lo + k];
+    }
 
     if (tid < width) {
         const int j = gl * width + tid;
@@ -468,6 +479,51 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
         __syncthreads();
     }
     if (kFromPoints || up > 0) store_level<D>(s_box, nodes, vl, L, lvl_in - up, width >> up, gl);
+    if (fused_accel) {
+        // Radix-tree node i = g0 + tid of this cloud (Karras 2012).  Its
+        // range stays inside the group iff the first position past the
+        // group's edge in its direction shares no longer prefix with i than
+        // dmin; then the search and both child boxes use only LDS (the code
+        // window and the subtree).  Spanning nodes are listed, compacted in
+        // the group's own record rows, for launch_accel_span.
+        constexpr int R = 4 * D + 4;
+        const int i = g0 + tid;
+        const int64_t rec0 = g.start - s;  // the cloud's first record row
+        bool spans = false;
+        if (tid < width && i < g.n - 1) {
+            CodeView cv;
+            cv.codes = out.sorted_codes + g.start;
+            cv.win = s_codes;
+            cv.w_lo = w_lo;
+            cv.w_hi = w_hi;
+            cv.n = g.n;
+            const uint32_t ci = cv.at(i);
+            int dir, dmin;
+            karras_dir(cv, i, ci, dir, dmin);
+            spans = cv.prefix_len(i, ci, dir > 0 ? g0 + width : g0 - 1) > dmin;
+            if (!spans) {
+                int first, last, gamma;
+                karras_range(cv, i, ci, dir, dmin, kSubtreeLeaves, first, last, gamma);
+                if (i == 0 || last - first + 1 > kAccelBucket) {
+                    float* rec = out.accel_records + (rec0 + i) * R;
+                    float box[2 * D];
+                    range_box_lds<D>(s_box, width, first - g0, gamma - g0, box);
+#pragma unroll
+                    for (int k = 0; k < 2 * D; ++k) rec[k] = box[k];
+                    range_box_lds<D>(s_box, width, gamma + 1 - g0, last - g0, box);
+#pragma unroll
+                    for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
+                    rec[4 * D] = __int_as_float(child_ref(first, gamma, gamma));
+                    rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
+                    rec[4 * D + 2] = 0.0f;
+                    rec[4 * D + 3] = 0.0f;
+                }
+            }
+        }
+        if (spans) out.span_list[rec0 + g0 + atomicAdd(&s_span, 1u)] = static_cast<uint32_t>(i);
+        __syncthreads();
+        if (tid == 0) out.span_count[grp] = s_span;
+    }
 }
 
 inline unsigned grid_for(int64_t items) {

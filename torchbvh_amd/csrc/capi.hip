@@ -192,12 +192,25 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
     to.arrays_packed = ragged;
     to.accel_points = o.accel ? static_cast<float4*>(o.accel) : nullptr;
     to.leaf_boxes = boxes;
+    if (o.accel) {
+        // Radix-tree records in the first tree pass; the sort's value
+        // buffers (dead after the sort) hold the spanning-node marks.
+        to.sorted_codes = sorted_keys;
+        to.accel_records = reinterpret_cast<float*>(static_cast<char*>(o.accel) + accel_points_bytes(rows));
+        to.span_list = sb.vals_a;
+        to.span_count = sb.vals_b;
+    }
     const int64_t max_n = ragged ? (rows < kMaxCloud ? rows : kMaxCloud) : n_uniform;
     if ((e = launch_tree(points, D, segs, S, rows, max_n, o.sorted_indices, o.node_aabbs, to,
                          stream)) != hipSuccess) {
         return e;
     }
-    if (o.accel) return launch_accel_nodes(o.node_aabbs, D, segs, S, rows, sorted_keys, o.accel, stream);
+    if (o.accel) {
+        // First-pass work-groups: at most one per 256 leaves of each cloud.
+        const int64_t groups_bound = (rows + kSubtreeLeaves - 1) / kSubtreeLeaves + S;
+        return launch_accel_span(o.node_aabbs, D, segs, S, rows, groups_bound, sorted_keys, sb.vals_a, sb.vals_b,
+                                 o.accel, stream);
+    }
     return hipSuccess;
 }
 

@@ -165,6 +165,16 @@ struct TreeOutputs {
     bool arrays_packed;    // ragged: per-segment arrays at node_start; batched: segment 0 only
     float4* accel_points;  // Morton-ordered float4 points for the accel (null: not written)
     const float* leaf_boxes = nullptr;  // primitive BVH: [rows, 2D] leaf boxes (null: point leaves)
+    // Fused accel records (first pass): with `sorted_codes` set, every
+    // radix-tree node of a work-group's leaves whose range lies inside the
+    // group gets its record in `accel_records`; the others are listed for
+    // launch_accel_span: node indices compacted in the group's own record
+    // rows of `span_list`, their count per first-pass work-group in
+    // `span_count`.
+    const uint32_t* sorted_codes = nullptr;
+    float* accel_records = nullptr;
+    uint32_t* span_list = nullptr;   // one word per record row
+    uint32_t* span_count = nullptr;  // one word per first-pass work-group
 };
 
 // Implicit-tree node AABBs (all passes), optionally the traversal arrays and
@@ -186,6 +196,12 @@ size_t accel_bytes(int64_t total, int64_t S, int D);
 hipError_t launch_accel_points(const float* points, const int64_t* sorted, const float* scene_min,
                                const float* scene_max, int D, const Segment* segs, int64_t S,
                                int64_t total, uint32_t* codes, void* accel, hipStream_t stream);
+// Records of the nodes the fused first tree pass listed (after all tree
+// passes: their boxes need the upper levels).  `groups_bound` bounds the
+// first pass's work-group count.
+hipError_t launch_accel_span(const float* node_aabbs, int D, const Segment* segs, int64_t S, int64_t total,
+                             int64_t groups_bound, const uint32_t* sorted_codes, const uint32_t* span_list,
+                             const uint32_t* span_count, void* accel, hipStream_t stream);
 // Radix-tree records from Morton-sorted codes and the implicit tree.
 hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* segs, int64_t S,
                               int64_t total, const uint32_t* sorted_codes, void* accel,
