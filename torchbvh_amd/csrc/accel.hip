@@ -15,8 +15,9 @@
 //   records [n-1]  per radix-tree internal node i: left box (2D floats), right
 //                  box (2D floats), left ref, right ref, 2 pad words
 //                  (16 floats = 64 B in 3-D, 12 floats = 48 B in 2-D)
-// A child ref >= 0 is an internal node; a negative ref is a bucket of <= 4
-// consecutive points: 0x80000000 | (count - 1) << 28 | first.  Cloud c's
+// A child ref >= 0 is an internal node; a negative ref is a bucket of at most
+// accel_bucket<D>() (4 in 3-D, 8 in 2-D) consecutive points:
+// 0x80000000 | (count - 1) << 28 | first.  Cloud c's
 // records start at row (first point of c) - c.
 //
 // Child boxes are exact: each is the min/max over its point range, assembled
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
     cv.w_hi = static_cast<int>(hi < n ? (hi > 0 ? hi : 0) : n);
     int first, last, gamma;
     karras_node(cv, i, first, last, gamma);
-    if (i != 0 && last - first + 1 <= kAccelBucket) return;
+    if (i != 0 && last - first + 1 <= accel_bucket<D>()) return;
 
     const float* nodes = node_aabbs + g.node_start * 2 * D;
     float* rec = records + r * R;
@@ -118,8 +119,8 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
     range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
 #pragma unroll
     for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
-    rec[4 * D] = __int_as_float(child_ref(first, gamma, gamma));
-    rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
+    rec[4 * D] = __int_as_float(child_ref<D>(first, gamma, gamma));
+    rec[4 * D + 1] = __int_as_float(child_ref<D>(gamma + 1, last, gamma + 1));
     rec[4 * D + 2] = 0.0f;
     rec[4 * D + 3] = 0.0f;
 }
@@ -192,8 +193,8 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
         range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
 #pragma unroll
         for (int c = 0; c < 2 * D; ++c) rec[2 * D + c] = box[c];
-        rec[4 * D] = __int_as_float(child_ref(first, gamma, gamma));
-        rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
+        rec[4 * D] = __int_as_float(child_ref<D>(first, gamma, gamma));
+        rec[4 * D + 1] = __int_as_float(child_ref<D>(gamma + 1, last, gamma + 1));
         rec[4 * D + 2] = 0.0f;
         rec[4 * D + 3] = 0.0f;
     }

@@ -160,9 +160,10 @@ __device__ __forceinline__ void karras_node(const CodeView& cv, int i, int& firs
     karras_range(cv, i, ci, dir, dmin, lmax, first, last, gamma);
 }
 
+template <int D>
 __device__ __forceinline__ int32_t child_ref(int first, int last, int internal) {
     const int count = last - first + 1;
-    if (count <= kAccelBucket) {
+    if (count <= accel_bucket<D>()) {
         return static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(count - 1) << 28) |
                                     static_cast<uint32_t>(first));
     }

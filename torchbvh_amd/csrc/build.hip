@@ -504,7 +504,7 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
             if (!spans) {
                 int first, last, gamma;
                 karras_range(cv, i, ci, dir, dmin, kSubtreeLeaves, first, last, gamma);
-                if (i == 0 || last - first + 1 > kAccelBucket) {
+                if (i == 0 || last - first + 1 > accel_bucket<D>()) {
                     float* rec = out.accel_records + (rec0 + i) * R;
                     float box[2 * D];
                     range_box_lds<D>(s_box, width, first - g0, gamma - g0, box);
@@ -513,8 +513,8 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                     range_box_lds<D>(s_box, width, gamma + 1 - g0, last - g0, box);
 #pragma unroll
                     for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
-                    rec[4 * D] = __int_as_float(child_ref(first, gamma, gamma));
-                    rec[4 * D + 1] = __int_as_float(child_ref(gamma + 1, last, gamma + 1));
+                    rec[4 * D] = __int_as_float(child_ref<D>(first, gamma, gamma));
+                    rec[4 * D + 1] = __int_as_float(child_ref<D>(gamma + 1, last, gamma + 1));
                     rec[4 * D + 2] = 0.0f;
                     rec[4 * D + 3] = 0.0f;
                 }

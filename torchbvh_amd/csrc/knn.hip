@@ -208,7 +208,7 @@ struct NodeStack {
     }
 };
 
-// Brute-forces one bucket (<= kAccelBucket consecutive Morton-ordered
+// Brute-forces one bucket (<= accel_bucket<D>() consecutive Morton-ordered
 // points, loaded together) into the candidate list.
 template <int D, int K>
 __device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int n, const float* q,
@@ -216,13 +216,14 @@ __device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int 
     const int first = ref & 0x0fffffff;
     const int count = ((ref >> 28) & 7) + 1;
     if (first + count > n) return;  // a corrupt ref never reads outside the cloud
-    float4 p[kAccelBucket];
+    constexpr int kBucket = accel_bucket<D>();
+    float4 p[kBucket];
 #pragma unroll
-    for (int j = 0; j < kAccelBucket; ++j) {
+    for (int j = 0; j < kBucket; ++j) {
         p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int j = 0; j < kAccelBucket; ++j) {
+    for (int j = 0; j < kBucket; ++j) {
         if (j < count) {
             const float d = point_distance<D>(q, p[j]);
             const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
 
     NodeStack stack;
     stack.col = lds_stack + threadIdx.x;
-    int32_t ref = n <= kAccelBucket
+    int32_t ref = n <= accel_bucket<D>()
                       ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
                       : 0;
     float nd = 0.0f;
