@@ -384,8 +384,10 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].group_first[p]); },
                                      S, grp, &s_seg);
     const Segment g = segs[s];
-    const int gl = static_cast<int>(grp - g.group_first[p]);
-    if (gl >= g.groups[p]) return;
+    // The pass-indexed fields come from the table itself: indexing the local
+    // copy with the runtime pass number would put the whole copy in scratch.
+    const int gl = static_cast<int>(grp - segs[s].group_first[p]);
+    if (gl >= segs[s].groups[p]) return;
     const int L = g.leaf_level;
     const int vl = g.vl;
     const int lvl_in = L - p * kSubtreeLevels;
