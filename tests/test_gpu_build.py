@@ -226,8 +226,8 @@ def test_fused_accel_matches_standalone_ragged():
 
 
 def test_build_million_points_many_tiles():
-    """245 sort tiles per pass: long look-back chains and the last-tile bounds
-    reduction, bit-exact against the oracle."""
+    """245 sort tiles per pass: offsets scanned over many tiles and the
+    reduction of many tile boxes, bit-exact against the oracle."""
     rng = np.random.default_rng(2024)
     check_single_build(rng.random((1_000_000, 3), dtype=np.float32))
 

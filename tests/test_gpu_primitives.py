@@ -5,7 +5,7 @@ bit-exact.
 Primitive sets follow the reference's ray tests (torchbvh
 tests/test_raytrace.py:94-116: segments (3, 37, 2, 2) and triangles
 (3, 29, 3, 3) in [-2, 2]) plus sizes around this library's 4096-primitive
-tiles, whose bounds reduction finishes in the last tile."""
+tiles, each of which contributes one partial box to its sample's bounds."""
 
 from __future__ import annotations
 
@@ -75,8 +75,8 @@ def test_primitive_build_degenerate_equals_point_build(V, D):
 
 
 def test_primitive_build_many_tiles():
-    """62 tiles per sample: the last-tile bounds reduction and long sort
-    look-back chains."""
+    """62 tiles per sample: the per-cloud reduction of many tile boxes and
+    sort offsets accumulated over many tiles."""
     check_primitive_build(random_primitives(np.random.default_rng(77), 2, 250_000, 3, 3))
 
 
