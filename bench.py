@@ -299,7 +299,7 @@ def main() -> int:
         ei[0].record()
         for _ in range(args.implicit_reps):
             _C.query_knn_batched_cached_bounds_ordered(
-                nodes, sidx, qb, order, bvh["num_leaves"], bvh["num_real_nodes"], D, k)
+                nodes, sidx, qb, order, bvh["num_leaves"], bvh["num_real_nodes"], D, k, accel=False)
         ei[1].record()
         torch.cuda.synchronize()
         implicit_ms = ei[0].elapsed_time(ei[1]) / args.implicit_reps

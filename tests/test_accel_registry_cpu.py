@@ -1,0 +1,50 @@
+"""The accel registry behind the reference-style k-NN bindings (CPU
+tensors stand in for device ones: the registry only compares tensors)."""
+
+from __future__ import annotations
+
+import gc
+
+import torch
+
+from torchbvh_amd import _native
+
+
+def test_registered_accel_follows_the_build_tensors_and_their_views():
+    nodes = torch.rand(2, 7, 6)
+    order = torch.arange(8).repeat(2, 1)
+    accel = torch.zeros(16, dtype=torch.uint8)
+    _native._register_accel(nodes, order, accel)
+    assert _native._registered_accel(nodes, order) is accel
+    assert _native._registered_accel(nodes[None], order[None]) is accel  # views of every element
+    assert _native._registered_accel(nodes.clone(), order) is None
+    assert _native._registered_accel(nodes, order.clone()) is None
+    assert _native._registered_accel(nodes[:1], order) is None  # a part is not the BVH
+    assert _native._pick_accel(False, nodes, order) is None
+    other = torch.ones(1)
+    assert _native._pick_accel(other, nodes, order) is other
+    assert _native._pick_accel(None, nodes, order) is accel
+
+
+def test_modified_tensors_lose_the_accel():
+    nodes = torch.rand(1, 3, 4)
+    order = torch.arange(2)[None]
+    accel = torch.zeros(4, dtype=torch.uint8)
+    _native._register_accel(nodes, order, accel)
+    nodes[None].mul_(1.0)  # in place through a view: the shared version counter moves
+    assert _native._registered_accel(nodes, order) is None
+    nodes2 = torch.rand(1, 3, 4)
+    order2 = torch.arange(2)[None]
+    _native._register_accel(nodes2, order2, accel)
+    order2.add_(0)
+    assert _native._registered_accel(nodes2, order2) is None
+
+
+def test_entry_goes_with_the_build_tensor():
+    nodes = torch.rand(1, 3, 4)
+    key = nodes.data_ptr()
+    _native._register_accel(nodes, torch.arange(2)[None], torch.zeros(4, dtype=torch.uint8))
+    assert key in _native._accel_registry
+    del nodes
+    gc.collect()
+    assert key not in _native._accel_registry

@@ -20,6 +20,7 @@ from parity import (
     knn_pathological_clouds,
     unit_direction_points,
 )
+from torchbvh_amd import _native
 from torchbvh_amd._native import _C
 
 pytestmark = pytest.mark.gpu
@@ -37,10 +38,10 @@ def implicit_knn(h, queries: torch.Tensor, k: int, sort: bool):
     if sort:
         order = _C.morton_sort_queries_narrow(q, h["scene_min"][None], h["scene_max"][None])
         out = _C.query_knn_batched_cached_bounds_ordered(
-            nodes, sidx, q, order, h["num_leaves"], h["num_real_nodes"], h["dim"], k)
+            nodes, sidx, q, order, h["num_leaves"], h["num_real_nodes"], h["dim"], k, accel=False)
     else:
         out = _C.query_knn_batched_cached_bounds(
-            nodes, sidx, q, h["num_leaves"], h["num_real_nodes"], h["dim"], k)
+            nodes, sidx, q, h["num_leaves"], h["num_real_nodes"], h["dim"], k, accel=False)
     return out[0][0], out[1][0]
 
 
@@ -288,7 +289,7 @@ def test_spatial_output_is_ordered_output_in_launch_order(dim, k, use_accel):
     qd = dev(q)
     order = _C.morton_sort_queries_narrow(qd, h["scene_min"], h["scene_max"])
     args = (h["node_aabbs"], h["sorted_indices"], qd, order, h["num_leaves"], h["num_real_nodes"], dim, k)
-    accel = h._aux["accel"] if use_accel else None
+    accel = h._aux["accel"] if use_accel else False
     si, sd = _C.query_knn_batched_cached_bounds_spatial(*args, accel=accel)
     oi, od = _C.query_knn_batched_cached_bounds_ordered(*args, accel=accel)
     perm = order.unsqueeze(-1).expand(-1, -1, k)
@@ -336,7 +337,8 @@ def test_routed_knn_spatial_matches_oracle(dim, k, use_accel):
     qd, rd = dev(q), dev(routes)
     order = _C.morton_sort_routed_queries_batched(qd, rd, ht["scene_min"], ht["scene_max"],
                                                   hf["scene_min"], hf["scene_max"])
-    kw = {"true_accel": ht._aux["accel"], "false_accel": hf._aux["accel"]} if use_accel else {}
+    kw = ({"true_accel": ht._aux["accel"], "false_accel": hf._aux["accel"]} if use_accel
+          else {"true_accel": False, "false_accel": False})
     idx, dist = _C.query_knn_routed_batched_cached_bounds_spatial(
         ht["node_aabbs"], ht["sorted_indices"], hf["node_aabbs"], hf["sorted_indices"], qd, rd, order,
         ht["num_leaves"], ht["num_real_nodes"], hf["num_leaves"], hf["num_real_nodes"], dim, k, **kw)
@@ -345,3 +347,31 @@ def test_routed_knn_spatial_matches_oracle(dim, k, use_accel):
         ei, ed = oracle.knn_routed(tp[b], fp[b], q[b][o[b]], routes[b][o[b]], k)
         assert_same_int(idx[b].cpu().numpy(), ei, f"cloud {b} indices")
         assert_same_f32(dist[b].cpu().numpy(), ed, f"cloud {b} distances")
+
+
+def test_reference_style_bindings_use_the_registered_accel():
+    """A caller of the reference's `_C` surface builds with
+    build_bvh_batched_cooperative(points) and passes the dict's tensors to
+    the k-NN bindings: the result keeps exactly the reference's keys, and
+    the query takes the accel registered with those tensors (identical to
+    the implicit tree's result and the oracle's) until they are modified."""
+    rng = np.random.default_rng(77)
+    p = rng.random((2, 5000, 3), dtype=np.float32)
+    q = rng.random((2, 900, 3), dtype=np.float32)
+    pd, qd = dev(p), dev(q)
+    d = _C.build_bvh_batched_cooperative(pd)
+    assert set(d) == {"node_aabbs", "sorted_indices", "scene_min", "scene_max", "batch_size", "num_leaves",
+                      "num_real_nodes", "leaf_level", "virtual_leaves", "dim", "left_child_mem",
+                      "right_child_mem", "mem_to_leaf"}
+    assert _native._registered_accel(d["node_aabbs"], d["sorted_indices"]) is not None
+    order = _C.morton_sort_queries_narrow(qd, d["scene_min"], d["scene_max"])
+    args = (d["node_aabbs"], d["sorted_indices"], qd, order, d["num_leaves"], d["num_real_nodes"], 3, 16)
+    ai, ad = _C.query_knn_batched_cached_bounds_ordered(*args)
+    ii, idd = _C.query_knn_batched_cached_bounds_ordered(*args, accel=False)
+    assert torch.equal(ai, ii) and torch.equal(ad, idd)
+    for b in range(2):
+        ei, ed = oracle.knn(p[b], q[b], 16)
+        assert_same_int(ai[b].cpu().numpy(), ei, f"cloud {b} indices")
+        assert_same_f32(ad[b].cpu().numpy(), ed, f"cloud {b} distances")
+    d["node_aabbs"].mul_(1.0)
+    assert _native._registered_accel(d["node_aabbs"], d["sorted_indices"]) is None
