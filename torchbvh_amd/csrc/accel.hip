@@ -24,6 +24,12 @@
 // from the implicit tree's node AABBs with an iterative segment-tree cover of
 // the range (min/max is exact and idempotent), so no pass here needs
 // cross-work-group synchronisation.
+//
+// Two ways to build it: the standalone passes below (points + codes, then
+// one thread per node: tbvh_accel_build*), and the fused build
+// (tbvh_build*_with_accel), where the first implicit-tree pass writes the
+// points and the records of nodes inside each 256-leaf group and
+// accel_span_kernel finishes the others.  Both produce the same bytes.
 #include <float.h>
 
 #include "accel_tree.hpp"
@@ -31,7 +37,8 @@
 namespace tbvh {
 namespace {
 
-// Pass 1: Morton-ordered points (float4) and their codes, one thread per point.
+// Standalone pass 1: Morton-ordered points (float4) and their codes, one
+// thread per point.
 template <int D>
 __global__ __launch_bounds__(kBlock) void accel_points_kernel(
     const float* __restrict__ points, const int64_t* __restrict__ sorted,
@@ -59,8 +66,8 @@ __global__ __launch_bounds__(kBlock) void accel_points_kernel(
     leaf_points[r] = v;
 }
 
-// Pass 2: radix-tree internal nodes (Karras 2012, section 4), one thread per
-// node; nodes inside a bucket are not referenced and write nothing.  The
+// Standalone pass 2: radix-tree internal nodes (Karras 2012, section 4), one
+// thread per node; nodes inside a bucket are not referenced and write nothing.  The
 // block first stages the sorted codes around its nodes in LDS (most nodes
 // span few positions, so most of the searches' reads stay there; measured
 // -5% in 3-D, -16% in 2-D).  Child boxes come from the implicit tree's node

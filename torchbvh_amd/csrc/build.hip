@@ -1,6 +1,7 @@
 // BVH build kernels: segment planning, per-cloud bounds, Morton codes (with
 // the first sort digit's tile counts), implicit-tree node AABBs, fused with
-// the traversal arrays and the accel's Morton-ordered points.
+// the traversal arrays and, when requested, the k-NN accel's Morton-ordered
+// points and the radix-tree records of nodes inside each 256-leaf group.
 //
 // Reference behaviour followed (torchbvh/csrc/bvh_build.cu):
 //   bounds      :453-494  fminf/fmaxf from +-1e30 seeds, per cloud
