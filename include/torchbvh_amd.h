@@ -173,10 +173,11 @@ int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets,
 /* ---- traversal schedule ----------------------------------------------------------------
  * No counterpart in the reference (`query_knn` there orders queries with the
  * full sort above, `_query.py:142,241`).  The order only schedules the
- * traversal — k-NN results do not depend on it — so these sort on the top
- * 16 Morton bits only (stable: ties keep ascending query index), two radix
- * passes instead of four; measured on MI355X the traversal is as fast as
- * with the full order.  Same arguments and workspace sizes as
+ * traversal — k-NN results do not depend on it — so these key each query
+ * on the Hilbert index of its Morton-grid cell (1024 cells per axis in 3-D,
+ * 65536 in 2-D; J. Skilling, AIP Conf. Proc. 707, 2004) and sort on its top
+ * 16 bits only (stable: ties keep ascending query index), two radix passes
+ * instead of four.  Same arguments and workspace sizes as
  * tbvh_sort_queries / tbvh_sort_queries_ragged. */
 int tbvh_schedule_queries(const float* queries, int64_t B, int64_t M, int D,
                           const float* scene_min, const float* scene_max,

@@ -48,6 +48,8 @@ def lib():
         L.orc_morton.argtypes = [_f32p, c_int, _f32p, _f32p]
         L.orc_morton.restype = ctypes.c_uint32
         L.orc_morton_codes.argtypes = [_f32p, c_i64, c_int, _f32p, _f32p, _u32p]
+        L.orc_hilbert_codes.argtypes = [_f32p, c_i64, c_int, _f32p, _f32p, _u32p]
+        L.orc_hilbert_cells.argtypes = [_u32p, c_i64, c_int, c_int, _u32p]
         L.orc_bounds.argtypes = [_f32p, c_i64, c_int, _f32p, _f32p]
         L.orc_stable_argsort.argtypes = [_u32p, c_i64, _i64p]
         L.orc_build.argtypes = [_f32p, c_int, c_int, _f32p, _i64p, _f32p, _f32p, _i32p, _i32p, _i32p]
@@ -113,6 +115,24 @@ def morton_codes(points, lo, hi) -> np.ndarray:
     n, D = p.shape
     out = np.empty(n, np.uint32)
     lib().orc_morton_codes(p, n, D, _f32(lo), _f32(hi), out)
+    return out
+
+
+def hilbert_codes(points, lo, hi) -> np.ndarray:
+    """Hilbert index of each point's Morton cell (30 bits in 3-D, 32 in 2-D)."""
+    p = _f32(points)
+    n, D = p.shape
+    out = np.empty(n, np.uint32)
+    lib().orc_hilbert_codes(p, n, D, _f32(lo), _f32(hi), out)
+    return out
+
+
+def hilbert_of_cells(cells, bits: int) -> np.ndarray:
+    """Hilbert index of integer cells (n, D) with `bits` bits per axis."""
+    c = np.ascontiguousarray(cells, dtype=np.uint32)
+    n, D = c.shape
+    out = np.empty(n, np.uint32)
+    lib().orc_hilbert_cells(c, n, D, bits, out)
     return out
 
 
@@ -184,10 +204,11 @@ def query_order(queries, scene_min, scene_max) -> np.ndarray:
 def schedule_order(queries, scene_min, scene_max) -> np.ndarray:
     """Traversal schedule of this library's query_knn (no reference
     counterpart; the reference uses query_order above): stable order by the
-    top 16 bits of the Morton code, ties by ascending query index."""
+    top 16 bits of the Hilbert index of the query's Morton cell, ties by
+    ascending query index."""
     q = _f32(queries)
     bits = 30 if q.shape[1] == 3 else 32
-    codes = morton_codes(q, scene_min, scene_max).astype(np.uint64)
+    codes = hilbert_codes(q, scene_min, scene_max).astype(np.uint64)
     return stable_argsort((codes >> np.uint64(bits - 16)).astype(np.uint32))
 
 

@@ -100,6 +100,52 @@ void orc_morton_codes(const float* pts, int64_t n, int D, const float* lo, const
 }
 
 /* ------------------------------------------------------------------------
+ * Hilbert index of integer cells, b bits per axis (no reference
+ * counterpart: this library's traversal schedule).  Skilling, "Programming
+ * the Hilbert curve", AIP Conf. Proc. 707 (2004): the axes-to-transpose
+ * transform (undo excess work, Gray encode), then the transposed bits read
+ * level by level from the top, axis 0 first within a level.
+ * ---------------------------------------------------------------------- */
+uint32_t orc_hilbert_cell(const uint32_t* cell, int D, int b) {
+    uint32_t x[3] = {0u, 0u, 0u};
+    for (int d = 0; d < D; ++d) x[d] = cell[d];
+    for (uint32_t q = 1u << (b - 1); q > 1u; q >>= 1) {
+        const uint32_t m = q - 1u;
+        for (int i = 0; i < D; ++i) {
+            if (x[i] & q) {
+                x[0] ^= m;
+            } else {
+                const uint32_t t = (x[0] ^ x[i]) & m;
+                x[0] ^= t;
+                x[i] ^= t;
+            }
+        }
+    }
+    for (int i = 1; i < D; ++i) x[i] ^= x[i - 1];
+    uint32_t t = 0u;
+    for (uint32_t q = 1u << (b - 1); q > 1u; q >>= 1)
+        if (x[D - 1] & q) t ^= q - 1u;
+    for (int i = 0; i < D; ++i) x[i] ^= t;
+    uint32_t h = 0u;
+    for (int j = b - 1; j >= 0; --j)
+        for (int i = 0; i < D; ++i) h = (h << 1) | ((x[i] >> j) & 1u);
+    return h;
+}
+void orc_hilbert_cells(const uint32_t* cells, int64_t n, int D, int b, uint32_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_hilbert_cell(cells + i * D, D, b);
+}
+/* The same cells as the Morton codes (1024 per axis in 3-D, 65536 in 2-D). */
+void orc_hilbert_codes(const float* pts, int64_t n, int D, const float* lo, const float* hi,
+                       uint32_t* out) {
+    const int b = D == 3 ? 10 : 16;
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t c[3];
+        for (int d = 0; d < D; ++d) c[d] = quantize(normalize_axis(pts[i * D + d], lo[d], hi[d]), 1u << b);
+        out[i] = orc_hilbert_cell(c, D, b);
+    }
+}
+
+/* ------------------------------------------------------------------------
  * Bounds — torchbvh/csrc/bvh_build.cu:453-494 (fminf/fmaxf from +-1e30)
  * ---------------------------------------------------------------------- */
 void orc_bounds(const float* pts, int64_t n, int D, float* lo, float* hi) {

@@ -148,20 +148,73 @@ def test_stable_argsort_matches_numpy_stable():
 
 
 @pytest.mark.parametrize("dim", [2, 3])
-def test_schedule_order_is_stable_sort_on_top_16_code_bits(dim):
+def test_schedule_order_is_stable_sort_on_top_16_hilbert_bits(dim):
     """The schedule is pinned by its definition through a plain Python sort
-    on (code >> (bits - 16), query index): a wrong shift, an unstable sort or
-    a full-code sort all fail it (the data has many equal top bits)."""
+    on (hilbert >> (bits - 16), query index) over the Hilbert indices of the
+    queries' Morton cells (cells recomputed here with numpy's IEEE fp32
+    quantisation): a wrong shift, an unstable sort, a full-code sort or the
+    Morton curve all fail it."""
     rng = np.random.default_rng(61 + dim)
     q = rng.random((3000, dim), dtype=np.float32)
     lo = np.zeros(dim, np.float32)
     hi = np.ones(dim, np.float32)
-    codes = oracle.morton_codes(q, lo, hi).astype(np.int64)
+    b = 10 if dim == 3 else 16
+    cells = np.minimum((q * np.float32(1 << b)).astype(np.uint32), (1 << b) - 1)
+    hil = oracle.hilbert_of_cells(cells, b).astype(np.int64)
+    assert_same_int(oracle.hilbert_codes(q, lo, hi).astype(np.int64), hil, "hilbert codes")
     shift = (30 if dim == 3 else 32) - 16
-    want = sorted(range(len(codes)), key=lambda i: (codes[i] >> shift, i))
+    want = sorted(range(len(hil)), key=lambda i: (hil[i] >> shift, i))
     got = oracle.schedule_order(q, lo, hi)
     assert_same_int(got, np.array(want, np.int64), "schedule")
-    assert not np.array_equal(got, oracle.query_order(q, lo, hi))  # coarser than the full order
+    codes = oracle.morton_codes(q, lo, hi).astype(np.int64)
+    morton_sched = sorted(range(len(codes)), key=lambda i: (codes[i] >> shift, i))
+    assert not np.array_equal(got, np.array(morton_sched))
+
+
+def all_cells(dim: int, b: int) -> np.ndarray:
+    axes = np.meshgrid(*[np.arange(1 << b)] * dim, indexing="ij")
+    return np.stack([a.ravel() for a in axes], axis=1).astype(np.uint32)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_hilbert_index_at_full_resolution_on_aligned_subcubes(dim):
+    """At the schedule's resolution (10 bits per axis in 3-D, 16 in 2-D) the
+    grid is too large to enumerate; by the prefix property every aligned
+    sub-cube is a contiguous index range and a jump-free path through it,
+    checked on random aligned 8^3 / 32^2 sub-cubes."""
+    b = 10 if dim == 3 else 16
+    side = 8 if dim == 3 else 32
+    rng = np.random.default_rng(900 + dim)
+    local = all_cells(dim, side.bit_length() - 1)
+    for _ in range(20):
+        corner = rng.integers(0, (1 << b) // side, dim) * side
+        cells = (local + corner).astype(np.uint32)
+        h = oracle.hilbert_of_cells(cells, b).astype(np.int64)
+        hs = np.sort(h)
+        assert hs[-1] - hs[0] == len(h) - 1, "not a contiguous range"
+        path = cells[np.argsort(h)].astype(np.int64)
+        assert np.all(np.abs(np.diff(path, axis=0)).sum(1) == 1)
+
+
+@pytest.mark.parametrize("dim,b", [(2, 1), (2, 2), (2, 3), (2, 5), (3, 1), (3, 2), (3, 3), (3, 4)])
+def test_hilbert_index_is_a_hilbert_curve(dim, b):
+    """What makes an order a Hilbert curve, checked on every cell of small
+    grids: a bijection onto [0, 2^(D*b)) starting at the origin, consecutive
+    indices at unit L1 distance (no jumps), and every prefix of D*k bits
+    covering exactly one aligned cube of side 2^(b-k)."""
+    cells = all_cells(dim, b)
+    h = oracle.hilbert_of_cells(cells, b).astype(np.int64)
+    assert_same_int(np.sort(h), np.arange(len(h)), "bijection")
+    path = cells[np.argsort(h)].astype(np.int64)
+    assert np.all(path[0] == 0)
+    assert np.all(np.abs(np.diff(path, axis=0)).sum(1) == 1), "consecutive cells must be adjacent"
+    for k in range(1, b + 1):
+        side = 1 << (b - k)
+        for prefix in np.unique(h >> (dim * (b - k))):
+            members = cells[(h >> (dim * (b - k))) == prefix].astype(np.int64)
+            corner = members.min(0)
+            assert np.all(corner % side == 0) and np.all(members.max(0) - corner == side - 1)
+            assert len(members) == side ** dim
 
 
 @pytest.mark.parametrize("dim", [2, 3])

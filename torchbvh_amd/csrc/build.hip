@@ -291,11 +291,11 @@ __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// Morton codes + the first sort digit's tile counts
+// Morton (or schedule Hilbert) keys + the first sort digit's tile counts
 // ---------------------------------------------------------------------------
 // One work-group per tile (the sort's tiles).  Digit counts are gathered
 // with LDS atomics and stored digit-major; surplus tiles store zeros.
-template <int D>
+template <int D, bool kHilbert>
 __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __restrict__ points,
                                                               const Segment* __restrict__ segs, int S,
                                                               const float* __restrict__ scene_min,
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __res
     for (int i = 0; i < kTileRows; ++i) {
         const int j = i * kTileThreads + threadIdx.x;
         if (j < count) {
-            const uint32_t code = morton::encode<D>(r[i].v, lo, hi);
+            const uint32_t code = kHilbert ? hilbert::encode<D>(r[i].v, lo, hi) : morton::encode<D>(r[i].v, lo, hi);
             keys[row0 + j] = code;
             if (tile_hist) atomicAdd(&s_hist[(code >> first_bit) & (kRadix - 1)], 1u);
         }
@@ -595,12 +595,14 @@ hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_
                          uint32_t* tile_hist, int64_t tstride, SortBits bits, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
+    auto run = [&](auto kernel) {
+        kernel<<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
+                                                  tstride, bits.first_bit);
+    };
     if (D == 3) {
-        morton_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys,
-                                                            tile_hist, tstride, bits.first_bit);
+        bits.hilbert ? run(morton_kernel<3, true>) : run(morton_kernel<3, false>);
     } else {
-        morton_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys,
-                                                            tile_hist, tstride, bits.first_bit);
+        bits.hilbert ? run(morton_kernel<2, true>) : run(morton_kernel<2, false>);
     }
     return hipGetLastError();
 }

@@ -126,9 +126,9 @@ bool supported_k(int k) { return k == 4 || k == 8 || k == 16 || k == 32; }
 int full_key_bits(int D) { return D == 3 ? 30 : 32; }
 
 // Digits of a full Morton sort, and of the traversal schedule (the top 16
-// code bits: two passes instead of four).
+// bits of Hilbert keys on the same grid: two passes instead of four).
 SortBits full_sort(int D) { return SortBits{0, full_key_bits(D)}; }
-SortBits schedule_sort(int D) { return SortBits{full_key_bits(D) - 16, full_key_bits(D)}; }
+SortBits schedule_sort(int D) { return SortBits{full_key_bits(D) - 16, full_key_bits(D), true}; }
 
 // Everything one build call launches, in order: plan (+ clear), bounds
 // (primitive builds: boxes, centres and bounds), Morton (+ the first

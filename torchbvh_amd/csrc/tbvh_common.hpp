@@ -137,6 +137,55 @@ constexpr int key_bits() { return D == 3 ? 30 : 32; }
 }  // namespace morton
 
 // ---------------------------------------------------------------------------
+// Hilbert keys on the Morton grid (1024 cells per axis in 3-D, 65536 in 2-D),
+// used only to order queries for traversal: consecutive keys are adjacent
+// cells, so a wave's queries stay closer together than along the Z curve.
+// Cell -> index follows J. Skilling, "Programming the Hilbert curve", AIP
+// Conf. Proc. 707 (2004): the AxesToTranspose steps, then the transposed
+// index read level by level from the top with axis 0 the most significant
+// bit of each level.
+// ---------------------------------------------------------------------------
+namespace hilbert {
+
+template <int D>
+TBVH_HD uint32_t encode(const float* p, const float* lo, const float* hi) {
+    constexpr int b = D == 3 ? 10 : 16;
+    constexpr uint32_t bins = 1u << b;
+    uint32_t x[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) x[d] = morton::cell(morton::unit_coord(p[d], lo[d], hi[d]), bins);
+    // Inverse undo: reflect / exchange low bits level by level.
+    for (uint32_t q = 1u << (b - 1); q > 1u; q >>= 1) {
+        const uint32_t m = q - 1u;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            if (x[i] & q) {
+                x[0] ^= m;
+            } else {
+                const uint32_t t = (x[0] ^ x[i]) & m;
+                x[0] ^= t;
+                x[i] ^= t;
+            }
+        }
+    }
+    // Gray encode.
+#pragma unroll
+    for (int i = 1; i < D; ++i) x[i] ^= x[i - 1];
+    uint32_t t = 0u;
+    for (uint32_t q = 1u << (b - 1); q > 1u; q >>= 1)
+        if (x[D - 1] & q) t ^= q - 1u;
+#pragma unroll
+    for (int i = 0; i < D; ++i) x[i] ^= t;
+    if constexpr (D == 3) {
+        return morton::spread3(x[2]) | (morton::spread3(x[1]) << 1) | (morton::spread3(x[0]) << 2);
+    } else {
+        return morton::spread2(x[1]) | (morton::spread2(x[0]) << 1);
+    }
+}
+
+}  // namespace hilbert
+
+// ---------------------------------------------------------------------------
 // Segments.  Single, batched and ragged inputs are all a list of clouds
 // ("segments") packed back to back; kernels index them through this table,
 // which a planning kernel fills on the device from either (B, N) or device

@@ -126,10 +126,12 @@ hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_
                          hipStream_t stream);
 
 // Digit range of a sort: 8-bit digits at bits first_bit, first_bit + 8, ...
-// below end_bit (so passes = ceil((end_bit - first_bit) / 8) <= 4).
+// below end_bit (so passes = ceil((end_bit - first_bit) / 8) <= 4), and the
+// curve launch_morton keys rows on (Hilbert only for the query schedule).
 struct SortBits {
     int first_bit;
     int end_bit;
+    bool hilbert = false;
     int passes() const { return (end_bit - first_bit + kRadixBits - 1) / kRadixBits; }
 };
 
@@ -139,7 +141,8 @@ hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment
                                  int64_t tiles, float* centers, float* boxes, float* partials,
                                  float* scene_min, float* scene_max, hipStream_t stream);
 
-// Morton codes of every row against its segment's bounds and, unless
+// Morton (or, with bits.hilbert, Hilbert) keys of every row against its
+// segment's bounds and, unless
 // `tile_hist` is null, every tile's count of the first sort digit (digit at
 // bits.first_bit; [digit][tile], row stride `tstride`, surplus tiles zero).
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
