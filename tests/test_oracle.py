@@ -177,6 +177,19 @@ def all_cells(dim: int, b: int) -> np.ndarray:
 
 
 @pytest.mark.parametrize("dim", [2, 3])
+def test_hilbert_top_levels_depend_only_on_top_cell_levels(dim):
+    """The schedule sorts on the top 16 index bits, and the GPU key computes
+    only those: the index of the top 6 (3-D) / 8 (2-D) levels of the cell.
+    That equals the full index's top bits (self-similarity)."""
+    b, top = (10, 6) if dim == 3 else (16, 8)
+    rng = np.random.default_rng(77 + dim)
+    cells = rng.integers(0, 1 << b, (100_000, dim)).astype(np.uint32)
+    full = oracle.hilbert_of_cells(cells, b).astype(np.uint64)
+    coarse = oracle.hilbert_of_cells((cells >> (b - top)).astype(np.uint32), top).astype(np.uint64)
+    assert np.array_equal(full >> np.uint64(dim * (b - top)), coarse)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
 def test_hilbert_index_at_full_resolution_on_aligned_subcubes(dim):
     """At the schedule's resolution (10 bits per axis in 3-D, 16 in 2-D) the
     grid is too large to enumerate; by the prefix property every aligned

@@ -16,7 +16,7 @@
 //                  box (2D floats), left ref, right ref, 2 pad words
 //                  (16 floats = 64 B in 3-D, 12 floats = 48 B in 2-D)
 // A child ref >= 0 is an internal node; a negative ref is a bucket of at most
-// accel_bucket<D>() (4 in 3-D, 8 in 2-D) consecutive points:
+// accel_bucket<D>() (6 in 3-D, 8 in 2-D) consecutive points:
 // 0x80000000 | (count - 1) << 28 | first.  Cloud c's
 // records start at row (first point of c) - c.
 //

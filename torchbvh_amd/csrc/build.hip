@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __res
     for (int i = 0; i < kTileRows; ++i) {
         const int j = i * kTileThreads + threadIdx.x;
         if (j < count) {
-            const uint32_t code = kHilbert ? hilbert::encode<D>(r[i].v, lo, hi) : morton::encode<D>(r[i].v, lo, hi);
+            const uint32_t code = kHilbert ? hilbert::schedule_key<D>(r[i].v, lo, hi) : morton::encode<D>(r[i].v, lo, hi);
             keys[row0 + j] = code;
             if (tile_hist) atomicAdd(&s_hist[(code >> first_bit) & (kRadix - 1)], 1u);
         }

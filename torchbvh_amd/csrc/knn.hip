@@ -45,15 +45,37 @@ __device__ __forceinline__ uint64_t candidate_key(float dist, uint32_t idx) {
     return (static_cast<uint64_t>(__float_as_uint(dist)) << 32) | idx;
 }
 
-// Insert `key` into the ascending list `best`, dropping the largest entry.
+// Minimum / maximum of two candidate keys by f64 min / max.  A key read as
+// an IEEE double is never negative and never NaN: its sign bit is the sign
+// of a distance >= 0, and an all-ones exponent field would need a float
+// distance with an all-ones exponent (inf/NaN), which is never inserted
+// (the largest key holds FLT_MAX).  Such doubles order exactly like the
+// 64-bit unsigned keys, and with f64 denormals kept (the default mode;
+// distance-0 keys read as denormals) v_min_f64 / v_max_f64 return one
+// operand bit for bit.  Written as instructions: the compiler's fmin/fmax
+// would first canonicalise each operand, one more instruction per slot.
+__device__ __forceinline__ uint64_t key_min(uint64_t a, uint64_t b) {
+    double r;
+    asm("v_min_f64 %0, %1, %2" : "=v"(r) : "v"(__longlong_as_double(a)), "v"(__longlong_as_double(b)));
+    return static_cast<uint64_t>(__double_as_longlong(r));
+}
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) {
+    double r;
+    asm("v_max_f64 %0, %1, %2" : "=v"(r) : "v"(__longlong_as_double(a)), "v"(__longlong_as_double(b)));
+    return static_cast<uint64_t>(__double_as_longlong(r));
+}
+
+// Insert `key` into the ascending list `best`, dropping the largest entry:
+// slot i becomes min(best[i], max(best[i - 1], key)), which is best[i]
+// below the insertion point, key at it and best[i - 1] above it.  Two
+// independent instructions per slot (a compare-and-select chain needs a
+// compare and four selects, serialised through the compare mask); measured
+// on MI355X: traversal -7% at k = 16 (cfg2), -20% at k = 32 (cfg5).
 template <int K>
 __device__ __forceinline__ void insert_sorted(uint64_t (&best)[K], uint64_t key) {
-    bool lt[K];
 #pragma unroll
-    for (int i = 0; i < K; ++i) lt[i] = key < best[i];
-#pragma unroll
-    for (int i = K - 1; i > 0; --i) best[i] = lt[i - 1] ? best[i - 1] : (lt[i] ? key : best[i]);
-    best[0] = lt[0] ? key : best[0];
+    for (int i = K - 1; i > 0; --i) best[i] = key_min(best[i], key_max(best[i - 1], key));
+    best[0] = key_min(best[0], key);
 }
 
 template <int D, int K, bool kOrdered, bool kRagged>
@@ -232,13 +254,6 @@ __device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int 
     }
 }
 
-// Buckets a lane may park before it waits for the wave's next bucket round
-// (measured on MI355X: two for k <= 8, one for k >= 16).
-template <int K>
-struct Parking {
-    static constexpr int slots = K <= 8 ? 2 : 1;
-};
-
 // Branch-and-bound over the acceleration structure (see accel.hip): the
 // pruning rule, near-first order and cached far-child distances of the
 // implicit-tree kernel above; deferred nodes on a per-lane stack.
@@ -246,7 +261,9 @@ struct Parking {
 // Postponed buckets.  With one query per lane, the O(K) insertion into the
 // sorted list is the dominant cost, and the wave pays for it whenever any
 // lane inserts.  So a lane that reaches a bucket parks it and keeps
-// traversing; a lane that reaches a bucket with no free parking slot waits.
+// traversing; a lane that reaches a bucket while it holds one waits (one
+// parked bucket per lane: two measured 2% slower at k = 8 and no better at
+// k >= 16).
 // At the loop head, which every lane of the wave passes each iteration, the
 // wave scans all parked buckets together once at least half of its live
 // lanes hold one, or no lane can move: the insertions then run with most
@@ -265,7 +282,6 @@ struct Parking {
 template <int D, int K, bool kOrdered, bool kRagged>
 __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     constexpr int R = 4 * D + 4;
-    constexpr int kSlots = Parking<K>::slots;
     __shared__ uint64_t lds_stack[kLdsStack * kAccelBlock];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
@@ -321,9 +337,7 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
                       ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
                       : 0;
     float nd = 0.0f;
-    int32_t parked[kSlots];  // bucket refs are negative, so 0 means a free slot
-#pragma unroll
-    for (int s = 0; s < kSlots; ++s) parked[s] = 0;
+    int32_t parked = 0;  // bucket refs are negative, so 0 means none
     bool waiting = false;
     bool done = false;
 
@@ -331,41 +345,31 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     // in a tight loop (a flag-driven single loop of the same work measured
     // 2x slower).
     while (true) {
-        const uint64_t holding = __ballot(parked[0] != 0);
+        const uint64_t holding = __ballot(parked != 0);
         if (holding != 0) {
             const uint64_t live = __ballot(true);
             const uint64_t movable = __ballot(!waiting && !done);
             if (movable == 0 || __popcll(live) <= 2 * __popcll(holding)) {
-#pragma unroll
-                for (int s = 0; s < kSlots; ++s) {
-                    if (parked[s] != 0) scan_bucket<D>(pts, parked[s], n, q, best);
-                    parked[s] = 0;
-                }
+                if (parked != 0) scan_bucket<D>(pts, parked, n, q, best);
+                parked = 0;
                 waiting = false;
             }
         }
         if (done) {
-            if (parked[0] == 0) break;
+            if (parked == 0) break;
             continue;
         }
         if (waiting) continue;
         const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
         if (nd <= worst) {
             if (ref < 0) {
-                // Park in the first free slot (slots fill in order), else
-                // wait and revisit this bucket after the next round.
-                bool placed = false;
-#pragma unroll
-                for (int s = 0; s < kSlots; ++s) {
-                    if (!placed && parked[s] == 0) {
-                        parked[s] = ref;
-                        placed = true;
-                    }
-                }
-                if (!placed) {
+                // Park the bucket; a lane already holding one waits and
+                // revisits this bucket after the next round.
+                if (parked != 0) {
                     waiting = true;
                     continue;
                 }
+                parked = ref;
             } else if (ref < n - 1) {
                 const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
                 float rec[R];

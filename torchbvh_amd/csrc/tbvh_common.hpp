@@ -144,17 +144,22 @@ constexpr int key_bits() { return D == 3 ? 30 : 32; }
 // Conf. Proc. 707 (2004): the AxesToTranspose steps, then the transposed
 // index read level by level from the top with axis 0 the most significant
 // bit of each level.
+//
+// The traversal schedule sorts on the key's top 16 bits only.  Those are
+// the index of the top 6 levels (3-D) or 8 levels (2-D): each step of the
+// transform reads one bit level and rewrites only the levels below it, so
+// the top levels of the index depend only on the top levels of the cell
+// (the curve's self-similarity).  schedule_key therefore transforms just
+// those levels of the cell and leaves the key's low bits zero: its top 16
+// bits equal the full index's, at under half the work.
 // ---------------------------------------------------------------------------
 namespace hilbert {
 
-template <int D>
-TBVH_HD uint32_t encode(const float* p, const float* lo, const float* hi) {
-    constexpr int b = D == 3 ? 10 : 16;
-    constexpr uint32_t bins = 1u << b;
-    uint32_t x[D];
+// Index of the `b`-level cell x (b bits per axis; x is clobbered).
+template <int D, int b>
+TBVH_HD uint32_t index(uint32_t (&x)[D]) {
+    // Inverse undo: reflect / exchange the lower levels, level by level.
 #pragma unroll
-    for (int d = 0; d < D; ++d) x[d] = morton::cell(morton::unit_coord(p[d], lo[d], hi[d]), bins);
-    // Inverse undo: reflect / exchange low bits level by level.
     for (uint32_t q = 1u << (b - 1); q > 1u; q >>= 1) {
         const uint32_t m = q - 1u;
 #pragma unroll
@@ -172,6 +177,7 @@ TBVH_HD uint32_t encode(const float* p, const float* lo, const float* hi) {
 #pragma unroll
     for (int i = 1; i < D; ++i) x[i] ^= x[i - 1];
     uint32_t t = 0u;
+#pragma unroll
     for (uint32_t q = 1u << (b - 1); q > 1u; q >>= 1)
         if (x[D - 1] & q) t ^= q - 1u;
 #pragma unroll
@@ -181,6 +187,18 @@ TBVH_HD uint32_t encode(const float* p, const float* lo, const float* hi) {
     } else {
         return morton::spread2(x[1]) | (morton::spread2(x[0]) << 1);
     }
+}
+
+// Schedule key: the top 16 bits of the Hilbert index of p's Morton cell in
+// bits [key_bits - 16, key_bits), zeros below.
+template <int D>
+TBVH_HD uint32_t schedule_key(const float* p, const float* lo, const float* hi) {
+    constexpr int b = D == 3 ? 10 : 16;      // levels of the full grid
+    constexpr int top = D == 3 ? 6 : 8;      // levels that fix the top 16 bits
+    uint32_t x[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) x[d] = morton::cell(morton::unit_coord(p[d], lo[d], hi[d]), 1u << b) >> (b - top);
+    return index<D, top>(x) << (D * (b - top));
 }
 
 }  // namespace hilbert

@@ -189,10 +189,11 @@ hipError_t launch_tree(const float* points, int D, const Segment* segs, int64_t 
 
 // k-NN acceleration structure (radix tree + Morton-ordered float4 points).
 // Max points per leaf bucket (bucket refs hold count - 1 in 3 bits).
-// Measured on MI355X: 8 is 8% faster than 4 for 2-D k-NN (cfg4); in 3-D, 5-7
-// were within noise at k = 16 and 3-30% slower at k = 32.
+// Measured on MI355X with the min/max candidate insertion: 3-D 6 against 4:
+// -11% at cfg3, -1% at cfg2 and cfg5 (5 and 7: slower than 6 at cfg2, 8:
+// +22% at cfg5); 2-D 8 is 8% faster than 4 (cfg4), 6 slower than 8.
 template <int D>
-__host__ __device__ constexpr int accel_bucket() { return D == 2 ? 8 : 4; }
+__host__ __device__ constexpr int accel_bucket() { return D == 2 ? 8 : 6; }
 constexpr int64_t kMaxAccelCloud = int64_t(1) << 28;  // bucket refs hold 28-bit starts
 __host__ __device__ inline size_t accel_points_bytes(int64_t total) {
     return (static_cast<size_t>(total) * 16 + 255) / 256 * 256;
