@@ -205,26 +205,37 @@ __device__ __forceinline__ float point_distance(const float* q, const float4 p) 
 
 constexpr int kAccelStackDepth = 64;   // radix-tree depth <= 64 (64-bit keys)
 constexpr int kAccelBlock = 256;
-constexpr int kLdsStack = 12;          // first stack entries kept in LDS per lane
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 
-// Deferred-node stack of one lane: the first kLdsStack entries live in an
-// LDS column (stride kAccelBlock), deeper ones in scratch.  12 LDS entries
-// measured best: 16, 20 or 24 remove the scratch traffic but cost more
-// occupancy than they save.
+// Stack entries kept in LDS per lane, by dimension and k (the rest spill
+// to scratch).  Deeper LDS stacks cut scratch traffic until the LDS, not
+// the registers, limits the work-groups per CU.  Measured on MI355X against
+// 12: 3-D k = 16 with 15, -4.5% (cfg2) and -6% (cfg3), 14 and 16 slower
+// than 15; 3-D k = 32 with 15, -3% (cfg5), 14, 16 and 20 slower; 2-D k = 8
+// with 20, -2% (cfg4), 14, 18 and 24 slower.  Other (D, k) keep 12.
+template <int D, int K>
+constexpr int lds_stack_entries() {
+    if (D == 2 && K == 8) return 20;
+    if (D == 3 && K >= 16) return 15;
+    return 12;
+}
+
+// Deferred-node stack of one lane: the first L entries live in an LDS
+// column (stride kAccelBlock), deeper ones in scratch.
+template <int L>
 struct NodeStack {
     uint64_t* col;
-    uint64_t spill[kAccelStackDepth - kLdsStack];
+    uint64_t spill[kAccelStackDepth - L];
     int sp = 0;
     __device__ __forceinline__ void push(float d, int32_t ref) {
         const uint64_t e = (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<uint32_t>(ref);
-        if (sp < kLdsStack) col[sp * kAccelBlock] = e;
-        else spill[sp - kLdsStack] = e;
+        if (sp < L) col[sp * kAccelBlock] = e;
+        else spill[sp - L] = e;
         ++sp;
     }
     __device__ __forceinline__ void pop(float& d, int32_t& ref) {
         --sp;
-        const uint64_t e = sp < kLdsStack ? col[sp * kAccelBlock] : spill[sp - kLdsStack];
+        const uint64_t e = sp < L ? col[sp * kAccelBlock] : spill[sp - L];
         ref = static_cast<int32_t>(static_cast<uint32_t>(e));
         d = __uint_as_float(static_cast<uint32_t>(e >> 32));
     }
@@ -282,7 +293,8 @@ __device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int 
 template <int D, int K, bool kOrdered, bool kRagged>
 __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     constexpr int R = 4 * D + 4;
-    __shared__ uint64_t lds_stack[kLdsStack * kAccelBlock];
+    constexpr int kLds = lds_stack_entries<D, K>();
+    __shared__ uint64_t lds_stack[kLds * kAccelBlock];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     const int64_t gid = tile * kAccelBlock + threadIdx.x;
@@ -331,7 +343,7 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
 #pragma unroll
     for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
 
-    NodeStack stack;
+    NodeStack<kLds> stack;
     stack.col = lds_stack + threadIdx.x;
     int32_t ref = n <= accel_bucket<D>()
                       ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
