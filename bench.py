@@ -100,7 +100,8 @@ def make_workload(name: str, scale: float = 1.0) -> dict:
 
 
 # ---------------------------------------------------------------------------
-# Algorithmic bytes (fixed formulas)
+# Algorithmic bytes: fixed per-unit formulas, independent of this
+# implementation's pass count
 # ---------------------------------------------------------------------------
 def real_node_count(n: int) -> int:
     L = (n - 1).bit_length()
@@ -195,7 +196,7 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md, not implemented", file=sys.stderr)
+              "sharding across GPUs is not implemented", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
