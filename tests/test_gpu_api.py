@@ -96,12 +96,38 @@ def test_sort_queries_routes_through_ordered_traversal(monkeypatch):
     def fake_unordered(*args, **kwargs):
         raise AssertionError("unordered route must not be used when sort_queries=True")
 
+    monkeypatch.setattr(query_module, "SCHEDULE_MIN_QUERIES", 0)
     monkeypatch.setattr(query_module._C, "morton_sort_queries_narrow", fake_sort)
     monkeypatch.setattr(query_module._C, "query_knn_batched_cached_bounds_ordered", fake_ordered)
     monkeypatch.setattr(query_module._C, "query_knn_batched_cached_bounds", fake_unordered)
     idx, dist = tb.query_knn(bvh, pts[:5].contiguous(), 4, sort_queries=True)
     assert idx.shape == (5, 4)
     assert calls == [("sort", (1, 5, 3)), ("ordered", (1, 5), 4)]
+
+
+def test_small_query_sets_traverse_in_input_order(monkeypatch):
+    """Up to SCHEDULE_MIN_QUERIES queries, query_knn skips the schedule sort
+    even with sort_queries=True (the order never changes results); above it
+    the schedule is used."""
+    pts = rand(16, 3, seed=4)
+    bvh = tb.build_bvh(pts)
+    calls = []
+    real_sort = query_module._C.morton_sort_queries_narrow
+
+    def counting_sort(*args, **kwargs):
+        calls.append("sort")
+        return real_sort(*args, **kwargs)
+
+    monkeypatch.setattr(query_module._C, "morton_sort_queries_narrow", counting_sort)
+    q = pts[:6].contiguous()
+    want = tb.query_knn(bvh, q, 4, sort_queries=False)
+    got = tb.query_knn(bvh, q, 4, sort_queries=True)
+    assert calls == []
+    monkeypatch.setattr(query_module, "SCHEDULE_MIN_QUERIES", 5)
+    got_sched = tb.query_knn(bvh, q, 4, sort_queries=True)
+    assert calls == ["sort"]
+    for a, b in ((got, want), (got_sched, want)):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
 def test_batched_lifecycle_and_validation():

@@ -24,6 +24,18 @@ from torchbvh_amd import _native
 from torchbvh_amd._native import _C
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, params=["scheduled", "input-order"])
+def schedule_mode(request, monkeypatch):
+    """Every case twice: query_knn with the traversal schedule forced on
+    (threshold 0) and with its default, under which these small query sets
+    traverse in input order."""
+    from torchbvh_amd import _query
+
+    if request.param == "scheduled":
+        monkeypatch.setattr(_query, "SCHEDULE_MIN_QUERIES", 0)
+    return request.param
 DEV = torch.device("cuda")
 DIST_RTOL = 1e-6  # contractual tolerance; checked in addition to bit equality
 

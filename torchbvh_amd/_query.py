@@ -151,6 +151,18 @@ def build_bvh(
 # ---------------------------------------------------------------------------
 # Queries
 # ---------------------------------------------------------------------------
+# query_knn orders its traversal (the Hilbert schedule) only above this many
+# queries.  Results do not depend on the order; below it the two-pass sort
+# costs more than the coherence it buys (measured on MI355X with random-order
+# queries: 10k-100k queries traverse 10-35% faster unsorted, sort included;
+# from ~2^17-2^18 up the sorted order wins, 2x at 1M).
+SCHEDULE_MIN_QUERIES = 1 << 17
+
+
+def _schedule(sort_queries: bool, total_queries: int) -> bool:
+    return sort_queries and total_queries > SCHEDULE_MIN_QUERIES
+
+
 def _query_knn_single(
     bvh: BVHHandle,
     query_points: torch.Tensor,
@@ -172,7 +184,7 @@ def _query_knn_single(
     node_aabbs = data["node_aabbs"].unsqueeze(0)
     sorted_indices = data["sorted_indices"].unsqueeze(0)
     accel = bvh._aux.get("accel")
-    if sort_queries:
+    if _schedule(sort_queries, int(queries.size(1))):
         order = _C.morton_sort_queries_narrow(
             queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0), schedule=True
         )
@@ -247,7 +259,7 @@ def _query_knn_batched(
         raise ValueError("query_knn: query_points must be on the same device as the BVH")
     queries = _as_contiguous(query_points)
     accel = bvh._aux.get("accel")
-    if sort_queries:
+    if _schedule(sort_queries, int(queries.size(0) * queries.size(1))):
         order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"],
                                               schedule=True)
         indices, distances = _C.query_knn_batched_cached_bounds_ordered(
@@ -312,10 +324,12 @@ def _query_knn_ragged(
         source_points = _as_contiguous(source_points)
 
     packed = bvh._aux["packed"]
-    order = _C.morton_sort_queries_ragged(
-        queries, query_offsets, packed["scene_min"], packed["scene_max"], data["batch_size"],
-        schedule=True,
-    )
+    order = None
+    if _schedule(True, int(queries.size(0))):
+        order = _C.morton_sort_queries_ragged(
+            queries, query_offsets, packed["scene_min"], packed["scene_max"], data["batch_size"],
+            schedule=True,
+        )
     indices, distances = _C.query_knn_ragged(
         packed["node_aabbs"], packed["sorted_indices"], data["batch_offsets"],
         packed["node_offsets"], queries, query_offsets, order, data["batch_size"],
