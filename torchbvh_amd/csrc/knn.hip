@@ -204,7 +204,10 @@ __device__ __forceinline__ float point_distance(const float* q, const float4 p) 
 }
 
 constexpr int kAccelStackDepth = 64;   // radix-tree depth <= 64 (64-bit keys)
-constexpr int kAccelBlock = 256;
+// One wave per work-group: measured against 256 threads, -3.5% at cfg2 and
+// -14% at cfg5, whose waves differ most in cost (finer-grained balancing
+// over the CUs); 128 falls between, 512 is 13-24% slower.
+constexpr int kAccelBlock = 64;
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 
 // Stack entries kept in LDS per lane, by dimension and k (the rest spill
