@@ -214,11 +214,12 @@ constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-ro
 // to scratch).  Deeper LDS stacks cut scratch traffic until the LDS, not
 // the registers, limits the work-groups per CU.  Measured on MI355X against
 // 12: 3-D k = 16 with 15, -4.5% (cfg2) and -6% (cfg3), 14 and 16 slower
-// than 15; 3-D k = 32 with 15, -3% (cfg5), 14, 16 and 20 slower; 2-D k = 8
-// with 20, -2% (cfg4), 14, 18 and 24 slower.  Other (D, k) keep 12.
+// than 15; 3-D k = 32 with 20, -4% (cfg5; -1% over 15), 14 and 16 slower; 2-D k = 8 with 20,
+// -2% (cfg4), 14, 16, 18 and 24 slower.  Other (D, k) keep 12.
 template <int D, int K>
 constexpr int lds_stack_entries() {
     if (D == 2 && K == 8) return 20;
+    if (D == 3 && K >= 32) return 20;
     if (D == 3 && K >= 16) return 15;
     return 12;
 }
