@@ -298,14 +298,16 @@ __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __r
 template <int D, bool kHilbert>
 __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __restrict__ points,
                                                               const Segment* __restrict__ segs, int S,
-                                                              const float* __restrict__ scene_min,
-                                                              const float* __restrict__ scene_max,
+                                                              float* __restrict__ scene_min,
+                                                              float* __restrict__ scene_max,
                                                               uint32_t* __restrict__ keys,
                                                               uint32_t* __restrict__ tile_hist, int64_t tstride,
-                                                              int first_bit) {
+                                                              int first_bit, BoundsFinish fin) {
     static_assert(kTileThreads >= kRadix, "one thread per digit");
     __shared__ int s_seg;
     __shared__ uint32_t s_hist[kRadix];
+    __shared__ float s_red[kTileThreads / kWave][2 * D];
+    __shared__ float s_box[2 * D];
     const int64_t t = blockIdx.x;
     if (threadIdx.x < kRadix) s_hist[threadIdx.x] = 0u;
     const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
@@ -326,10 +328,37 @@ __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __res
         if (j < count) r[i] = rows[j];
     }
     float lo[D], hi[D];
+    if (fin.partials) {
+        // The cloud's bounds from its tiles' partial boxes: every work-group
+        // of the cloud reduces the same rows (min/max is exact, so all get
+        // the same box) and the first one stores it.
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        lo[d] = scene_min[static_cast<int64_t>(s) * D + d];
-        hi[d] = scene_max[static_cast<int64_t>(s) * D + d];
+        for (int d = 0; d < D; ++d) { lo[d] = fin.seed_lo; hi[d] = fin.seed_hi; }
+        for (int j = threadIdx.x; j < g.tiles; j += kTileThreads) {
+            const float* p = fin.partials + (static_cast<int64_t>(g.tile_first) + j) * 2 * D;
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                lo[d] = fminf(lo[d], p[d]);
+                hi[d] = fmaxf(hi[d], p[D + d]);
+            }
+        }
+        block_box<D, kTileThreads>(lo, hi, s_red, s_box);
+        __syncthreads();
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            lo[d] = s_box[d];
+            hi[d] = s_box[D + d];
+        }
+        if (lt == 0 && threadIdx.x < D) {
+            scene_min[static_cast<int64_t>(s) * D + threadIdx.x] = s_box[threadIdx.x];
+            scene_max[static_cast<int64_t>(s) * D + threadIdx.x] = s_box[D + threadIdx.x];
+        }
+    } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            lo[d] = scene_min[static_cast<int64_t>(s) * D + d];
+            hi[d] = scene_max[static_cast<int64_t>(s) * D + d];
+        }
     }
 #pragma unroll
     for (int i = 0; i < kTileRows; ++i) {
@@ -555,35 +584,44 @@ hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S,
 
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles, float* partials, float* scene_min, float* scene_max,
-                         hipStream_t stream) {
+                         bool finalize, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
+    const unsigned cgrid = static_cast<unsigned>(S);
     const int Si = static_cast<int>(S);
     if (D == 3) {
         bounds_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, partials);
-        bounds_final_kernel<3><<<static_cast<unsigned>(S), kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi,
-                                                                                scene_min, scene_max);
+        if (finalize) {
+            bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi, scene_min,
+                                                                 scene_max);
+        }
     } else {
         bounds_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, partials);
-        bounds_final_kernel<2><<<static_cast<unsigned>(S), kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi,
-                                                                                scene_min, scene_max);
+        if (finalize) {
+            bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi, scene_min,
+                                                                 scene_max);
+        }
     }
     return hipGetLastError();
 }
 
 hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment* segs, int64_t S,
                                  int64_t tiles, float* centers, float* boxes, float* partials,
-                                 float* scene_min, float* scene_max, hipStream_t stream) {
+                                 float* scene_min, float* scene_max, bool finalize, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const unsigned cgrid = static_cast<unsigned>(S);
     const int Si = static_cast<int>(S);
     if (D == 3 && V == 3) {
         primitive_prep_kernel<3, 3><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials);
-        bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, INFINITY, -INFINITY, scene_min,
-                                                             scene_max);
+        if (finalize) {
+            bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, INFINITY, -INFINITY, scene_min,
+                                                                 scene_max);
+        }
     } else if (D == 2 && V == 2) {
         primitive_prep_kernel<2, 2><<<grid, kBlock, 0, stream>>>(prims, segs, Si, centers, boxes, partials);
-        bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, INFINITY, -INFINITY, scene_min,
-                                                             scene_max);
+        if (finalize) {
+            bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, INFINITY, -INFINITY, scene_min,
+                                                                 scene_max);
+        }
     } else {
         return hipErrorInvalidValue;
     }
@@ -591,13 +629,13 @@ hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment
 }
 
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S, int64_t tiles,
-                         const float* scene_min, const float* scene_max, uint32_t* keys,
-                         uint32_t* tile_hist, int64_t tstride, SortBits bits, hipStream_t stream) {
+                         float* scene_min, float* scene_max, uint32_t* keys, uint32_t* tile_hist,
+                         int64_t tstride, SortBits bits, BoundsFinish fin, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
     auto run = [&](auto kernel) {
         kernel<<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
-                                                  tstride, bits.first_bit);
+                                                  tstride, bits.first_bit, fin);
     };
     if (D == 3) {
         bits.hilbert ? run(morton_kernel<3, true>) : run(morton_kernel<3, false>);

@@ -162,22 +162,32 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
     if (e != hipSuccess) return e;
     float* partials = carve<float>(ws, l.partials);
     const float* boxes = nullptr;
+    // Bounds reduced inside the Morton kernel unless a cloud may span more
+    // than kFuseBoundsTiles tiles (ragged: bounded by all rows).
+    const int64_t cloud_bound = ragged ? rows : n_uniform;
+    const bool fuse = (cloud_bound + kSortTile - 1) / kSortTile <= kFuseBoundsTiles;
+    BoundsFinish fin;
+    if (fuse) {
+        fin.partials = partials;
+        fin.seed_lo = V > 0 ? INFINITY : kSeedLo;
+        fin.seed_hi = V > 0 ? -INFINITY : kSeedHi;
+    }
     if (V > 0) {
         float* centers = carve<float>(ws, l.centers);
         float* leaf_boxes = carve<float>(ws, l.boxes);
         if ((e = launch_primitive_prep(points, D, V, segs, S, l.tiles, centers, leaf_boxes, partials,
-                                       o.scene_min, o.scene_max, stream)) != hipSuccess) {
+                                       o.scene_min, o.scene_max, !fuse, stream)) != hipSuccess) {
             return e;
         }
         points = centers;
         boxes = leaf_boxes;
-    } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max,
+    } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max, !fuse,
                                   stream)) != hipSuccess) {
         return e;
     }
     const SortBits bits = full_sort(D);
     if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.tile_hist,
-                           sb.tstride, bits, stream)) != hipSuccess) {
+                           sb.tstride, bits, fin, stream)) != hipSuccess) {
         return e;
     }
     uint32_t* sorted_keys = o.accel ? last_pass_keys(sb) : nullptr;
@@ -225,8 +235,10 @@ hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t 
                            : launch_plan_uniform(segs, S, m_uniform, false, stream);
     if (e != hipSuccess) return e;
     uint32_t* keys = codes_only ? codes_only : sb.keys_a;
-    if ((e = launch_morton(queries, D, segs, S, l.tiles, scene_min, scene_max, keys,
-                           codes_only ? nullptr : sb.tile_hist, sb.tstride, bits, stream)) != hipSuccess) {
+    // Bounds given (BoundsFinish empty): the kernel only reads them.
+    if ((e = launch_morton(queries, D, segs, S, l.tiles, const_cast<float*>(scene_min),
+                           const_cast<float*>(scene_max), keys, codes_only ? nullptr : sb.tile_hist, sb.tstride,
+                           bits, BoundsFinish{}, stream)) != hipSuccess) {
         return e;
     }
     if (codes_only) return hipSuccess;

@@ -119,11 +119,26 @@ hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S,
                                int64_t* node_offsets, hipStream_t stream);
 
 // Per-cloud bounds: one work-group per tile writes a partial box
-// (`partials`: 2D floats per tile), then one work-group per cloud reduces
-// them into scene_min/max.
+// (`partials`: 2D floats per tile); with `finalize`, one work-group per
+// cloud then reduces them into scene_min/max (otherwise launch_morton does,
+// given the same partials in a BoundsFinish).
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles_bound, float* partials, float* scene_min, float* scene_max,
-                         hipStream_t stream);
+                         bool finalize, hipStream_t stream);
+
+// Clouds of at most this many tiles get their bounds reduced inside the
+// Morton kernel (each of a cloud's work-groups reads all its partial boxes,
+// so the reads grow with the square of its tile count); larger ones take
+// the separate per-cloud reduction.
+constexpr int64_t kFuseBoundsTiles = 1024;
+
+// Bounds still to reduce when keys are computed: the partial boxes and the
+// seeds of the reduction (partials null: scene_min/max are final already).
+struct BoundsFinish {
+    const float* partials = nullptr;
+    float seed_lo = 0.0f;
+    float seed_hi = 0.0f;
+};
 
 // Digit range of a sort: 8-bit digits at bits first_bit, first_bit + 8, ...
 // below end_bit (so passes = ceil((end_bit - first_bit) / 8) <= 4), and the
@@ -139,16 +154,17 @@ struct SortBits {
 // bounds over the boxes (partials as in launch_bounds).
 hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment* segs, int64_t S,
                                  int64_t tiles, float* centers, float* boxes, float* partials,
-                                 float* scene_min, float* scene_max, hipStream_t stream);
+                                 float* scene_min, float* scene_max, bool finalize, hipStream_t stream);
 
 // Morton (or, with bits.hilbert, Hilbert) keys of every row against its
-// segment's bounds and, unless
-// `tile_hist` is null, every tile's count of the first sort digit (digit at
-// bits.first_bit; [digit][tile], row stride `tstride`, surplus tiles zero).
+// segment's bounds and, unless `tile_hist` is null, every tile's count of
+// the first sort digit (digit at bits.first_bit; [digit][tile], row stride
+// `tstride`, surplus tiles zero).  With fin.partials the bounds are first
+// reduced from the partial boxes and stored into scene_min/max.
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
-                         int64_t tiles_bound, const float* scene_min, const float* scene_max,
+                         int64_t tiles_bound, float* scene_min, float* scene_max,
                          uint32_t* keys, uint32_t* tile_hist, int64_t tstride, SortBits bits,
-                         hipStream_t stream);
+                         BoundsFinish fin, hipStream_t stream);
 
 // Stable LSD sort of (key, local index) per segment on the digits of
 // `bits`; writes int64 local indices in key order into `order` and, if
