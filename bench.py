@@ -8,6 +8,7 @@ HBM.  Prints one JSON line.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
                     [--cpu-sample Q] [--no-cpu-baseline]
     python bench.py --published   # the reference's published latency rows
+    python bench.py --extras      # spatial/routed k-NN, gather, primitive build, point order
 
 The synthetic workloads of every BASELINE config are defined here
 (``make_workload``) and shared with the parity tests.
@@ -236,6 +237,86 @@ def published_latencies() -> int:
     return 0
 
 
+def extras() -> int:
+    """The rows either side of the hot path (spatial-output k-NN, routed
+    ordering + k-NN, neighbour-position gather, primitive build, point
+    ordering), each timed with device events at a stated size and reported
+    against its algorithmic bytes; one JSON line each."""
+    import numpy as np
+
+    import torchbvh_amd as tb
+    from torchbvh_amd._native import _C
+
+    dev = torch.device("cuda:0")
+
+    def timed(fn, reps: int = 20, warmup: int = 3) -> float:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def line(row: str, workload: str, ms: float, nbytes: int, formula: str) -> None:
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"row": row, "workload": workload, "ms": round(ms, 4),
+                          "algorithmic_bytes": nbytes, "bytes_formula": formula, "gb_per_s": round(gbs, 1),
+                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+    D, K = 3, 16
+    w = make_workload("cfg2")
+    p, q = w["points"].to(dev)[None].contiguous(), w["queries"].to(dev)[None].contiguous()
+    N = Q = p.shape[1]
+    d = _C.build_bvh_batched_cooperative(p)
+    nr = d["num_real_nodes"]
+
+    def spatial():
+        order = _C.morton_sort_queries_narrow(q, d["scene_min"], d["scene_max"])
+        return _C.query_knn_batched_cached_bounds_spatial(d["node_aabbs"], d["sorted_indices"], q, order,
+                                                          N, nr, D, K)
+    line("(f)1 spatial-output k-NN (MLS call pattern: full Morton order, launch-order output)",
+         "cfg2: 1M uniform 3-D points and queries, k=16", timed(spatial),
+         qsort_bytes(Q, D) + knn_bytes(Q, D, K), "Q(4D+72) + Q(4D+4+12K)")
+
+    g = torch.Generator("cpu").manual_seed(6001)
+    nt = nf = N // 2
+    tp = torch.rand((1, nt, D), generator=g).to(dev)
+    fp = (torch.rand((1, nf, D), generator=g) * 2 - 0.5).to(dev)
+    routes = (torch.rand((1, Q), generator=g) < 0.5).to(dev)
+    dt, df = _C.build_bvh_batched_cooperative(tp), _C.build_bvh_batched_cooperative(fp)
+
+    def routed():
+        order = _C.morton_sort_routed_queries_batched(q, routes, dt["scene_min"], dt["scene_max"],
+                                                      df["scene_min"], df["scene_max"])
+        return _C.query_knn_routed_batched_cached_bounds_spatial(
+            dt["node_aabbs"], dt["sorted_indices"], df["node_aabbs"], df["sorted_indices"], q, routes, order,
+            nt, dt["num_real_nodes"], nf, df["num_real_nodes"], D, K)
+    line("(f)2 routed ordering + routed spatial k-NN (two trees, per-query route)",
+         "cfg2 queries, true/false clouds of 512k uniform points each, 50% routes, k=16", timed(routed),
+         qsort_bytes(Q, D) + Q + knn_bytes(Q, D, K), "Q(4D+72) + Q (routes) + Q(4D+4+12K)")
+
+    h = tb.build_bvh(p[0])
+    idx, _ = tb.query_knn(h, q[0], K)
+    src = p[0].contiguous()
+    line("(f)3 neighbour-position gather (query_knn source_points)", "cfg2 result rows, k=16",
+         timed(lambda: src[idx]), Q * K * (8 + 2 * 4 * D), "QK(8 + 2*4D): index read, row read, row written")
+
+    F, V = 1 << 20, 3
+    anchor = torch.rand((1, F, 1, D), generator=g)
+    prims = (anchor + (torch.rand((1, F, V, D), generator=g) - 0.5) * 0.01).contiguous().to(dev)
+    nrf = real_node_count(F)
+    line("(f)4 primitive BVH build (triangles)", "1M triangles in [0,1)^3", timed(lambda: _C.build_primitive_bvh_batched(prims)),
+         F * (4 * V * D + 24 * D + 80) + 8 * D * nrf,
+         "F(4VD + 24D + 80) + 8D nr: vertices, centres and boxes, keys, sort, leaf boxes, nodes")
+    line("(f)4 point Morton ordering (FPS)", "cfg2 points", timed(lambda: _C.morton_sort_points_batched(p)),
+         N * (8 * D + 76), "N(8D + 76): two point reads, keys, sort, int64 order")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,6 +331,8 @@ def main() -> int:
                     help="end with a 256 MiB device copy (for rocprofv3 counter calibration)")
     ap.add_argument("--published", action="store_true",
                     help="instead: time the reference's published latency rows with its protocol")
+    ap.add_argument("--extras", action="store_true",
+                    help="instead: time the rows either side of the path (spatial, routed, gather, primitives)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -261,6 +344,8 @@ def main() -> int:
         return 2
     if args.published:
         return published_latencies()
+    if args.extras:
+        return extras()
 
     import torchbvh_amd as tb
 
