@@ -170,6 +170,27 @@ int tbvh_sort_queries_ragged(const float* queries, const int64_t* query_offsets,
                              void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* ---- k-NN with neighbour rows (fused gather) ------------------------------------------
+ * No entry-point counterpart: the reference gathers source_points[indices]
+ * in Python after the k-NN call (torchbvh/_query.py:169-174, 203-215,
+ * 362-366).  These run tbvh_knn_accel / tbvh_knn_accel_ragged and also write,
+ * for result row r and neighbour j, the source row of that neighbour:
+ * out_positions[(r * k + j) * source_cols + c].  `source_points` has the
+ * points' layout ([B, num_leaves, source_cols] batched, packed rows with
+ * point_offsets ragged), float32. */
+int tbvh_knn_accel_positions(const void* accel, const float* queries, const int64_t* order,
+                             int64_t B, int64_t M, int64_t num_leaves, int D, int k,
+                             const float* source_points, int source_cols,
+                             int64_t* out_indices, float* out_distances, float* out_positions,
+                             void* stream);
+int tbvh_knn_accel_ragged_positions(const void* accel, const int64_t* point_offsets,
+                                    int64_t total_points, const float* queries,
+                                    const int64_t* query_offsets, const int64_t* order,
+                                    int64_t B, int64_t total_q, int D, int k,
+                                    const float* source_points, int source_cols,
+                                    int64_t* out_indices, float* out_distances,
+                                    float* out_positions, void* stream);
+
 /* ---- traversal schedule ----------------------------------------------------------------
  * No counterpart in the reference (`query_knn` there orders queries with the
  * full sort above, `_query.py:142,241`).  The order only schedules the

@@ -85,8 +85,8 @@ def test_sort_queries_routes_through_ordered_traversal(monkeypatch):
         B, M, _ = qb.shape
         return torch.arange(M, device=qb.device).expand(B, M).contiguous()
 
-    def fake_ordered(*args, accel=None):
-        assert accel is not None
+    def fake_ordered(*args, accel=None, source_points=None):
+        assert accel is not None and source_points is None
         calls.append(("ordered", tuple(args[3].shape), args[-1]))
         B, M, _ = args[2].shape
         k = int(args[-1])

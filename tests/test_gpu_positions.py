@@ -1,0 +1,113 @@
+"""Neighbour rows (`query_knn(..., source_points=...)`): gathered in the
+k-NN epilogue when the traversal runs on the accel and no gradient is
+needed (the binding accepts any row width), else by torch afterwards.  Either
+way the rows must equal source_points indexed by the returned indices, as
+the reference computes them (torchbvh/_query.py:169-174, 203-215, 362-366),
+and indices/distances must equal the call without source_points."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import torchbvh_amd as tb
+from torchbvh_amd import _query
+from torchbvh_amd._native import _C
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def rand(*shape, seed=0, dtype=torch.float32):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.rand(shape, generator=g, dtype=dtype).to(DEV)
+
+
+@pytest.fixture(params=["scheduled", "input-order"])
+def mode(request, monkeypatch):
+    if request.param == "scheduled":
+        monkeypatch.setattr(_query, "SCHEDULE_MIN_QUERIES", 0)
+    return request.param
+
+
+@pytest.mark.parametrize("dim,k", [(3, 16), (2, 8), (3, 32), (3, 4)])
+def test_single_rows_equal_indexing(dim, k, mode):
+    cols = dim
+    p = rand(20_000, dim, seed=1)
+    q = rand(3_000, dim, seed=2)
+    src = rand(20_000, cols, seed=3) * 10
+    h = tb.build_bvh(p)
+    idx0, d0 = tb.query_knn(h, q, k)
+    idx, d, pos = tb.query_knn(h, q, k, source_points=src)
+    assert torch.equal(idx, idx0) and torch.equal(d, d0)
+    assert pos.shape == (3_000, k, cols) and pos.dtype == torch.float32
+    assert torch.equal(pos, src[idx])
+
+
+@pytest.mark.parametrize("dim,k", [(3, 16), (2, 8)])
+def test_batched_rows_equal_indexing(dim, k, mode):
+    p = rand(3, 9_000, dim, seed=4)
+    q = rand(3, 1_500, dim, seed=5)
+    src = rand(3, 9_000, dim, seed=6)
+    h = tb.build_bvh(p)
+    idx, d, pos = tb.query_knn(h, q, k, source_points=src)
+    assert pos.shape == (3, 1_500, k, dim)
+    for b in range(3):
+        assert torch.equal(pos[b], src[b][idx[b]])
+
+
+def test_ragged_rows_equal_indexing(mode):
+    counts, qcounts = [5_000, 17, 12_000, 300], [700, 5, 2_100, 40]
+    p = rand(sum(counts), 3, seed=7)
+    q = rand(sum(qcounts), 3, seed=8)
+    po = torch.tensor(np.concatenate(([0], np.cumsum(counts))), dtype=torch.int64, device=DEV)
+    qo = torch.tensor(np.concatenate(([0], np.cumsum(qcounts))), dtype=torch.int64, device=DEV)
+    src = rand(sum(counts), 3, seed=9)
+    h = tb.build_bvh(p, batch_offsets=po)
+    idx, d, pos = tb.query_knn(h, q, 16, query_offsets=qo, source_points=src)
+    starts = torch.repeat_interleave(po[:-1], qo[1:] - qo[:-1])
+    assert torch.equal(pos, src[idx + starts[:, None]])
+
+
+def test_non_contiguous_source():
+    p = rand(8_000, 3, seed=10)
+    q = rand(900, 3, seed=11)
+    h = tb.build_bvh(p)
+    wide = rand(8_000, 6, seed=13)
+    strided = wide[:, ::2]  # non-contiguous columns: made contiguous, then fused
+    idx, _, pos = tb.query_knn(h, q, 8, source_points=strided)
+    assert torch.equal(pos, strided[idx])
+
+
+def test_sources_needing_gradients_take_the_differentiable_gather():
+    p = rand(5_000, 3, seed=17)
+    q = rand(400, 3, seed=18)
+    src = rand(5_000, 3, seed=19).requires_grad_()
+    h = tb.build_bvh(p)
+    idx, _, pos = tb.query_knn(h, q, 8, source_points=src)
+    assert pos.requires_grad and torch.equal(pos.detach(), src.detach()[idx])
+    pos.sum().backward()
+    assert torch.equal(src.grad, torch.bincount(idx.reshape(-1), minlength=5_000).float()[:, None].expand(-1, 3))
+    with torch.no_grad():
+        idx2, _, pos2 = tb.query_knn(h, q, 8, source_points=src)  # fused: no graph to build
+    assert not pos2.requires_grad and torch.equal(pos2, pos.detach())
+
+
+def test_binding_rows_without_accel_match_fused():
+    p = rand(2, 6_000, 3, seed=14)
+    q = rand(2, 800, 3, seed=15)
+    src = rand(2, 6_000, 3, seed=16)
+    d = _C.build_bvh_batched_cooperative(p)
+    args = (d["node_aabbs"], d["sorted_indices"], q, d["num_leaves"], d["num_real_nodes"], 3, 16)
+    fused = _C.query_knn_batched_cached_bounds(*args, source_points=src)
+    implicit = _C.query_knn_batched_cached_bounds(*args, accel=False, source_points=src)
+    for a, b in zip(fused, implicit):
+        assert torch.equal(a, b)
+    # The binding takes any row width (query_knn requires D columns).
+    for cols in (1, 5, 17):
+        wide = rand(2, 6_000, cols, seed=20 + cols)
+        idx, _, pos = _C.query_knn_batched_cached_bounds(*args, source_points=wide)
+        assert pos.shape == (2, 800, 16, cols)
+        for b in range(2):
+            assert torch.equal(pos[b], wide[b][idx[b]])

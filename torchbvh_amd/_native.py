@@ -96,6 +96,12 @@ def _declare(L) -> None:
     L.tbvh_knn_accel_ragged.argtypes = (
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp]
     )
+    L.tbvh_knn_accel_positions.argtypes = (
+        [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp]
+    )
+    L.tbvh_knn_accel_ragged_positions.argtypes = (
+        [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp]
+    )
     for name in (
         "tbvh_build_workspace_size", "tbvh_build", "tbvh_build_ragged_workspace_size",
         "tbvh_build_ragged", "tbvh_build_with_accel", "tbvh_build_ragged_with_accel",
@@ -105,6 +111,7 @@ def _declare(L) -> None:
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
         "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
+        "tbvh_knn_accel_positions", "tbvh_knn_accel_ragged_positions",
         "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
         "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
@@ -239,6 +246,36 @@ def _registered_accel(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor):
     if not (_same_tensor(node_aabbs, nref(), nver) and _same_tensor(sorted_indices, sref(), sver)):
         return None
     return accel
+
+
+def _fusable_source(source_points, device, lead: tuple) -> bool:
+    """True when the traversal's epilogue can gather `source_points` rows:
+    contiguous float32 on the queries' device with the points' leading
+    shape (`lead`) and at most 4096 columns, and no gradient to carry (the
+    reference's indexing is differentiable; a source that needs one takes
+    the torch gather)."""
+    if source_points is not None and torch.is_grad_enabled() and source_points.requires_grad:
+        return False
+    return (source_points is not None and isinstance(source_points, torch.Tensor)
+            and source_points.is_cuda and source_points.device == device
+            and source_points.dtype == torch.float32 and source_points.is_contiguous()
+            and source_points.dim() == len(lead) + 1 and tuple(source_points.shape[:-1]) == lead
+            and 1 <= source_points.size(-1) <= 4096)
+
+
+def _with_positions(indices, distances, positions, source_points):
+    """(indices, distances) or, when neighbour rows were asked for, also
+    the rows: the fused result, or source_points[.., indices] gathered here."""
+    if source_points is None:
+        return indices, distances
+    if positions is None:
+        if indices.dim() == 3:  # batched: [B, M, k] indices into [B, N, C] rows
+            B, M, k = indices.shape
+            rows = source_points.gather(1, indices.reshape(B, M * k, 1).expand(B, M * k, source_points.size(-1)))
+            positions = rows.reshape(B, M, k, source_points.size(-1))
+        else:
+            positions = source_points[indices]
+    return indices, distances, positions
 
 
 def _pick_accel(accel, node_aabbs: torch.Tensor, sorted_indices: torch.Tensor):
@@ -563,7 +600,7 @@ class _NativeOps:
 
     @staticmethod
     def _knn(op, node_aabbs, sorted_indices, query_points, query_order, num_leaves,
-             num_real_nodes, dim, k, accel=None, spatial=False):
+             num_real_nodes, dim, k, accel=None, spatial=False, source_points=None):
         _require(dim in (2, 3), op, "D must be 2 or 3")
         _require_device_f32(op, query_points, "query_points")
         _require(query_points.dim() == 3 and query_points.size(2) == dim, op,
@@ -588,11 +625,22 @@ class _NativeOps:
         B, M = int(query_points.size(0)), int(query_points.size(1))
         indices = torch.empty((B, M, k), dtype=torch.int64, device=dev)
         distances = torch.empty((B, M, k), dtype=torch.float32, device=dev)
+        fused = _fusable_source(source_points, dev, (B, int(num_leaves))) and accel is not None
+        positions = None
+        if fused:
+            C = int(source_points.size(-1))
+            positions = torch.empty((B, M, k, C), dtype=torch.float32, device=dev)
         if M == 0:
-            return indices, distances
+            return _with_positions(indices, distances, positions, source_points)
         L = load()
         with torch.cuda.device(dev):
-            if accel is not None:
+            if fused:
+                _require(accel.is_cuda and accel.device == dev, op, "accel must be on the queries' device")
+                _check(L.tbvh_knn_accel_positions(
+                    _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
+                    int(dim), int(k), _ptr(source_points), C, _ptr(indices), _ptr(distances),
+                    _ptr(positions), _stream(dev)))
+            elif accel is not None:
                 _require(accel.is_cuda and accel.device == dev, op, "accel must be on the queries' device")
                 fn = L.tbvh_knn_accel_spatial if spatial else L.tbvh_knn_accel
                 _check(fn(
@@ -604,24 +652,32 @@ class _NativeOps:
                     _ptr(node_aabbs), _ptr(sorted_indices), _ptr(query_points), _ptr(query_order),
                     B, M, int(num_leaves), int(num_real_nodes), int(dim), int(k),
                     _ptr(indices), _ptr(distances), _stream(dev)))
-        return indices, distances
+        return _with_positions(indices, distances, positions, source_points)
 
     @classmethod
     def query_knn_batched_cached_bounds(cls, node_aabbs, sorted_indices, query_points,
-                                        num_leaves, num_real_nodes, dim, k, *, accel=None):
+                                        num_leaves, num_real_nodes, dim, k, *, accel=None,
+                                        source_points=None):
         """Unordered traversal.  `accel`: an accel tensor (identical results,
         fewer node visits), None for the one the batched build registered
-        with these tensors (if any), False for the implicit tree."""
+        with these tensors (if any), False for the implicit tree.  With
+        `source_points` ([B, num_leaves, C]) also returns the neighbours'
+        rows [B, M, k, C] (source_points[b, indices[b, m, j]]), gathered in
+        the traversal's epilogue when it runs on an accel and the source is
+        contiguous float32, else with a torch gather afterwards."""
         return cls._knn("query_knn_batched_cached_bounds", node_aabbs, sorted_indices,
-                        query_points, None, num_leaves, num_real_nodes, dim, k, accel)
+                        query_points, None, num_leaves, num_real_nodes, dim, k, accel,
+                        source_points=source_points)
 
     @classmethod
     def query_knn_batched_cached_bounds_ordered(cls, node_aabbs, sorted_indices, query_points,
                                                 query_order, num_leaves, num_real_nodes, dim, k,
-                                                *, accel=None):
-        """Morton-ordered traversal; `accel` as for the unordered one."""
+                                                *, accel=None, source_points=None):
+        """Morton-ordered traversal; `accel` and `source_points` as for the
+        unordered one."""
         return cls._knn("query_knn_batched_cached_bounds_ordered", node_aabbs, sorted_indices,
-                        query_points, query_order, num_leaves, num_real_nodes, dim, k, accel)
+                        query_points, query_order, num_leaves, num_real_nodes, dim, k, accel,
+                        source_points=source_points)
 
     @classmethod
     def query_knn_batched_cached_bounds_spatial(cls, node_aabbs, sorted_indices, query_points,
@@ -725,7 +781,7 @@ class _NativeOps:
     @staticmethod
     def query_knn_ragged(node_aabbs, sorted_indices, point_offsets, node_offsets, query_points,
                          query_offsets, query_order, batch_size, dim, k, *, accel=None,
-                         total_points=None):
+                         total_points=None, source_points=None):
         op = "query_knn_ragged"
         if accel is False:  # the implicit trees, as for the batched bindings
             accel = None
@@ -739,11 +795,26 @@ class _NativeOps:
         dev = query_points.device
         indices = torch.empty((T, k), dtype=torch.int64, device=dev)
         distances = torch.empty((T, k), dtype=torch.float32, device=dev)
+        # Neighbour rows (packed like the points; indices are cloud-local):
+        # fused in the traversal with an accel, else gathered by the caller.
+        fused = (accel is not None and total_points is not None
+                 and _fusable_source(source_points, dev, (int(total_points),)))
+        positions = None
+        if fused:
+            C = int(source_points.size(-1))
+            positions = torch.empty((T, k, C), dtype=torch.float32, device=dev)
         if T == 0:
-            return indices, distances
+            if source_points is None:
+                return indices, distances
+            return indices, distances, source_points.new_empty((0, k) + tuple(source_points.shape[1:]))
         L = load()
         with torch.cuda.device(dev):
-            if accel is not None:
+            if fused:
+                _check(L.tbvh_knn_accel_ragged_positions(
+                    _ptr(accel), _ptr(point_offsets), int(total_points), _ptr(query_points),
+                    _ptr(query_offsets), _ptr(query_order), int(batch_size), T, int(dim), int(k),
+                    _ptr(source_points), C, _ptr(indices), _ptr(distances), _ptr(positions), _stream(dev)))
+            elif accel is not None:
                 _check(L.tbvh_knn_accel_ragged(
                     _ptr(accel), _ptr(point_offsets), int(total_points), _ptr(query_points),
                     _ptr(query_offsets), _ptr(query_order), int(batch_size), T, int(dim), int(k),
@@ -753,7 +824,13 @@ class _NativeOps:
                     _ptr(node_aabbs), _ptr(sorted_indices), _ptr(point_offsets), _ptr(node_offsets),
                     _ptr(query_points), _ptr(query_offsets), _ptr(query_order), int(batch_size), T,
                     int(dim), int(k), _ptr(indices), _ptr(distances), _stream(dev)))
-        return indices, distances
+        if source_points is None:
+            return indices, distances
+        if positions is None:  # not fused: rows of each query's cloud, indices cloud-local
+            counts = query_offsets[1:] - query_offsets[:-1]
+            starts = point_offsets[:-1].repeat_interleave(counts, output_size=T)
+            positions = source_points[indices + starts[:, None]]
+        return indices, distances, positions
 
 
 _C = _NativeOps()

@@ -184,25 +184,24 @@ def _query_knn_single(
     node_aabbs = data["node_aabbs"].unsqueeze(0)
     sorted_indices = data["sorted_indices"].unsqueeze(0)
     accel = bvh._aux.get("accel")
+    src = None
+    if source_points is not None:
+        _validate_single_source_points("query_knn", data, source_points)
+        src = _as_contiguous(source_points).unsqueeze(0)
     if _schedule(sort_queries, int(queries.size(1))):
         order = _C.morton_sort_queries_narrow(
             queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0), schedule=True
         )
-        indices, distances = _C.query_knn_batched_cached_bounds_ordered(
+        out = _C.query_knn_batched_cached_bounds_ordered(
             node_aabbs, sorted_indices, queries, order.contiguous(),
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel, source_points=src,
         )
     else:
-        indices, distances = _C.query_knn_batched_cached_bounds(
+        out = _C.query_knn_batched_cached_bounds(
             node_aabbs, sorted_indices, queries,
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel, source_points=src,
         )
-    indices = indices.squeeze(0)
-    distances = distances.squeeze(0)
-    if source_points is None:
-        return indices, distances
-    _validate_single_source_points("query_knn", data, source_points)
-    return indices, distances, _as_contiguous(source_points)[indices]
+    return tuple(t.squeeze(0) for t in out)
 
 
 def _validate_single_source_points(prefix: str, data: Mapping, source_points: torch.Tensor) -> None:
@@ -231,13 +230,6 @@ def _validate_batched_source_points(prefix: str, data: Mapping, source_points: t
         raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
 
 
-def _gather_batched_neighbor_positions(source_points, indices) -> torch.Tensor:
-    B, M, K = indices.shape
-    D = source_points.size(2)
-    flat = indices.reshape(B, M * K, 1).expand(-1, -1, D)
-    return torch.gather(source_points, 1, flat).reshape(B, M, K, D)
-
-
 def _query_knn_batched(
     bvh: BatchedBVHHandle,
     query_points: torch.Tensor,
@@ -259,23 +251,21 @@ def _query_knn_batched(
         raise ValueError("query_knn: query_points must be on the same device as the BVH")
     queries = _as_contiguous(query_points)
     accel = bvh._aux.get("accel")
+    src = None
+    if source_points is not None:
+        _validate_batched_source_points("query_knn", data, source_points)
+        src = _as_contiguous(source_points)
     if _schedule(sort_queries, int(queries.size(0) * queries.size(1))):
         order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"],
                                               schedule=True)
-        indices, distances = _C.query_knn_batched_cached_bounds_ordered(
+        return _C.query_knn_batched_cached_bounds_ordered(
             data["node_aabbs"], data["sorted_indices"], queries, order.contiguous(),
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
+            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel, source_points=src,
         )
-    else:
-        indices, distances = _C.query_knn_batched_cached_bounds(
-            data["node_aabbs"], data["sorted_indices"], queries,
-            data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel,
-        )
-    if source_points is None:
-        return indices, distances
-    _validate_batched_source_points("query_knn", data, source_points)
-    positions = _gather_batched_neighbor_positions(_as_contiguous(source_points), indices)
-    return indices, distances, positions
+    return _C.query_knn_batched_cached_bounds(
+        data["node_aabbs"], data["sorted_indices"], queries,
+        data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel, source_points=src,
+    )
 
 
 def _validate_ragged_source_points(prefix, data, source_points, *, total_rows, device) -> None:
@@ -330,19 +320,12 @@ def _query_knn_ragged(
             queries, query_offsets, packed["scene_min"], packed["scene_max"], data["batch_size"],
             schedule=True,
         )
-    indices, distances = _C.query_knn_ragged(
+    return _C.query_knn_ragged(
         packed["node_aabbs"], packed["sorted_indices"], data["batch_offsets"],
         packed["node_offsets"], queries, query_offsets, order, data["batch_size"],
         data["dim"], k, accel=bvh._aux.get("accel"), total_points=p_offsets[-1],
+        source_points=source_points,
     )
-    if source_points is None:
-        return indices, distances
-    counts = torch.tensor(
-        [b - a for a, b in zip(q_offsets, q_offsets[1:])], device=queries.device
-    )
-    starts = data["batch_offsets"][:-1].repeat_interleave(counts)
-    positions = source_points[indices + starts[:, None]]
-    return indices, distances, positions
 
 
 def query_knn(

@@ -823,7 +823,8 @@ int tbvh_accel_build_ragged(const float* points, const int64_t* offsets, const i
 static int knn_accel_batched(const char* op, const void* accel, const float* queries,
                              const int64_t* order, int64_t B, int64_t M, int64_t num_leaves, int D,
                              int k, bool spatial, int64_t* out_indices, float* out_distances,
-                             void* stream_ptr) {
+                             void* stream_ptr, const float* source_points = nullptr, int source_cols = 0,
+                             float* out_positions = nullptr) {
     if (int r = check_dim(op, D)) return r;
     if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
@@ -849,6 +850,9 @@ static int knn_accel_batched(const char* op, const void* accel, const float* que
     a.accel = accel;
     a.total_points = B * num_leaves;
     a.spatial_output = spatial;
+    a.source_points = source_points;
+    a.source_cols = source_cols;
+    a.out_positions = out_positions;
     TBVH_TRY(op, launch_knn_accel(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
     return ok();
 }
@@ -867,11 +871,11 @@ int tbvh_knn_accel_spatial(const void* accel, const float* queries, const int64_
                              true, out_indices, out_distances, stream_ptr);
 }
 
-int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets, int64_t total_points,
-                          const float* queries, const int64_t* query_offsets, const int64_t* order,
-                          int64_t B, int64_t total_q, int D, int k, int64_t* out_indices,
-                          float* out_distances, void* stream_ptr) {
-    const char* op = "tbvh_knn_accel_ragged";
+static int knn_accel_ragged(const char* op, const void* accel, const int64_t* point_offsets,
+                            int64_t total_points, const float* queries, const int64_t* query_offsets,
+                            const int64_t* order, int64_t B, int64_t total_q, int D, int k,
+                            int64_t* out_indices, float* out_distances, void* stream_ptr,
+                            const float* source_points, int source_cols, float* out_positions) {
     if (int r = check_dim(op, D)) return r;
     if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
     if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
@@ -893,8 +897,50 @@ int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets, int64
     a.out_distances = out_distances;
     a.accel = accel;
     a.total_points = total_points;
+    a.source_points = source_points;
+    a.source_cols = source_cols;
+    a.out_positions = out_positions;
     TBVH_TRY(op, launch_knn_accel(a, D, k, true, static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets, int64_t total_points,
+                          const float* queries, const int64_t* query_offsets, const int64_t* order,
+                          int64_t B, int64_t total_q, int D, int k, int64_t* out_indices,
+                          float* out_distances, void* stream_ptr) {
+    return knn_accel_ragged("tbvh_knn_accel_ragged", accel, point_offsets, total_points, queries,
+                            query_offsets, order, B, total_q, D, k, out_indices, out_distances, stream_ptr,
+                            nullptr, 0, nullptr);
+}
+
+static int check_positions(const char* op, const float* source_points, int source_cols, float* out_positions) {
+    if (!source_points || !out_positions) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null source or positions pointer", op);
+    if (source_cols < 1 || source_cols > 4096) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: source_cols must be in [1, 4096], got %d", op, source_cols);
+    }
+    return 0;
+}
+
+int tbvh_knn_accel_positions(const void* accel, const float* queries, const int64_t* order, int64_t B,
+                             int64_t M, int64_t num_leaves, int D, int k, const float* source_points,
+                             int source_cols, int64_t* out_indices, float* out_distances,
+                             float* out_positions, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_positions";
+    if (int r = check_positions(op, source_points, source_cols, out_positions)) return r;
+    return knn_accel_batched(op, accel, queries, order, B, M, num_leaves, D, k, false, out_indices,
+                             out_distances, stream_ptr, source_points, source_cols, out_positions);
+}
+
+int tbvh_knn_accel_ragged_positions(const void* accel, const int64_t* point_offsets, int64_t total_points,
+                                    const float* queries, const int64_t* query_offsets, const int64_t* order,
+                                    int64_t B, int64_t total_q, int D, int k, const float* source_points,
+                                    int source_cols, int64_t* out_indices, float* out_distances,
+                                    float* out_positions, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_ragged_positions";
+    if (int r = check_positions(op, source_points, source_cols, out_positions)) return r;
+    return knn_accel_ragged(op, accel, point_offsets, total_points, queries, query_offsets, order, B, total_q,
+                            D, k, out_indices, out_distances, stream_ptr, source_points, source_cols,
+                            out_positions);
 }
 
 // ---------------------------------------------------------------------------

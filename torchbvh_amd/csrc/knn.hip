@@ -78,6 +78,58 @@ __device__ __forceinline__ void insert_sorted(uint64_t (&best)[K], uint64_t key)
     best[0] = key_min(best[0], key);
 }
 
+// Writes one result row: the K (index, distance) pairs and, when asked,
+// the neighbours' source rows.  `pstart` is the cloud's first point row,
+// `index_offset` what the routed traversal adds to false-route indices.
+template <int C>
+struct SourceRow {
+    float v[C];
+};
+
+template <int K, int D = 0>
+__device__ __forceinline__ void write_results(const KnnArgs& a, int64_t out_row, const uint64_t (&best)[K],
+                                              int64_t index_offset, int64_t pstart) {
+    int64_t* oi = a.out_indices + out_row * K;
+    float* od = a.out_distances + out_row * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+        oi[i] = idx >= 0 ? idx + index_offset : idx;
+        od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
+    }
+    if constexpr (D > 0 && (K * D) % 4 == 0) {
+        if (a.out_positions != nullptr && a.source_cols == D) {
+            // Rows of D floats: one load per neighbour, the result row
+            // (K * D floats, 16-byte aligned) stored as float4s.
+            float row[K * D];
+            const SourceRow<D>* src = reinterpret_cast<const SourceRow<D>*>(a.source_points) + pstart;
+#pragma unroll
+            for (int i = 0; i < K; ++i) {
+                const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+                const SourceRow<D> r = src[idx >= 0 ? idx : 0];
+#pragma unroll
+                for (int c = 0; c < D; ++c) row[i * D + c] = idx >= 0 ? r.v[c] : 0.0f;
+            }
+            float4* op = reinterpret_cast<float4*>(a.out_positions + out_row * K * D);
+#pragma unroll
+            for (int v = 0; v < K * D / 4; ++v) {
+                op[v] = make_float4(row[4 * v], row[4 * v + 1], row[4 * v + 2], row[4 * v + 3]);
+            }
+            return;
+        }
+    }
+    if (a.out_positions != nullptr) {
+        const int C = a.source_cols;
+        float* op = a.out_positions + out_row * K * C;
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+            const float* src = a.source_points + (pstart + (idx >= 0 ? idx : 0)) * C;
+            for (int c = 0; c < C; ++c) op[i * C + c] = idx >= 0 ? src[c] : 0.0f;
+        }
+    }
+}
+
 template <int D, int K, bool kOrdered, bool kRagged>
 __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -177,14 +229,7 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
 
     // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
     const int64_t out_row = a.spatial_output ? qbase + local : row;
-    int64_t* oi = a.out_indices + out_row * K;
-    float* od = a.out_distances + out_row * K;
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-        const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
-        oi[i] = idx >= 0 ? idx + index_offset : idx;
-        od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
-    }
+    write_results<K, D>(a, out_row, best, index_offset, pstart);
 }
 
 // Exact distance to a point stored as float4.  On a leaf's degenerate box
@@ -423,14 +468,7 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
 
     // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
     const int64_t out_row = a.spatial_output ? qbase + local : row;
-    int64_t* oi = a.out_indices + out_row * K;
-    float* od = a.out_distances + out_row * K;
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-        const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
-        oi[i] = idx >= 0 ? idx + index_offset : idx;
-        od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
-    }
+    write_results<K, D>(a, out_row, best, index_offset, pstart);
 }
 
 template <int D, int K>

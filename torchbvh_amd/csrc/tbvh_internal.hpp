@@ -264,6 +264,13 @@ struct KnnArgs {
     const void* accel;             // accelerated traversal only
     int64_t total_points;          // accelerated traversal only
     bool spatial_output;           // write row `launch position` instead of `query index`
+    // Fused neighbour rows: with out_positions set, row j of a result also
+    // gets the source_points row of neighbour j (source_cols floats; the
+    // source has the points' layout, so a cloud's rows start where its
+    // points do).  Not with routes.
+    const float* source_points;
+    int32_t source_cols;
+    float* out_positions;
     // Routed traversal (batched only): a query whose route is false searches
     // the second structure and its indices are offset by num_leaves.
     const uint8_t* routes;         // null: not routed
