@@ -202,3 +202,25 @@ def test_primitive_build_and_point_sort_argument_errors():
     assert size.value > point_size.value
     assert L.tbvh_morton_sort_points(FAKE, 2, 1000, 3, None, FAKE, size.value, None) == 1
     assert L.tbvh_morton_sort_points(FAKE, 2, 1000, 3, FAKE, FAKE, size.value - 1, None) == 2
+
+
+def test_knn_positions_argument_errors():
+    """The fused-row entry points check their source and positions pointers
+    and the row width before the traversal's own checks."""
+    L = _native.load()
+    NUL = None
+    args = lambda src, cols, pos: (FAKE, FAKE, FAKE, 1, 10, 100, 3, 16, src, cols, FAKE, FAKE, pos, None)  # noqa: E731
+    assert L.tbvh_knn_accel_positions(*args(NUL, 3, FAKE)) == 1
+    assert "null source or positions" in _err(L)
+    assert L.tbvh_knn_accel_positions(*args(FAKE, 3, NUL)) == 1
+    assert "null source or positions" in _err(L)
+    for cols in (0, -1, 4097):
+        assert L.tbvh_knn_accel_positions(*args(FAKE, cols, FAKE)) == 1
+        assert "source_cols must be in [1, 4096]" in _err(L)
+    # Then the traversal's own checks apply (k here).
+    bad_k = (FAKE, FAKE, FAKE, 1, 10, 100, 3, 5, FAKE, 3, FAKE, FAKE, FAKE, None)
+    assert L.tbvh_knn_accel_positions(*bad_k) == 1
+    assert "k must be 4, 8, 16, or 32" in _err(L)
+    ragged = (FAKE, FAKE, 100, FAKE, FAKE, FAKE, 2, 10, 3, 16, NUL, 3, FAKE, FAKE, FAKE, None)
+    assert L.tbvh_knn_accel_ragged_positions(*ragged) == 1
+    assert "tbvh_knn_accel_ragged_positions" in _err(L) and "null source" in _err(L)
