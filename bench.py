@@ -307,6 +307,20 @@ def extras() -> int:
          "cfg2, k=16 (query_knn with source_points minus without)", with_rows - plain,
          Q * K * (2 * 4 * D), "QK(2*4D): neighbour row read, row written")
 
+    Bm, Nm, Hm, Km = 4, 65_536, 4, 8
+    pos = torch.rand((Bm, Nm, D), generator=g).to(dev)
+    qd = (pos[:, :, None, :] + (torch.rand((Bm, Nm, Hm, D), generator=g).to(dev) - 0.5) * 0.02).contiguous()
+    vals = torch.rand((Bm, Nm, Hm, 16), generator=g).to(dev)
+    Qm = Bm * Nm * Hm
+    line("(f)3 multi-head displaced-query k-NN (query_displaced_knn: build + k-NN + neighbour rows)",
+         "4 clouds x 65,536 3-D points, 4 heads, k=8", timed(lambda: tb.query_displaced_knn(pos, qd, Km)),
+         build_bytes(Nm, D) * Bm + qsort_bytes(Qm, D) + knn_bytes(Qm, D, Km) + Qm * Km * 2 * 4 * D,
+         "B(build) + Q(4D+72) + Q(4D+4+12K) + QK(2*4D), Q = B*N*H")
+    line("(f)3 multi-head interpolation (interpolate_displaced, 16 channels)",
+         "4 clouds x 65,536 3-D points, 4 heads, k=8", timed(lambda: tb.interpolate_displaced(pos, qd, vals, Km)),
+         build_bytes(Nm, D) * Bm + qsort_bytes(Qm, D) + knn_bytes(Qm, D, Km) + Qm * Km * 16 * 4 + Qm * 16 * 4,
+         "as above without rows + QK*4C gathered values + Q*4C written, C = 16")
+
     F, V = 1 << 20, 3
     anchor = torch.rand((1, F, 1, D), generator=g)
     prims = (anchor + (torch.rand((1, F, V, D), generator=g) - 0.5) * 0.01).contiguous().to(dev)

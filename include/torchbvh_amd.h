@@ -336,6 +336,20 @@ int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_acce
                                   int D, int k,
                                   int64_t* out_indices, float* out_distances, void* stream);
 
+/* ---- displaced-query interpolation --------------------------------------------------
+ * Replaces the neighbour gather and rank loop of `interpolate_displaced`
+ * (torchbvh/_multihead.py:123-144): values (B, N, H, C), indices, weights
+ * and exact (B, N, H, k; indices local to the cloud, weights already
+ * normalised, exact non-zero where the neighbour is an exact hit), out
+ * (B, N, H, C).  out[b, n, h, c] = sum over ranks j in order of
+ * values[b, indices[.., j], h, c] * weights[.., j], or, where any exact[.., j]
+ * is set, the sum of those neighbours' values divided by their count; each
+ * step rounds the product and the sum separately, as the reference's tensor
+ * operations do.  An index outside [0, N) contributes zero. */
+int tbvh_interpolate_neighbors(const float* values, const int64_t* indices, const float* weights,
+                               const uint8_t* exact, int64_t B, int64_t N, int64_t H, int64_t C, int k,
+                               float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -224,3 +224,18 @@ def test_knn_positions_argument_errors():
     ragged = (FAKE, FAKE, 100, FAKE, FAKE, FAKE, 2, 10, 3, 16, NUL, 3, FAKE, FAKE, FAKE, None)
     assert L.tbvh_knn_accel_ragged_positions(*ragged) == 1
     assert "tbvh_knn_accel_ragged_positions" in _err(L) and "null source" in _err(L)
+
+
+def test_interpolate_neighbors_argument_errors():
+    """Shape and pointer checks of the interpolation entry point come before
+    any launch; an empty cloud set is a no-op."""
+    L = _native.load()
+    args = lambda B, N, H, C, k, v=FAKE: (v, FAKE, FAKE, FAKE, B, N, H, C, k, FAKE, None)  # noqa: E731
+    for bad in ((-1, 4, 2, 3, 8), (1, -1, 2, 3, 8), (1, 4, 0, 3, 8), (1, 4, 2, 0, 8), (1, 4, 2, 3, 0)):
+        assert L.tbvh_interpolate_neighbors(*args(*bad)) == 1
+        assert "need B >= 0, N >= 0, H >= 1, C >= 1 and k >= 1" in _err(L)
+    assert L.tbvh_interpolate_neighbors(*args(1, 4, 2, 3, 8, None)) == 1
+    assert "null input or output" in _err(L)
+    assert L.tbvh_interpolate_neighbors(*args(1, 1 << 20, 1 << 10, 1 << 12, 8)) == 1
+    assert "exceeds 2^40" in _err(L)
+    assert L.tbvh_interpolate_neighbors(*args(0, 4, 2, 3, 8, None)) == 0

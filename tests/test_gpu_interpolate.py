@@ -1,0 +1,120 @@
+"""The fused interpolation kernel of interpolate_displaced: bit-identical to
+the reference's tensor formula (torchbvh/_multihead.py:123-144, 186-190), evaluated
+here with torch on the same k-NN result, for vector and scalar channel
+layouts, exact hits of several multiplicities, and the autograd path."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import torchbvh_amd as tb
+from torchbvh_amd._native import _C
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def inputs(B, N, H, D, C, seed, dup=0):
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand((B, N, D), generator=g)
+    if dup:  # points repeated dup times: exact hits of that multiplicity
+        pos[:, : N // 2] = pos[:, : N // (2 * dup)].repeat_interleave(dup, dim=1)[:, : N // 2]
+    q = pos[:, :, None, :] + 0.02 * torch.randn((B, N, H, D), generator=g)
+    q[:, ::3, 0] = pos[:, ::3]  # every third point's head 0 sits on it
+    values = torch.randn((B, N, H, C), generator=g)
+    return pos.to(DEV), q.to(DEV).contiguous(), values.to(DEV)
+
+
+def tensor_formula(values, idx, d2):
+    """The reference's sequence of tensor operations, one rank at a time."""
+    B, N, H, C = values.shape
+    k = idx.size(-1)
+    b = torch.arange(B, device=DEV).view(B, 1, 1, 1)
+    h = torch.arange(H, device=DEV).view(1, 1, H, 1)
+    nv = values[b, idx, h]
+    exact = d2 <= 1e-12
+    w = torch.reciprocal(d2 + 1e-12)
+    w = w / w.sum(-1, keepdim=True).clamp(min=1e-12)
+    want = torch.zeros_like(values)
+    ex = torch.zeros_like(values)
+    for r in range(k):
+        want = want + nv[..., r, :] * w[..., r].unsqueeze(-1)
+        ex = ex + nv[..., r, :] * exact[..., r].float().unsqueeze(-1)
+    ex = ex / exact.float().sum(-1, keepdim=True).clamp(min=1.0)
+    return torch.where(exact.any(-1, keepdim=True), ex, want), exact
+
+
+@pytest.mark.parametrize("C", [1, 3, 4, 16, 33, 64])
+@pytest.mark.parametrize("k,dim", [(4, 2), (8, 3), (16, 3), (32, 2)])
+def test_fused_matches_tensor_formula(C, k, dim):
+    pos, q, values = inputs(2, 257, 3, dim, C, seed=100 * C + k)
+    out = tb.interpolate_displaced(pos, q, values, k)
+    idx, d2 = tb.query_displaced_knn(pos, q, k, return_positions=False)
+    want, exact = tensor_formula(values, idx, d2)
+    assert exact.any()
+    assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("dup", [2, 3, 5])
+def test_exact_hits_of_several_points_average(dup):
+    pos, q, values = inputs(2, 300, 2, 3, 8, seed=31 + dup, dup=dup)
+    out = tb.interpolate_displaced(pos, q, values, 8)
+    idx, d2 = tb.query_displaced_knn(pos, q, 8, return_positions=False)
+    want, exact = tensor_formula(values, idx, d2)
+    assert (exact.sum(-1) >= dup).any()
+    assert torch.equal(out, want)
+
+
+def test_gradient_path_agrees_and_differentiates():
+    pos, q, values = inputs(1, 200, 2, 3, 6, seed=5)
+    fused = tb.interpolate_displaced(pos, q, values, 8)
+    v = values.clone().requires_grad_(True)
+    traced = tb.interpolate_displaced(pos, q, v, 8)
+    assert traced.requires_grad
+    assert torch.equal(traced.detach(), fused)
+    traced.sum().backward()
+    assert v.grad is not None and torch.isfinite(v.grad).all()
+    with torch.no_grad():
+        assert torch.equal(tb.interpolate_displaced(pos, q, v, 8), fused)
+
+
+def test_misaligned_values_take_the_scalar_layout():
+    """C % 4 == 0 but values start 4 bytes past a 16-byte boundary."""
+    pos, q, values = inputs(1, 128, 2, 2, 8, seed=9)
+    store = torch.empty(values.numel() + 1, device=DEV)
+    shifted = store[1:].view(values.shape)
+    shifted.copy_(values)
+    assert shifted.data_ptr() % 16 != 0
+    idx, d2 = tb.query_displaced_knn(pos, q, 4, return_positions=False)
+    assert torch.equal(tb.interpolate_displaced(pos, q, shifted, 4), tensor_formula(values, idx, d2)[0])
+
+
+def test_binding_out_of_range_indices_contribute_zero():
+    g = torch.Generator().manual_seed(3)
+    B, N, H, C, k = 2, 10, 2, 5, 4
+    values = torch.randn((B, N, H, C), generator=g).to(DEV)
+    idx = torch.randint(-3, N + 3, (B, N, H, k), generator=g).to(DEV)
+    w = torch.rand((B, N, H, k), generator=g).to(DEV)
+    exact = torch.zeros((B, N, H, k), dtype=torch.bool, device=DEV)
+    out = _C.interpolate_neighbors(values, idx, w, exact)
+    valid = (idx >= 0) & (idx < N)
+    b = torch.arange(B, device=DEV).view(B, 1, 1, 1)
+    h = torch.arange(H, device=DEV).view(1, 1, H, 1)
+    nv = values[b, idx.clamp(0, N - 1), h] * valid.unsqueeze(-1)
+    want = torch.zeros_like(values)
+    for r in range(k):
+        want = want + nv[..., r, :] * w[..., r].unsqueeze(-1)
+    assert torch.equal(out, want)
+
+
+def test_binding_empty_and_shape_errors():
+    values = torch.zeros((0, 4, 2, 3), device=DEV)
+    idx = torch.zeros((0, 4, 2, 8), dtype=torch.int64, device=DEV)
+    w = torch.zeros((0, 4, 2, 8), device=DEV)
+    ex = torch.zeros((0, 4, 2, 8), dtype=torch.bool, device=DEV)
+    assert _C.interpolate_neighbors(values, idx, w, ex).shape == (0, 4, 2, 3)
+    with pytest.raises(RuntimeError, match="weights must have shape"):
+        _C.interpolate_neighbors(values, idx, w[..., :4], ex)
+    with pytest.raises(RuntimeError, match="exact must be a contiguous bool"):
+        _C.interpolate_neighbors(values, idx, w, ex.to(torch.uint8))

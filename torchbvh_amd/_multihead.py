@@ -14,6 +14,7 @@ import torch
 
 from ._constants import EXACT_DISTANCE_EPSILON, SUPPORTED_DIMS
 from ._handles import _temporary_bvh
+from ._native import _C
 from ._query import _build_bvh_batched, _query_knn_batched
 from ._validation import _as_contiguous, _as_contiguous_int64, _validate_cuda_float32
 
@@ -122,9 +123,13 @@ def interpolate_displaced(pos: torch.Tensor, q: torch.Tensor, values: torch.Tens
     exact = d2 <= eps
     weights = torch.reciprocal(d2 + eps)
     weights = weights / weights.sum(dim=-1, keepdim=True).clamp(min=eps)
+    if not (values.requires_grad and torch.is_grad_enabled()):
+        # One kernel: the same rank-by-rank sums and exact-hit select, with
+        # no gathered copy and no host synchronisation.
+        return _C.interpolate_neighbors(values, indices, weights, exact)
     neighbours = gather_neighbor_values(values, indices)  # (B, N, H, k, Ch)
     # Accumulated neighbour rank by neighbour rank, the reference's order of
-    # fp32 additions (_multihead.py:126-147).
+    # fp32 additions (_multihead.py:123-144).
     weighted = torch.zeros_like(values)
     exact_sum = torch.zeros_like(values)
     for r in range(indices.size(-1)):

@@ -102,6 +102,7 @@ def _declare(L) -> None:
     L.tbvh_knn_accel_ragged_positions.argtypes = (
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp]
     )
+    L.tbvh_interpolate_neighbors.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp]
     for name in (
         "tbvh_build_workspace_size", "tbvh_build", "tbvh_build_ragged_workspace_size",
         "tbvh_build_ragged", "tbvh_build_with_accel", "tbvh_build_ragged_with_accel",
@@ -116,6 +117,7 @@ def _declare(L) -> None:
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
         "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
         "tbvh_morton_sort_points_workspace_size", "tbvh_morton_sort_points",
+        "tbvh_interpolate_neighbors",
     ):
         getattr(L, name).restype = _int
 
@@ -831,6 +833,31 @@ class _NativeOps:
             starts = point_offsets[:-1].repeat_interleave(counts, output_size=T)
             positions = source_points[indices + starts[:, None]]
         return indices, distances, positions
+
+    @staticmethod
+    def interpolate_neighbors(values, indices, weights, exact):
+        """Rank loop and exact-hit select of `interpolate_displaced`
+        (_multihead.py:123-144) in one kernel: values (B, N, H, C);
+        indices, weights, exact (B, N, H, k).  Returns (B, N, H, C)."""
+        op = "interpolate_neighbors"
+        _require_device_f32(op, values, "values")
+        _require_device_i64(op, indices, "indices")
+        _require_device_f32(op, weights, "weights")
+        _require(exact.dtype == torch.bool and exact.is_contiguous(), op, "exact must be a contiguous bool tensor")
+        B, N, H, C = (int(x) for x in values.shape)
+        k = int(indices.size(-1))
+        for name, t in (("indices", indices), ("weights", weights), ("exact", exact)):
+            _require(tuple(t.shape) == (B, N, H, k) and t.device == values.device, op,
+                     f"{name} must have shape (B, N, H, k) on the values' device")
+        out = torch.empty_like(values)
+        if out.numel() == 0:
+            return out
+        dev = values.device
+        with torch.cuda.device(dev):
+            _check(load().tbvh_interpolate_neighbors(
+                _ptr(values), _ptr(indices), _ptr(weights), _ptr(exact), B, N, H, C, k, _ptr(out),
+                _stream(dev)))
+        return out
 
 
 _C = _NativeOps()

@@ -1030,4 +1030,24 @@ int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_acce
     return ok();
 }
 
+int tbvh_interpolate_neighbors(const float* values, const int64_t* indices, const float* weights,
+                               const uint8_t* exact, int64_t B, int64_t N, int64_t H, int64_t C, int k,
+                               float* out, void* stream_ptr) {
+    const char* op = "tbvh_interpolate_neighbors";
+    if (B < 0 || N < 0 || H < 1 || C < 1 || k < 1) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 0, N >= 0, H >= 1, C >= 1 and k >= 1", op);
+    }
+    const int64_t rows = B * N * H;
+    if (rows == 0) return ok();
+    if (rows > (int64_t{1} << 40) / C) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: B * N * H * C exceeds 2^40", op);
+    }
+    if (!values || !indices || !weights || !exact || !out) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    TBVH_TRY(op, launch_interpolate(values, indices, weights, exact, rows, N, H, C, k, out,
+                                    static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
 }  // extern "C"

@@ -245,6 +245,12 @@ hipError_t launch_route_gather(const float* queries, const int64_t* part, const 
 hipError_t launch_route_finish(const int64_t* part, const int64_t* sorted_local, const int64_t* group_offsets,
                                int64_t B, int64_t M, int64_t* order, hipStream_t stream);
 
+// interpolate_displaced's rank loop and exact-hit select, one thread per
+// (query row, channel group); writes the (rows, C) result.
+hipError_t launch_interpolate(const float* values, const int64_t* indices, const float* weights,
+                              const uint8_t* exact, int64_t rows, int64_t N, int64_t H, int64_t C, int K,
+                              float* out, hipStream_t stream);
+
 // k-NN traversal.
 struct KnnArgs {
     const float* node_aabbs;
