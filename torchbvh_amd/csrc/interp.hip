@@ -16,6 +16,8 @@
 namespace tbvh {
 namespace {
 
+constexpr int64_t kMaxGrid = int64_t{1} << 20;  // work-groups per launch
+
 template <int V>
 struct Vec;
 template <>
@@ -37,16 +39,12 @@ __device__ __forceinline__ float lane(const typename Vec<V>::T& v, int i) {
 }
 
 template <int V>
-__global__ __launch_bounds__(kBlock) void interpolate_kernel(const float* __restrict__ values,
-                                                             const int64_t* __restrict__ indices,
-                                                             const float* __restrict__ weights,
-                                                             const uint8_t* __restrict__ exact, int64_t rows,
-                                                             int64_t N, int64_t H, int64_t C, int K,
-                                                             float* __restrict__ out) {
+__device__ __forceinline__ void interpolate_item(const float* __restrict__ values,
+                                                 const int64_t* __restrict__ indices,
+                                                 const float* __restrict__ weights,
+                                                 const uint8_t* __restrict__ exact, int64_t t, int64_t groups,
+                                                 int64_t N, int64_t H, int64_t C, int K, float* __restrict__ out) {
     using T = typename Vec<V>::T;
-    const int64_t groups = C / V;  // V-channel groups per row
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (t >= rows * groups) return;
     const int64_t r = t / groups;              // query row (b, n, h)
     const int64_t c = (t - r * groups) * V;    // first channel
     const int64_t h = r % H;
@@ -76,6 +74,23 @@ __global__ __launch_bounds__(kBlock) void interpolate_kernel(const float* __rest
     *reinterpret_cast<T*>(out + r * C + c) = res;
 }
 
+// Grid-stride over (row, channel group) items: the grid is capped, since a
+// launch holds fewer than 2^32 work-items.
+template <int V>
+__global__ __launch_bounds__(kBlock) void interpolate_kernel(const float* __restrict__ values,
+                                                             const int64_t* __restrict__ indices,
+                                                             const float* __restrict__ weights,
+                                                             const uint8_t* __restrict__ exact, int64_t rows,
+                                                             int64_t N, int64_t H, int64_t C, int K,
+                                                             float* __restrict__ out) {
+    const int64_t groups = C / V;  // V-channel groups per row
+    const int64_t items = rows * groups;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; t < items; t += stride) {
+        interpolate_item<V>(values, indices, weights, exact, t, groups, N, H, C, K, out);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_interpolate(const float* values, const int64_t* indices, const float* weights,
@@ -85,7 +100,7 @@ hipError_t launch_interpolate(const float* values, const int64_t* indices, const
                      reinterpret_cast<uintptr_t>(out) % 16 == 0;
     const int64_t items = rows * (vec ? C / 4 : C);
     if (items == 0) return hipSuccess;
-    const unsigned grid = static_cast<unsigned>((items + kBlock - 1) / kBlock);
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>((items + kBlock - 1) / kBlock, kMaxGrid));
     if (vec) {
         interpolate_kernel<4><<<grid, kBlock, 0, stream>>>(values, indices, weights, exact, rows, N, H, C, K, out);
     } else {
