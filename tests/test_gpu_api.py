@@ -388,3 +388,15 @@ def test_interpolate_displaced_weighted_mean_and_exact_hits():
     want = torch.where(exact.any(-1, keepdim=True), ex, want)
     assert torch.equal(out, want)
     assert exact[:, :, 0, 0].all()  # head 0's nearest neighbour is its own point
+
+
+def test_build_rejects_more_than_int32_points_without_copying():
+    """_query.py:30-35: total point count must fit in signed int32; checked
+    on the sizes, so an expanded (stride-0) view is never materialised."""
+    one = torch.zeros((1, 1, 3), device=DEV)
+    before = torch.cuda.memory_allocated(DEV)
+    with pytest.raises(ValueError, match="build_bvh: total point count must fit in signed int32"):
+        tb.build_bvh(one[0].expand(2**31, 3))
+    with pytest.raises(ValueError, match="build_bvh: total point count must fit in signed int32"):
+        tb.build_bvh(one.expand(2, 2**30, 3))
+    assert torch.cuda.memory_allocated(DEV) == before

@@ -51,8 +51,10 @@ def _build_bvh_single(points: torch.Tensor) -> BVHHandle:
     if points.size(1) not in SUPPORTED_DIMS:
         raise ValueError("build_bvh: D must be 2 or 3")
     _validate_cuda_float32("build_bvh", points, "points")
-    points = _as_contiguous(points)
+    # Sizes only, before any copy (an expanded view is rejected without
+    # materialising it).
     _validate_narrow_build_extent("build_bvh", points)
+    points = _as_contiguous(points)
     batched = points.unsqueeze(0)
     data = _C.build_bvh_batched_cooperative(batched, with_accel=True)
     accel = data.pop("accel")
@@ -69,8 +71,10 @@ def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
     if points.size(2) not in SUPPORTED_DIMS:
         raise ValueError("build_bvh: D must be 2 or 3")
     _validate_cuda_float32("build_bvh", points, "points")
-    points = _as_contiguous(points)
+    # Sizes only, before any copy (an expanded view is rejected without
+    # materialising it).
     _validate_narrow_build_extent("build_bvh", points)
+    points = _as_contiguous(points)
     data = _C.build_bvh_batched_cooperative(points, with_accel=True)
     accel = data.pop("accel")
     return BatchedBVHHandle(data, aux={"accel": accel})
