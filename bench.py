@@ -6,7 +6,7 @@ order the queries, run the traversal — the whole hot path, inputs resident in
 HBM.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
-                    [--cpu-sample Q] [--no-cpu-baseline]
+                    [--cpu-seconds S] [--no-cpu-baseline]
     python bench.py --published   # the reference's published latency rows
     python bench.py --extras      # spatial/routed k-NN, gather, primitive build, point order
 
@@ -145,19 +145,57 @@ def measured_traffic(config: str):
 # CPU baseline: the reference's brute-force test oracle (tests/test_knn.py:10-12)
 # with the (distance, index) tie rule, timed on a bounded sample of queries.
 # ---------------------------------------------------------------------------
-def cpu_baseline(points: torch.Tensor, queries: torch.Tensor, k: int, sample: int) -> dict:
-    from oracle.torch_bruteforce import knn_bruteforce
+def job_clouds(w: dict) -> list:
+    """(points, queries) of every cloud of a workload, as CPU numpy arrays."""
+    pts, q = w["points"].numpy(), w["queries"].numpy()
+    if w["kind"] == "batched":
+        return [(pts[b], q[b]) for b in range(pts.shape[0])]
+    if w["kind"] == "ragged":
+        po, qo = w["offsets"].tolist(), w["query_offsets"].tolist()
+        return [(pts[po[b]:po[b + 1]], q[qo[b]:qo[b + 1]]) for b in range(len(po) - 1)]
+    return [(pts, q)]
 
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    g = _gen(99)
-    sel = torch.randperm(queries.shape[0], generator=g)[:sample]
-    qs = queries[sel].contiguous()
-    knn_bruteforce(points, qs[:8], k)  # warm-up
+
+def cpu_baseline(clouds: list, k: int, seconds: float) -> dict:
+    """The whole job on the host with the C oracle, which restates the
+    reference's algorithm (implicit-tree build, DFS k-NN with the sorted
+    candidate list).  Every cloud is built in full (one thread); the k-NN is
+    timed on a uniform sample of the job's queries sized to about `seconds`
+    (OpenMP over queries) and extrapolated to all of them."""
+    import numpy as np
+
+    import oracle
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    oracle.lib().orc_set_num_threads(threads)
     t0 = time.perf_counter()
-    knn_bruteforce(points, qs, k)
-    dt = time.perf_counter() - t0
-    qps = sample / dt
+    bvhs = [oracle.build(p) for p, _ in clouds]
+    t_build = time.perf_counter() - t0
+    starts = np.cumsum([0] + [len(q) for _, q in clouds])
+    Q = int(starts[-1])
+    rng = np.random.default_rng(99)
+
+    def timed(n: int) -> float:
+        sel = np.sort(rng.choice(Q, n, replace=False))
+        parts = np.searchsorted(sel, starts)
+        t = time.perf_counter()
+        for b, (bvh, (_, q)) in enumerate(zip(bvhs, clouds)):
+            local = sel[parts[b]:parts[b + 1]] - starts[b]
+            if len(local):
+                oracle.knn_bvh(bvh, q[local], k)
+        return time.perf_counter() - t
+
+    probe = min(Q, 2048)
+    timed(probe)  # warm-up: thread pool, caches
+    per_query = timed(probe) / probe
+    n, dt = probe, 0.0
+    for _ in range(3):  # per-cloud call costs make small samples read slow: rescale
+        n = int(min(Q, max(n, seconds / per_query)))
+        dt = timed(n)
+        per_query = dt / n
+        if n == Q or dt >= 0.5 * seconds:
+            break
+    total = t_build + Q * per_query
     cpu_model = platform.processor() or "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -168,14 +206,14 @@ def cpu_baseline(points: torch.Tensor, queries: torch.Tensor, k: int, sample: in
     except OSError:
         pass
     return {
-        "value": qps,
+        "value": Q / total,
         "unit": "queries/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{sample} of {queries.shape[0]} queries (seeded) against all "
-                   f"{points.shape[0]} points, torch brute force in chunks; "
-                   f"{dt:.2f} s measured; extrapolated full-query time "
-                   f"{queries.shape[0] / qps:.1f} s; CPU: {cpu_model}"),
+        "sample": (f"C oracle (restated reference build + DFS k-NN, gcc -O2): all {len(clouds)} "
+                   f"cloud(s) built on 1 thread in {t_build:.3g} s; k-NN of {n} of {Q} queries "
+                   f"(uniform sample) on {threads} threads in {dt:.3g} s; extrapolated job "
+                   f"time {total:.3g} s; CPU: {cpu_model}"),
     }
 
 
@@ -339,7 +377,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-sample", type=int, default=3072)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="host time budget of the CPU baseline's sampled k-NN")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--implicit-reps", type=int, default=1,
                     help="also time the traversal over the implicit tree (0 = skip)")
@@ -519,12 +558,7 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        cpu_pts = w["points"] if kind != "batched" else w["points"][0]
-        cpu_q = w["queries"] if kind != "batched" else w["queries"][0]
-        if kind == "ragged":
-            cpu_pts = w["points"][: w["offsets"][1]]
-            cpu_q = w["queries"][: w["query_offsets"][1]]
-        line["cpu_baseline"] = cpu_baseline(cpu_pts, cpu_q, k, min(args.cpu_sample, cpu_q.shape[0]))
+        line["cpu_baseline"] = cpu_baseline(job_clouds(w), k, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 

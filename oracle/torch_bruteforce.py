@@ -2,8 +2,8 @@
 (tests/test_knn.py:10-12: ``(q[:, None] - p[None]).square().sum(-1)`` then
 ``topk(largest=False)``) with the (distance, index) tie rule.
 
-TEST INFRASTRUCTURE ONLY (oracle package): bench.py times it as the CPU
-baseline; tests may use it as a second, independent checker.
+TEST INFRASTRUCTURE ONLY (oracle package): tests use it as a second,
+independent checker.
 
 Ties: top-k runs on the int64 composite ``float_bits(d) << 32 | index``.
 Squared distances are >= 0, so their IEEE bit patterns order like the values
