@@ -118,3 +118,37 @@ def test_binding_empty_and_shape_errors():
         _C.interpolate_neighbors(values, idx, w[..., :4], ex)
     with pytest.raises(RuntimeError, match="exact must be a contiguous bool"):
         _C.interpolate_neighbors(values, idx, w, ex.to(torch.uint8))
+
+
+def test_binding_beyond_one_grid_of_work_items():
+    """1 x 2^24 x 17 rows of one channel: more items than one capped grid
+    (2^20 work-groups of 256) holds, so the grid-stride loop's second lap
+    runs; rows each side of the lap boundary, and the last rows, are checked
+    against the tensor formula (~17 GB of device memory)."""
+    B, N, H, C, k = 1, 1 << 24, 17, 1, 4
+    rows = B * N * H
+    lap = (1 << 20) * 256
+    assert rows > lap
+    g = torch.Generator(device=DEV).manual_seed(11)
+    values = torch.randn((B, N, H, C), generator=g, device=DEV)
+    idx = torch.randint(0, N, (B, N, H, k), generator=g, device=DEV)
+    w = torch.rand((B, N, H, k), generator=g, device=DEV)
+    exact = torch.rand((B, N, H, k), generator=g, device=DEV) < 0.05
+    out = _C.interpolate_neighbors(values, idx, w, exact).view(rows, C)
+    flat_idx, flat_w, flat_e = idx.view(rows, k), w.view(rows, k), exact.view(rows, k)
+    vflat = values.view(N * H, C)
+    for lo in (0, lap - 4096, rows - 4096):
+        r = torch.arange(lo, lo + 8192 if lo < rows - 8192 else rows, device=DEV)
+        h = r % H
+        nv = vflat[flat_idx[r] * H + h[:, None]]  # (rows, k, C)
+        e = flat_e[r]
+        want = torch.zeros((len(r), C), device=DEV)
+        ex = torch.zeros((len(r), C), device=DEV)
+        for j in range(k):
+            want = want + nv[:, j] * flat_w[r, j].unsqueeze(-1)
+            ex = ex + nv[:, j] * e[:, j].float().unsqueeze(-1)
+        ex = ex / e.float().sum(-1, keepdim=True).clamp(min=1.0)
+        want = torch.where(e.any(-1, keepdim=True), ex, want)
+        assert torch.equal(out[r], want), f"rows from {lo}"
+    del values, idx, w, exact, out, flat_idx, flat_w, flat_e, vflat
+    torch.cuda.empty_cache()
