@@ -152,3 +152,37 @@ def test_binding_beyond_one_grid_of_work_items():
         assert torch.equal(out[r], want), f"rows from {lo}"
     del values, idx, w, exact, out, flat_idx, flat_w, flat_e, vflat
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dim,k,duplicates", [(2, 4, False), (3, 8, True)])
+def test_values_only_gradient_boundary(dim, k, duplicates):
+    """tests/test_gradient_boundaries.py:104-143: with pos, the displacement
+    and values all requiring gradients, the output differentiates in values
+    only; indices, distances and neighbour positions carry no gradient.
+    Exact hits (head 0 sits on its point; duplicated points) are included."""
+    g = torch.Generator().manual_seed(40 + dim)
+    n = 16
+    base = torch.rand((2, n, dim), generator=g)
+    if duplicates:
+        base[:, 8:] = base[:, :8]
+    pos = base.to(DEV).requires_grad_(True)
+    disp = torch.zeros((2, n, 3, dim), device=DEV)
+    disp[:, :, 1, 0] = 0.02
+    disp[:, :, 2, 0] = torch.linspace(-0.03, 0.03, n, device=DEV)
+    rho = disp.requires_grad_(True)
+    q = (pos[:, :, None, :] + rho).contiguous()
+    q.retain_grad()
+    feats = torch.stack([base[..., 0], base[..., 1], base[..., 0].square() + 0.25,
+                         torch.sin(4 * base[..., 0]), torch.cos(3 * base[..., 1])], -1)
+    values = feats[:, :, None, :].repeat(1, 1, 3, 1).contiguous().to(DEV).requires_grad_(True)
+
+    out = tb.interpolate_displaced(pos, q, values, k)
+    idx, d2, rows = tb.query_displaced_knn(pos, q, k)
+    assert out.shape == values.shape and torch.isfinite(out).all()
+    assert (d2[:, :, 0] <= 1e-12).any()
+    assert not idx.requires_grad and not d2.requires_grad and not rows.requires_grad
+    with torch.no_grad():  # the fused kernel gives the same values
+        assert torch.equal(tb.interpolate_displaced(pos, q, values, k), out.detach())
+    out.square().mean().backward()
+    assert values.grad is not None and torch.isfinite(values.grad).all() and values.grad.abs().sum() > 0
+    assert pos.grad is None and rho.grad is None and q.grad is None
