@@ -400,3 +400,19 @@ def test_build_rejects_more_than_int32_points_without_copying():
     with pytest.raises(ValueError, match="build_bvh: total point count must fit in signed int32"):
         tb.build_bvh(one.expand(2, 2**30, 3))
     assert torch.cuda.memory_allocated(DEV) == before
+
+
+def test_readme_example_runs():
+    """tests/test_readme_examples.py:19-35 for this package's README: its
+    Python example runs as written and returns the documented shapes."""
+    import re
+    from pathlib import Path
+
+    readme = (Path(__file__).resolve().parents[1] / "README.md").read_text(encoding="utf-8")
+    examples = re.findall(r"```python\n(.*?)\n```", readme, re.DOTALL)
+    assert len(examples) == 1
+    ns: dict = {}
+    exec(compile(examples[0], "README.md", "exec"), ns)
+    assert ns["idx"].shape == (10_000, 16) and ns["idx"].dtype == torch.int64
+    assert ns["d2"].dtype == torch.float32 and (ns["d2"].diff(dim=1) >= 0).all()
+    assert ns["idx_b"].shape == (4, 2_000, 8)
