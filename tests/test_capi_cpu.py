@@ -30,6 +30,20 @@ def test_header_declares_the_expected_entry_points():
         assert required in names
 
 
+@pytest.mark.parametrize("compiler,lang,std", [("gcc", "c", "c99"), ("g++", "c++", "c++17")])
+def test_header_compiles_standalone(compiler, lang, std):
+    """The public header is plain C (and C++-includable): no HIP or torch
+    types, self-contained includes."""
+    import shutil
+    import subprocess
+
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not available")
+    r = subprocess.run([compiler, "-fsyntax-only", "-x", lang, f"-std={std}", "-Wall", "-Wextra", "-Werror",
+                        str(HEADER)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 def test_library_exports_every_declared_symbol():
     L = _native.load()
     missing = [n for n in declared_functions() if not hasattr(L, n)]
