@@ -250,6 +250,8 @@ def test_interpolate_neighbors_argument_errors():
         assert "need B >= 0, N >= 0, H >= 1, C >= 1 and k >= 1" in _err(L)
     assert L.tbvh_interpolate_neighbors(*args(1, 4, 2, 3, 8, None)) == 1
     assert "null input or output" in _err(L)
-    assert L.tbvh_interpolate_neighbors(*args(1, 1 << 20, 1 << 10, 1 << 12, 8)) == 1
-    assert "exceeds 2^40" in _err(L)
+    for huge in ((1, 1 << 20, 1 << 10, 1 << 12, 8), (1 << 40, 1 << 40, 1 << 10, 1, 8),
+                 (1 << 62, 4, 1, 1, 8), (1, 1, 1 << 32, 1 << 32, 8)):
+        assert L.tbvh_interpolate_neighbors(*args(*huge)) == 1  # no int64 wrap past the check
+        assert "exceeds 2^40" in _err(L)
     assert L.tbvh_interpolate_neighbors(*args(0, 4, 2, 3, 8, None)) == 0

@@ -1037,11 +1037,13 @@ int tbvh_interpolate_neighbors(const float* values, const int64_t* indices, cons
     if (B < 0 || N < 0 || H < 1 || C < 1 || k < 1) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 0, N >= 0, H >= 1, C >= 1 and k >= 1", op);
     }
-    const int64_t rows = B * N * H;
-    if (rows == 0) return ok();
-    if (rows > (int64_t{1} << 40) / C) {
+    // Checked products: sizes come from the caller.
+    int64_t rows = 0, items = 0;
+    if (__builtin_mul_overflow(B, N, &rows) || __builtin_mul_overflow(rows, H, &rows) ||
+        __builtin_mul_overflow(rows, C, &items) || items > (int64_t{1} << 40)) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: B * N * H * C exceeds 2^40", op);
     }
+    if (rows == 0) return ok();
     if (!values || !indices || !weights || !exact || !out) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }

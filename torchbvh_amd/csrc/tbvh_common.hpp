@@ -38,8 +38,11 @@ TBVH_HD int virtual_leaves(int n) { return (1 << leaf_level(n)) - n; }
 // Real nodes: n leaves + (n - 1) internal nodes with two children, plus one
 // internal node with a single real child for every level whose count of
 // virtual nodes is odd, i.e. one per set bit of the virtual-leaf count.
+// For n <= 2^30 the count fits in int (2^31 - 1 at n = 2^30, where the
+// popcount is 0); n + (n - 1) keeps the partial sums in range too, where
+// 2 * n would overflow at n = 2^30.
 TBVH_HD int real_node_count(int n) {
-    return 2 * n - 1 + popcount(static_cast<uint32_t>(virtual_leaves(n)));
+    return n + (n - 1) + popcount(static_cast<uint32_t>(virtual_leaves(n)));
 }
 
 TBVH_HD int level_of(int i) { return floor_log2(static_cast<uint32_t>(i) + 1u); }
