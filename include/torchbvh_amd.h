@@ -119,6 +119,26 @@ int tbvh_build_ragged_with_accel(const float* points, const int64_t* offsets,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* ---- build + acceleration structure without any allocation -------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tbvh_build_with_accel with its workspace taken from a
+ * library-owned device array of TBVH_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends) instead of a caller buffer.  Outputs and their
+ * layout are those of tbvh_build_with_accel, bit for bit.  Fails with
+ * TBVH_ERR_WORKSPACE_TOO_SMALL when tbvh_build_workspace_size(B, N, D)
+ * exceeds the array (about 3.9M points in total).  `stream` must belong to
+ * the calling thread's current device.  Calls no allocator.  Every call on
+ * one GPU uses that GPU's one array, so calls that overlap on one GPU
+ * (other streams, other host threads) race; calls in order on one stream
+ * do not. */
+#define TBVH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int tbvh_build_with_accel_noalloc(const float* points, int64_t B, int64_t N, int D,
+                                  float* node_aabbs, int64_t* sorted_indices,
+                                  float* scene_min, float* scene_max,
+                                  int32_t* left_child_mem, int32_t* right_child_mem,
+                                  int32_t* mem_to_leaf, void* accel, void* stream);
+
 /* ---- primitive build ----------------------------------------------------------
  * Replaces `build_primitive_bvh_batched` (torchbvh/csrc/bindings.cpp:159-160,
  * torchbvh/csrc/bvh_build.cu:60-93, 757-821; used by `_ray.py:195`):

@@ -255,3 +255,21 @@ def test_interpolate_neighbors_argument_errors():
         assert L.tbvh_interpolate_neighbors(*args(*huge)) == 1  # no int64 wrap past the check
         assert "exceeds 2^40" in _err(L)
     assert L.tbvh_interpolate_neighbors(*args(0, 4, 2, 3, 8, None)) == 0
+
+
+def test_build_noalloc_argument_errors():
+    """The no-allocation build rejects bad arguments and sizes beyond its
+    scratch array before touching the GPU."""
+    L = _native.load()
+    outs = [FAKE] * 7
+    assert L.tbvh_build_with_accel_noalloc(FAKE, 1, 1000, 3, *outs, None, None) == 1
+    assert "accel is null" in _err(L)
+    assert L.tbvh_build_with_accel_noalloc(FAKE, 1, 1000, 4, *outs, FAKE, None) == 1
+    assert "D must be 2 or 3" in _err(L)
+    assert L.tbvh_build_with_accel_noalloc(FAKE, 0, 1000, 3, *outs, FAKE, None) == 1
+    # 8M points need more workspace than the 64 MiB array holds.
+    size = ctypes.c_size_t()
+    assert L.tbvh_build_workspace_size(1, 1 << 23, 3, ctypes.byref(size)) == 0
+    assert size.value > 64 << 20
+    assert L.tbvh_build_with_accel_noalloc(FAKE, 1, 1 << 23, 3, *outs, FAKE, None) == 2
+    assert "scratch array holds 67108864" in _err(L)

@@ -52,6 +52,7 @@ def _declare(L) -> None:
     L.tbvh_build_with_accel.argtypes = (
         [_vp, _i64, _i64, _int] + [_vp] * 8 + [_vp, ctypes.c_size_t, _vp]
     )
+    L.tbvh_build_with_accel_noalloc.argtypes = [_vp, _i64, _i64, _int] + [_vp] * 9
     L.tbvh_build_ragged_with_accel.argtypes = (
         [_vp, _vp, _i64, _i64, _int] + [_vp] * 8 + [_i64, _vp, _vp, ctypes.c_size_t, _vp]
     )
@@ -117,7 +118,7 @@ def _declare(L) -> None:
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
         "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
         "tbvh_morton_sort_points_workspace_size", "tbvh_morton_sort_points",
-        "tbvh_interpolate_neighbors",
+        "tbvh_interpolate_neighbors", "tbvh_build_with_accel_noalloc",
     ):
         getattr(L, name).restype = _int
 

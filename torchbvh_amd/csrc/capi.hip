@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/torchbvh_amd.h"
@@ -320,6 +321,71 @@ int tbvh_build_with_accel(const float* points, int64_t B, int64_t N, int D, floa
                      right_child_mem, mem_to_leaf, nullptr, accel};
     return build_batched("tbvh_build_with_accel", points, B, N, D, o, workspace, workspace_bytes,
                          stream_ptr);
+}
+
+}  // extern "C"
+
+// Workspace of tbvh_build_with_accel_noalloc: one array per GPU, in each
+// GPU's copy of this code object.  In host code `noalloc_scratch` names a
+// host-side stand-in, never the device memory: only the addresses that
+// hipGetSymbolAddress returns (kept per device) are passed to kernels.
+namespace {
+
+static __device__ __align__(256) unsigned char noalloc_scratch[TBVH_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's array, looked up once per device
+// with that device current.
+int noalloc_scratch_for(const char* op, hipStream_t stream, void** out) {
+    int dev = -1;
+    TBVH_TRY(op, hipGetDevice(&dev));
+    int stream_dev = -1;
+    TBVH_TRY(op, hipStreamGetDevice(stream, &stream_dev));
+    if (stream_dev != dev) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: the stream belongs to device %d, but device %d is current",
+                    op, stream_dev, dev);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: device %d out of range", op, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        TBVH_TRY(op, hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch)));
+        if (p == nullptr || reinterpret_cast<uintptr_t>(p) % kAlign != 0) {
+            return fail(TBVH_ERR_HIP, "%s: the scratch array has no usable device address", op);
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TBVH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tbvh_build_with_accel_noalloc(const float* points, int64_t B, int64_t N, int D, float* node_aabbs,
+                                  int64_t* sorted_indices, float* scene_min, float* scene_max,
+                                  int32_t* left_child_mem, int32_t* right_child_mem, int32_t* mem_to_leaf,
+                                  void* accel, void* stream_ptr) {
+    const char* op = "tbvh_build_with_accel_noalloc";
+    if (!accel) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel is null", op);
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    const size_t need = make_layout(B, B * N, D, true).total;
+    if (need > TBVH_NOALLOC_SCRATCH_BYTES) {
+        return fail(TBVH_ERR_WORKSPACE_TOO_SMALL,
+                    "%s: %lld x %lld points need %zu bytes of workspace; the library's scratch array holds %zu",
+                    op, static_cast<long long>(B), static_cast<long long>(N), need,
+                    static_cast<size_t>(TBVH_NOALLOC_SCRATCH_BYTES));
+    }
+    void* scratch = nullptr;
+    if (int r = noalloc_scratch_for(op, static_cast<hipStream_t>(stream_ptr), &scratch)) return r;
+    const BuildOut o{node_aabbs, sorted_indices, scene_min, scene_max, left_child_mem,
+                     right_child_mem, mem_to_leaf, nullptr, accel};
+    return build_batched(op, points, B, N, D, o, scratch, TBVH_NOALLOC_SCRATCH_BYTES, stream_ptr);
 }
 
 int tbvh_build_ragged_workspace_size(int64_t B, int64_t total, int D, size_t* bytes) {
