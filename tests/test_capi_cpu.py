@@ -138,7 +138,7 @@ def test_accel_argument_errors():
     size = ctypes.c_size_t()
     assert L.tbvh_accel_size(2, 1, 3, ctypes.byref(size)) == 1
     assert L.tbvh_accel_size(2, 1000, 3, ctypes.byref(size)) == 0
-    assert size.value == ((1000 * 16 + 255) // 256) * 256 + (1000 - 2) * 16 * 4
+    assert size.value == ((1000 * 16 + 255) // 256) * 256 + 1000 * 16 * 4  # points, then one record row per point
     assert L.tbvh_accel_workspace_size(1, 1000, 2, ctypes.byref(size)) == 0
     need = size.value
     args = [FAKE] * 5 + [1, 1000, 2, FAKE]

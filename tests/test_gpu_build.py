@@ -170,9 +170,11 @@ def test_build_is_deterministic_across_calls():
 
 def assert_same_accel(a: torch.Tensor, b: torch.Tensor, counts: list[int], dim: int) -> None:
     """Accel buffers agree on every byte traversal can read: the `total`
-    16-byte points, and the node records reachable from each cloud's root
-    (records of ranges that fit one bucket are never written, nor is the
-    padding after the points)."""
+    16-byte points, the records reachable from each cloud's root (boxes,
+    child refs, parent link) and the bucket parent links (the last word of
+    the row where each bucket starts).  Nothing else is ever written: the
+    records of ranges that fit one bucket, the other last words, the
+    padding after the points."""
     assert a.shape == b.shape
     total = sum(counts)
     pts = total * 16
@@ -181,17 +183,20 @@ def assert_same_accel(a: torch.Tensor, b: torch.Tensor, counts: list[int], dim: 
     width = 4 * dim + 4
     ra = a[off:].cpu().numpy().view(np.int32).reshape(-1, width)
     rb = b[off:].cpu().numpy().view(np.int32).reshape(-1, width)
+    assert ra.shape[0] == total
     start = 0
     for c, n in enumerate(counts):
-        base = start - c  # cloud c's records start here
+        base = start  # cloud c's record rows follow its point rows
         start += n
         if n < 2:
             continue
         frontier = np.array([0])
         while frontier.size:
             rows = base + frontier
-            assert np.array_equal(ra[rows], rb[rows]), f"cloud {c}: records differ"
+            assert np.array_equal(ra[rows, :width - 1], rb[rows, :width - 1]), f"cloud {c}: records differ"
             refs = rb[rows, 4 * dim:4 * dim + 2].ravel()
+            buckets = base + (refs[refs < 0] & 0x0FFFFFFF)
+            assert np.array_equal(ra[buckets, width - 1], rb[buckets, width - 1]), f"cloud {c}: bucket links differ"
             frontier = refs[refs >= 0]
 
 
@@ -237,17 +242,23 @@ def _check_accel_boxes(points: np.ndarray, accel: torch.Tensor, sorted_idx: np.n
     children's point ranges (a bucket ref names its range; an internal child
     of a node covering [lo, hi] with index g covers [lo, g] on the left,
     [g + 1, hi] on the right); every stored child box must equal the exact
-    min/max of its points.  Returns the number of records checked."""
+    min/max of its points.  Also checks the parent links the traversal
+    resumes through: every reached record's parent word names the record
+    that referenced it (-1 at the root), and the last word of the row where
+    each bucket starts names the record that references the bucket.
+    Returns the number of records checked."""
     n = points.shape[0]
     width = 4 * dim + 4
     off = (n * 16 + 255) // 256 * 256
-    recs = accel.cpu().numpy()[off:off + (n - 1) * width * 4].view(np.float32).reshape(-1, width)
+    recs = accel.cpu().numpy()[off:off + n * width * 4].view(np.float32).reshape(-1, width)
     refs = recs[:, 4 * dim:4 * dim + 2].copy().view(np.int32)
+    links = recs[:, 4 * dim + 2:].copy().view(np.int32)
     sp = points[sorted_idx]  # Morton order
-    stack = [(0, 0, n - 1)]
+    stack = [(0, 0, n - 1, -1)]
     checked = 0
     while stack:
-        node, lo, hi = stack.pop()
+        node, lo, hi, parent = stack.pop()
+        assert int(links[node, 0]) == parent, f"record {node}: parent link"
         lref, rref = int(refs[node, 0]), int(refs[node, 1])
         if lref < 0:
             split = (lref & 0x0FFFFFFF) + ((lref >> 28) & 7)
@@ -261,9 +272,10 @@ def _check_accel_boxes(points: np.ndarray, accel: torch.Tensor, sorted_idx: np.n
                 f"record {node} child {c} range [{a}, {b}]"
             ref = (lref, rref)[c]
             if ref >= 0:
-                stack.append((ref, a, b))
+                stack.append((ref, a, b, node))
             else:
                 assert (ref & 0x0FFFFFFF) == a and ((ref >> 28) & 7) + 1 == b - a + 1
+                assert int(links[a, 1]) == node, f"bucket at {a}: parent link"
         checked += 1
     return checked
 

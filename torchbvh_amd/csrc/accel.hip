@@ -12,13 +12,18 @@
 //
 // Layout of one accel buffer (per cloud, clouds packed back to back):
 //   points  [n]    float4 (x, y, z|0, original index as int bits), Morton order
-//   records [n-1]  per radix-tree internal node i: left box (2D floats), right
-//                  box (2D floats), left ref, right ref, 2 pad words
+//   records [n]    row i < n - 1: radix-tree internal node i: left box (2D
+//                  floats), right box (2D floats), left ref, right ref,
+//                  parent node (-1 at the root); every row's last word: the
+//                  node whose record references the bucket that starts at
+//                  point row i, if one does (row n - 1 holds only that word)
 //                  (16 floats = 64 B in 3-D, 12 floats = 48 B in 2-D)
 // A child ref >= 0 is an internal node; a negative ref is a bucket of at most
 // accel_bucket<D>() (6 in 3-D, 8 in 2-D) consecutive points:
-// 0x80000000 | (count - 1) << 28 | first.  Cloud c's
-// records start at row (first point of c) - c.
+// 0x80000000 | (count - 1) << 28 | first.  Record rows follow point rows:
+// cloud c's rows start at its first point row.  The parent links let the
+// traversal resume exactly after its bounded stack dropped entries
+// (knn.hip); words no node writes are never read.
 //
 // Child boxes are exact: each is the min/max over its point range, assembled
 // from the implicit tree's node AABBs with an iterative segment-tree cover of
@@ -76,7 +81,7 @@ __global__ __launch_bounds__(kBlock) void accel_points_kernel(
 constexpr int kCodeWindow = 2 * kBlock + 2 * kCodeHalo;
 template <int D>
 __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
-    const Segment* __restrict__ segs, int S, int64_t total_internal, int64_t total_points,
+    const Segment* __restrict__ segs, int S, int64_t total_points,
     const uint32_t* __restrict__ all_codes, const float* __restrict__ node_aabbs,
     float* __restrict__ records) {
     constexpr int R = 4 * D + 4;
@@ -84,11 +89,9 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
     __shared__ int64_t s_w0;
     const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kBlock;
     const int64_t r = r0 + threadIdx.x;
-    auto rec_first = [&](int c) { return segs[c].start - c; };
     if (threadIdx.x == 0) {
-        // Record r belongs to cloud s at global code position r + s.
-        const int sa = find_segment(rec_first, S, r0);
-        const int64_t p0 = r0 + sa - kCodeHalo;
+        // Record row r is node r - start of the cloud holding point row r.
+        const int64_t p0 = r0 - kCodeHalo;
         s_w0 = p0 < 0 ? 0 : p0;
     }
     __syncthreads();
@@ -98,11 +101,11 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
         s_codes[k] = gp < total_points ? all_codes[gp] : 0u;
     }
     __syncthreads();
-    if (r >= total_internal) return;
-    const int s = find_segment(rec_first, S, r);
+    if (r >= total_points) return;
+    const int s = find_segment([&](int c) { return segs[c].start; }, S, r);
     const Segment g = segs[s];
     const int n = g.n;
-    const int i = static_cast<int>(r - (g.start - s));
+    const int i = static_cast<int>(r - g.start);
     if (i >= n - 1) return;
     // The window in positions of this cloud, clipped to it.
     CodeView cv;
@@ -126,10 +129,7 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
     range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
 #pragma unroll
     for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
-    rec[4 * D] = __int_as_float(child_ref<D>(first, gamma, gamma));
-    rec[4 * D + 1] = __int_as_float(child_ref<D>(gamma + 1, last, gamma + 1));
-    rec[4 * D + 2] = 0.0f;
-    rec[4 * D + 3] = 0.0f;
+    link_record<D>(records + g.start * R, i, first, gamma, last);
 }
 
 // Records of the radix-tree nodes the fused first tree pass could not
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
             if (gl < g.groups[0]) {
                 const int width = 1 << (g.leaf_level < kSubtreeLevels ? g.leaf_level : kSubtreeLevels);
                 cnt = span_count[G];
-                list0 = (g.start - sg) + static_cast<int64_t>(gl) * width;
+                list0 = g.start + static_cast<int64_t>(gl) * width;
             }
         }
         s_seg[tid] = sg;
@@ -191,8 +191,11 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
         cv.n = g.n;
         int first, last, gamma;
         karras_node(cv, i, first, last, gamma);
+        // A node inside a bucket is never referenced; it must not write,
+        // since its child links would overwrite the bucket's own link.
+        if (i != 0 && last - first + 1 <= accel_bucket<D>()) continue;
         const float* nodes = node_aabbs + g.node_start * 2 * D;
-        float* rec = records + ((g.start - sg) + i) * R;
+        float* rec = records + (g.start + i) * R;
         float box[2 * D];
         range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, box);
 #pragma unroll
@@ -200,10 +203,7 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
         range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
 #pragma unroll
         for (int c = 0; c < 2 * D; ++c) rec[2 * D + c] = box[c];
-        rec[4 * D] = __int_as_float(child_ref<D>(first, gamma, gamma));
-        rec[4 * D + 1] = __int_as_float(child_ref<D>(gamma + 1, last, gamma + 1));
-        rec[4 * D + 2] = 0.0f;
-        rec[4 * D + 3] = 0.0f;
+        link_record<D>(records + g.start * R, i, first, gamma, last);
     }
 }
 
@@ -213,8 +213,8 @@ inline unsigned grid_for(int64_t items) {
 
 }  // namespace
 
-size_t accel_bytes(int64_t total, int64_t S, int D) {
-    return accel_points_bytes(total) + static_cast<size_t>(total - S) * (4 * D + 4) * sizeof(float);
+size_t accel_bytes(int64_t total, int64_t /*S*/, int D) {
+    return accel_points_bytes(total) + static_cast<size_t>(total) * (4 * D + 4) * sizeof(float);
 }
 
 hipError_t launch_accel_points(const float* points, const int64_t* sorted, const float* scene_min,
@@ -239,11 +239,11 @@ hipError_t launch_accel_nodes(const float* node_aabbs, int D, const Segment* seg
     float* records = reinterpret_cast<float*>(static_cast<char*>(accel) + accel_points_bytes(total));
     const int Si = static_cast<int>(S);
     if (D == 3) {
-        accel_nodes_kernel<3><<<grid_for(total - S), kBlock, 0, stream>>>(
-            segs, Si, total - S, total, sorted_codes, node_aabbs, records);
+        accel_nodes_kernel<3><<<grid_for(total), kBlock, 0, stream>>>(segs, Si, total, sorted_codes, node_aabbs,
+                                                                      records);
     } else {
-        accel_nodes_kernel<2><<<grid_for(total - S), kBlock, 0, stream>>>(
-            segs, Si, total - S, total, sorted_codes, node_aabbs, records);
+        accel_nodes_kernel<2><<<grid_for(total), kBlock, 0, stream>>>(segs, Si, total, sorted_codes, node_aabbs,
+                                                                      records);
     }
     return hipGetLastError();
 }

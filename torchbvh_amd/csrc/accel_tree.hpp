@@ -170,5 +170,25 @@ __device__ __forceinline__ int32_t child_ref(int first, int last, int internal) 
     return internal;
 }
 
+// Child refs and parent links of radix-tree node i with range [first, last]
+// and split gamma (`records`: the cloud's first record row).  The node
+// writes its own child refs and its children's parent links: word 4D + 2
+// of an internal child's row, word 4D + 3 of the row where a bucket child
+// starts; the root also writes its own parent word (-1).  Every word has
+// exactly one writer, so no ordering between nodes is needed.
+template <int D>
+__device__ __forceinline__ void link_record(float* records, int i, int first, int gamma, int last) {
+    constexpr int R = 4 * D + 4;
+    float* rec = records + static_cast<int64_t>(i) * R;
+    const int32_t lref = child_ref<D>(first, gamma, gamma);
+    const int32_t rref = child_ref<D>(gamma + 1, last, gamma + 1);
+    rec[4 * D] = __int_as_float(lref);
+    rec[4 * D + 1] = __int_as_float(rref);
+    if (i == 0) rec[4 * D + 2] = __int_as_float(-1);
+    records[static_cast<int64_t>(lref >= 0 ? lref : first) * R + 4 * D + (lref >= 0 ? 2 : 3)] = __int_as_float(i);
+    records[static_cast<int64_t>(rref >= 0 ? rref : gamma + 1) * R + 4 * D + (rref >= 0 ? 2 : 3)] =
+        __int_as_float(i);
+}
+
 }  // namespace
 }  // namespace tbvh

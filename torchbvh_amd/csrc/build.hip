@@ -520,7 +520,7 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
         // the group's own record rows, for launch_accel_span.
         constexpr int R = 4 * D + 4;
         const int i = g0 + tid;
-        const int64_t rec0 = g.start - s;  // the cloud's first record row
+        const int64_t rec0 = g.start;  // the cloud's first record row
         bool spans = false;
         if (tid < width && i < g.n - 1) {
             CodeView cv;
@@ -545,10 +545,7 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                     range_box_lds<D>(s_box, width, gamma + 1 - g0, last - g0, box);
 #pragma unroll
                     for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
-                    rec[4 * D] = __int_as_float(child_ref<D>(first, gamma, gamma));
-                    rec[4 * D + 1] = __int_as_float(child_ref<D>(gamma + 1, last, gamma + 1));
-                    rec[4 * D + 2] = 0.0f;
-                    rec[4 * D + 3] = 0.0f;
+                    link_record<D>(out.accel_records + rec0 * R, i, first, gamma, last);
                 }
             }
         }

@@ -232,61 +232,80 @@ __global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
     write_results<K, D>(a, out_row, best, index_offset, pstart);
 }
 
-// Exact distance to a point stored as float4.  On a leaf's degenerate box
-// the box formula above gives delta = |q - p| per axis; e = p - q has the
-// same square (IEEE subtraction is sign-symmetric), so the fused chain over
-// e is bit-identical and costs half the instructions.
+// Exact distance to a point stored as float4, bit-identical to box_distance
+// on the point's degenerate box (lo = hi = p) for every input, NaN and inf
+// included.  There, delta = max(p - q, max(0, q - p)); IEEE subtraction is
+// sign-symmetric (q - p = -(p - q), also for inf, and NaN for NaN), so
+// delta = |p - q| when p - q is not NaN and 0 when it is (max returns the
+// non-NaN operand: a NaN query coordinate, or equal infinities, count 0 on
+// that axis).  max(|e|, 0) with e = p - q gives exactly that in one
+// instruction (abs is a source modifier; arithmetic NaNs are quiet).
 template <int D>
 __device__ __forceinline__ float point_distance(const float* q, const float4 p) {
     const float pc[3] = {p.x, p.y, p.z};
     float s = 0.0f;
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        const float e = pc[d] - q[d];
+        const float e = fmaxf(fabsf(pc[d] - q[d]), 0.0f);
         s = d == 0 ? e * e : __builtin_fmaf(e, e, s);
     }
     return s;
 }
 
-constexpr int kAccelStackDepth = 64;   // radix-tree depth <= 64 (64-bit keys)
 // One wave per work-group: measured against 256 threads, -3.5% at cfg2 and
 // -14% at cfg5, whose waves differ most in cost (finer-grained balancing
 // over the CUs); 128 falls between, 512 is 13-24% slower.
 constexpr int kAccelBlock = 64;
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 
-// Stack entries kept in LDS per lane, by dimension and k (the rest spill
-// to scratch).  Deeper LDS stacks cut scratch traffic until the LDS, not
-// the registers, limits the work-groups per CU.  Measured on MI355X against
-// 12: 3-D k = 16 with 15, -4.5% (cfg2) and -6% (cfg3), 14 and 16 slower
-// than 15; 3-D k = 32 with 20, -4% (cfg5; -1% over 15), 14 and 16 slower; 2-D k = 8 with 20,
-// -2% (cfg4), 14, 16, 18 and 24 slower.  Other (D, k) keep 12.
+// Entries of a lane's deferred-node stack, all in LDS (6 bytes each: a
+// 32-bit child ref and a 16-bit distance, in columns of stride
+// kAccelBlock): as many as the LDS budget of each (D, k) holds.  The budgets
+// are the ones measured best for the earlier 8-byte entries: 7.5 KB per
+// work-group for 3-D k = 16, 10 KB for 3-D k = 32 and 2-D k = 8, 6 KB
+// otherwise.
 template <int D, int K>
 constexpr int lds_stack_entries() {
-    if (D == 2 && K == 8) return 20;
-    if (D == 3 && K >= 32) return 20;
-    if (D == 3 && K >= 16) return 15;
-    return 12;
+    if (D == 2 && K == 8) return 26;
+    if (D == 3 && K >= 32) return 26;
+    if (D == 3 && K >= 16) return 20;
+    return 16;
 }
 
-// Deferred-node stack of one lane: the first L entries live in an LDS
-// column (stride kAccelBlock), deeper ones in scratch.
+// Bounded deferred-node stack of one lane: a ring of L entries in LDS.  An
+// entry is a child ref and its cached box distance truncated to the top 16
+// bits of the float (a lower bound: truncation rounds a non-negative float
+// down), which is all pruning needs; a popped node that survives it is
+// evaluated exactly.  A push onto a full ring drops the oldest entry (the
+// far child of the shallowest pending ancestor, pushed while the k-th
+// distance was loosest, so the likeliest to be pruned by the time it would
+// be popped) and keeps the smallest dropped distance in `lost_min`.
+// Nothing is lost for correctness: when the ring empties with lost_min <=
+// the k-th distance, the traversal resumes through the parent links (see
+// knn_accel_kernel).
 template <int L>
-struct NodeStack {
-    uint64_t* col;
-    uint64_t spill[kAccelStackDepth - L];
-    int sp = 0;
+struct RingStack {
+    uint32_t* refs;   // this lane's column: slot i at refs[i * kAccelBlock]
+    uint16_t* dists;  // likewise
+    int top = 0;      // slot of the next push
+    int count = 0;
+    float lost_min = INFINITY;
     __device__ __forceinline__ void push(float d, int32_t ref) {
-        const uint64_t e = (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<uint32_t>(ref);
-        if (sp < L) col[sp * kAccelBlock] = e;
-        else spill[sp - L] = e;
-        ++sp;
+        if (count == L) {
+            // Full: slot `top` holds the oldest entry.
+            lost_min = fminf(lost_min, __uint_as_float(static_cast<uint32_t>(dists[top * kAccelBlock]) << 16));
+        } else {
+            ++count;
+        }
+        refs[top * kAccelBlock] = static_cast<uint32_t>(ref);
+        dists[top * kAccelBlock] = static_cast<uint16_t>(__float_as_uint(d) >> 16);
+        top = top == L - 1 ? 0 : top + 1;
     }
     __device__ __forceinline__ void pop(float& d, int32_t& ref) {
-        --sp;
-        const uint64_t e = sp < L ? col[sp * kAccelBlock] : spill[sp - L];
-        ref = static_cast<int32_t>(static_cast<uint32_t>(e));
-        d = __uint_as_float(static_cast<uint32_t>(e >> 32));
+        top = top == 0 ? L - 1 : top - 1;
+        --count;
+        ref = static_cast<int32_t>(refs[top * kAccelBlock]);
+        d = __uint_as_float(static_cast<uint32_t>(dists[top * kAccelBlock]) << 16);
     }
 };
 
@@ -318,6 +337,26 @@ __device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int 
 // pruning rule, near-first order and cached far-child distances of the
 // implicit-tree kernel above; deferred nodes on a per-lane stack.
 //
+// Bounded stack, exact resume.  The stack is a ring of lds_stack_entries
+// entries in LDS (RingStack); nothing lives in scratch.  When a push drops the oldest
+// entry, the lane records the smallest dropped distance.  When the ring
+// runs empty, nothing dropped can matter if that distance exceeds the k-th
+// distance (which only shrinks), and the lane is done.  Otherwise it walks
+// up from the last node it entered through the parent links: at each
+// ancestor it recomputes the two child distances, and if it came up from
+// the near child and the far child is within the k-th distance, the far
+// child is still pending (it was dropped: a far child pushed and not
+// dropped is popped before the ring empties, after which the walk comes up
+// through it) and the traversal resumes there; otherwise it goes on up,
+// and at the root it is done.  The walk recomputes the same near/far
+// choice the descent made (same query, same boxes, ties to the left), so
+// no subtree is entered twice and no candidate is inserted twice.  Each
+// walk step costs two dependent loads (the parent link, then the parent's
+// record), and one walking lane holds up its wave, so the ring is sized to
+// make drops rare: a CPU model of the traversal at cfg2 showed no query
+// deeper than 21 entries (a 16-entry ring of 8-byte entries made every
+// query drop and measured +20% traversal time).
+//
 // Postponed buckets.  With one query per lane, the O(K) insertion into the
 // sorted list is the dominant cost, and the wave pays for it whenever any
 // lane inserts.  So a lane that reaches a bucket parks it and keeps
@@ -343,7 +382,8 @@ template <int D, int K, bool kOrdered, bool kRagged>
 __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     constexpr int R = 4 * D + 4;
     constexpr int kLds = lds_stack_entries<D, K>();
-    __shared__ uint64_t lds_stack[kLds * kAccelBlock];
+    __shared__ uint32_t lds_refs[kLds * kAccelBlock];
+    __shared__ uint16_t lds_dists[kLds * kAccelBlock];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     const int64_t gid = tile * kAccelBlock + threadIdx.x;
@@ -382,7 +422,8 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     const float4* pts = static_cast<const float4*>(accel) + pstart;
     const float* recs = reinterpret_cast<const float*>(static_cast<const char*>(accel) +
                                                        accel_points_bytes(total_points)) +
-                        (pstart - seg) * R;
+                        pstart * R;
+
 
     float q[D];
 #pragma unroll
@@ -392,8 +433,9 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
 #pragma unroll
     for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
 
-    NodeStack<kLds> stack;
-    stack.col = lds_stack + threadIdx.x;
+    RingStack<kLds> stack;
+    stack.refs = lds_refs + threadIdx.x;
+    stack.dists = lds_dists + threadIdx.x;
     int32_t ref = n <= accel_bucket<D>()
                       ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
                       : 0;
@@ -451,7 +493,7 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
                 const int32_t far_ref = left_near ? rref : lref;
                 const float near_d = left_near ? ld : rd;
                 const float far_d = left_near ? rd : ld;
-                if (far_d <= worst && stack.sp < kAccelStackDepth) stack.push(far_d, far_ref);
+                if (far_d <= worst) stack.push(far_d, far_ref);
                 if (near_d <= worst) {
                     ref = near_ref;
                     nd = near_d;
@@ -459,8 +501,44 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
                 }
             }
         }
-        if (stack.sp == 0) {
-            done = true;  // stays in the loop until its parked buckets are scanned
+        if (stack.count == 0) {
+            if (!(stack.lost_min <= worst)) {
+                done = true;  // stays in the loop until its parked buckets are scanned
+                continue;
+            }
+            // One step of the resume walk from `ref`, the last node entered
+            // (its subtree is finished), to its parent.
+            // An internal node's parent is in its own row; a bucket's, in the
+            // last word of the row where it starts.
+            const int32_t par = __float_as_int(
+                recs[static_cast<int64_t>(ref >= 0 ? ref : ref & 0x0fffffff) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
+            if (par < 0 || par >= n - 1) {
+                done = true;  // the root (or a link outside the cloud, which a well-formed accel never holds)
+                continue;
+            }
+            const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(par) * R);
+            float rec[R];
+#pragma unroll
+            for (int v = 0; v < R / 4; ++v) {
+                const float4 x = r4[v];
+                rec[4 * v] = x.x;
+                rec[4 * v + 1] = x.y;
+                rec[4 * v + 2] = x.z;
+                rec[4 * v + 3] = x.w;
+            }
+            const float ld = box_distance<D>(q, rec);
+            const float rd = box_distance<D>(q, rec + 2 * D);
+            const bool left_near = ld <= rd;
+            const int32_t near_ref = __float_as_int(rec[4 * D + (left_near ? 0 : 1)]);
+            const int32_t far_ref = __float_as_int(rec[4 * D + (left_near ? 1 : 0)]);
+            const float far_d = left_near ? rd : ld;
+            if (ref == near_ref && far_d <= worst) {
+                ref = far_ref;  // a dropped far child: resume there
+                nd = far_d;
+            } else {
+                ref = par;  // finished here too: next step from the parent
+                nd = INFINITY;
+            }
             continue;
         }
         stack.pop(nd, ref);
