@@ -160,8 +160,12 @@ int tbvh_build_primitives(const float* primitives, int64_t B, int64_t F, int V, 
  * Replaces `morton_sort_points_batched` (torchbvh/csrc/bindings.cpp:194,
  * torchbvh/csrc/bvh_build.cu:723-740; used by `_fps.py:112, 190`): each
  * cloud's bounds, 30/32-bit Morton codes against them and the stable order,
- * `sorted_indices` [B, N] int64 (cloud-local) -- the `sorted_indices` of
- * tbvh_build without the tree. */
+ * `sorted_indices` [B, N] int64 (cloud-local).  The bounds are the points'
+ * plain min / max (the reference's points.min(1) / max(1), :731-732), not
+ * the build's +-1e30-seeded ones, so the order equals tbvh_build's
+ * `sorted_indices` except for a cloud lying entirely beyond +-1e30 on an
+ * axis.  NaN coordinates are outside the contract (torch's min/max
+ * propagate NaN, the reduction here skips it). */
 int tbvh_morton_sort_points_workspace_size(int64_t B, int64_t N, int D, size_t* bytes);
 int tbvh_morton_sort_points(const float* points, int64_t B, int64_t N, int D,
                             int64_t* sorted_indices,
@@ -300,12 +304,17 @@ int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
  * directly (torchbvh/csrc/knn_query.cu:47-154).  Built from a finished BVH
  * (the points plus tbvh_build's / tbvh_build_ragged's outputs), an accel
  * buffer holds a radix tree over the same Morton order with exact child
- * boxes and 8-point leaf buckets; tbvh_knn_accel(_ragged) returns exactly
- * what tbvh_knn(_ragged) returns for the same BVH while visiting about ten
- * times fewer nodes.  Clouds may hold at most 2^28 points.
+ * boxes, parent links and leaf buckets of up to 6 (3-D) or 8 (2-D) points;
+ * tbvh_knn_accel(_ragged) returns exactly what tbvh_knn(_ragged) returns for
+ * the same BVH while visiting about ten times fewer nodes.  Clouds may hold
+ * at most 2^28 points.
  *   accel bytes   : tbvh_accel_size(B, total_points, D)
  *   workspace     : tbvh_accel_workspace_size(B, total_points, D)
- * For the batched form total_points = B * N. */
+ * For the batched form total_points = B * N.  tbvh_accel_build_from_tree
+ * needs only the BVH's node_aabbs and sorted_indices (a caller of the
+ * reference's query bindings holds nothing else): the leaf rows are the
+ * points in Morton order and the root box gives the build's bounds, so it
+ * writes the same bytes as tbvh_accel_build. */
 int tbvh_accel_size(int64_t B, int64_t total_points, int D, size_t* bytes);
 int tbvh_accel_workspace_size(int64_t B, int64_t total_points, int D, size_t* bytes);
 int tbvh_accel_build(const float* points, const int64_t* sorted_indices,
@@ -313,6 +322,9 @@ int tbvh_accel_build(const float* points, const int64_t* sorted_indices,
                      const float* scene_max, int64_t B, int64_t N, int D,
                      void* accel, void* workspace, size_t workspace_bytes,
                      void* stream);
+int tbvh_accel_build_from_tree(const float* node_aabbs, const int64_t* sorted_indices,
+                               int64_t B, int64_t N, int D, void* accel,
+                               void* workspace, size_t workspace_bytes, void* stream);
 int tbvh_accel_build_ragged(const float* points, const int64_t* offsets,
                             const int64_t* sorted_indices, const float* node_aabbs,
                             const float* scene_min, const float* scene_max,

@@ -181,6 +181,16 @@ def build(points) -> dict:
     }
 
 
+def morton_point_order(points) -> np.ndarray:
+    """Point ordering of one cloud (torchbvh/csrc/bvh_build.cu:723-740, used
+    by FPS): Morton codes against the points' plain min / max
+    (points.min(1) / max(1), :731-732; no +-1e30 seeds, unlike the build),
+    then a stable order (the reference's torch.sort is not stable; the two
+    agree wherever codes are distinct)."""
+    p = _f32(points)
+    return stable_argsort(morton_codes(p, p.min(0), p.max(0)))
+
+
 def build_batched(points) -> dict:
     """[B, N, D] build: the single build per cloud, stacked."""
     p = _f32(points)

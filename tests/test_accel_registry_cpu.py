@@ -20,10 +20,24 @@ def test_registered_accel_follows_the_build_tensors_and_their_views():
     assert _native._registered_accel(nodes.clone(), order) is None
     assert _native._registered_accel(nodes, order.clone()) is None
     assert _native._registered_accel(nodes[:1], order) is None  # a part is not the BVH
-    assert _native._pick_accel(False, nodes, order) is None
-    other = torch.ones(1)
-    assert _native._pick_accel(other, nodes, order) is other
-    assert _native._pick_accel(None, nodes, order) is accel
+    assert _native._pick_accel("op", False, nodes, order, 3) is None
+    assert _native._pick_accel("op", None, nodes, order, 3) is accel
+
+
+def test_explicit_accel_tensors_are_checked_before_launch():
+    """An accel handed in explicitly must be contiguous 1-D uint8 on the
+    queries' device and as large as the layout for the BVH's clouds; these
+    checks run before any native call."""
+    import pytest
+
+    nodes = torch.rand(2, 7, 6)
+    order = torch.arange(8).repeat(2, 1)
+    for bad in (torch.ones(1), torch.zeros((2, 8), dtype=torch.uint8),
+                torch.zeros(32, dtype=torch.uint8)[::2]):
+        with pytest.raises(RuntimeError, match="contiguous 1-D uint8"):
+            _native._pick_accel("op", bad, nodes, order, 3)
+    with pytest.raises(RuntimeError, match="queries' device"):
+        _native._pick_accel("op", torch.zeros(1 << 12, dtype=torch.uint8), nodes, order, 3)
 
 
 def test_modified_tensors_lose_the_accel():

@@ -77,13 +77,16 @@ def test_point_geometry_validation():
 
 
 def test_k_message_lists_supported_values():
-    from torchbvh_amd._validation import _validate_supported_k
+    """The reference's tests match "k must be 4, 8, or 16"; the message keeps
+    that wording and names the k = 32 extension after it."""
+    from torchbvh_amd._validation import check_k
 
     for k in (4, 8, 16, 32):
-        _validate_supported_k("query_knn", k)
+        check_k("query_knn", k)
     for k in (0, 1, 5, 12, 64):
-        with pytest.raises(ValueError, match="k must be 4, 8, 16, or 32"):
-            _validate_supported_k("query_knn", k)
+        with pytest.raises(ValueError, match="k must be 4, 8, or 16") as err:
+            check_k("query_knn", k)
+        assert "32 is also supported" in str(err.value)
 
 
 def test_handle_lifecycle_without_gpu():

@@ -100,7 +100,7 @@ def test_knn_argument_errors():
     nr = _native.real_node_count(100)
     base = [FAKE, FAKE, FAKE, None, 1, 10]
     assert L.tbvh_knn(*base, 100, nr, 3, 5, FAKE, FAKE, None) == 1
-    assert "k must be 4, 8, 16, or 32" in _err(L)
+    assert "k must be 4, 8, or 16 (32 is also supported)" in _err(L)
     assert L.tbvh_knn(*base, 100, nr, 4, 8, FAKE, FAKE, None) == 1
     assert "D must be 2 or 3" in _err(L)
     assert L.tbvh_knn(*base, 3, _native.real_node_count(3), 3, 4, FAKE, FAKE, None) == 1
@@ -234,7 +234,7 @@ def test_knn_positions_argument_errors():
     # Then the traversal's own checks apply (k here).
     bad_k = (FAKE, FAKE, FAKE, 1, 10, 100, 3, 5, FAKE, 3, FAKE, FAKE, FAKE, None)
     assert L.tbvh_knn_accel_positions(*bad_k) == 1
-    assert "k must be 4, 8, 16, or 32" in _err(L)
+    assert "k must be 4, 8, or 16 (32 is also supported)" in _err(L)
     ragged = (FAKE, FAKE, 100, FAKE, FAKE, FAKE, 2, 10, 3, 16, NUL, 3, FAKE, FAKE, FAKE, None)
     assert L.tbvh_knn_accel_ragged_positions(*ragged) == 1
     assert "tbvh_knn_accel_ragged_positions" in _err(L) and "null source" in _err(L)

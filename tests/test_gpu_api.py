@@ -54,7 +54,7 @@ def test_single_lifecycle_and_payload(dim):
 def test_single_query_validation():
     pts = rand(16, 3, seed=1)
     bvh = tb.build_bvh(pts)
-    with pytest.raises(ValueError, match="k must be 4, 8, 16, or 32"):
+    with pytest.raises(ValueError, match="k must be 4, 8, or 16"):
         tb.query_knn(bvh, pts, 5)
     with pytest.raises(TypeError, match="BVHHandle"):
         tb.query_knn(dict(bvh), pts[:3], 4)
@@ -205,7 +205,7 @@ def test_ragged_query_validation():
     pts = rand(11, 2, seed=5)
     q = rand(8, 2, seed=6)
     bvh = tb.build_bvh(pts, batch_offsets=offsets([0, 3, 11]))
-    with pytest.raises(ValueError, match="k must be 4, 8, 16, or 32"):
+    with pytest.raises(ValueError, match="k must be 4, 8, or 16"):
         tb.query_knn(bvh, q, 5, query_offsets=offsets([0, 4, 8]))
     with pytest.raises(ValueError, match="batch size"):
         tb.query_knn(bvh, q, 4, query_offsets=offsets([0, 2, 5, 8]))

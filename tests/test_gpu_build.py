@@ -20,6 +20,7 @@ from parity import (
     pathological_clouds,
     single_child_cloud,
 )
+from torchbvh_amd import _native
 from torchbvh_amd._native import _C
 
 pytestmark = pytest.mark.gpu
@@ -295,3 +296,34 @@ def test_accel_records_hold_exact_child_boxes(case):
     h = tb.build_bvh(dev(p))
     checked = _check_accel_boxes(p, h._aux["accel"], h["sorted_indices"].cpu().numpy(), p.shape[1])
     assert checked > p.shape[0] // 8
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("B,n", [(1, 1), (1, 6), (1, 4097), (3, 70_001), (1, 200_001)])
+def test_accel_from_tree_matches_fused_build(B, n, dim):
+    """An accel rebuilt from node_aabbs and sorted_indices alone (leaf rows
+    as the points, bounds from the root box) holds the fused build's bytes."""
+    rng = np.random.default_rng(B * n + dim)
+    pts = rng.random((B, n, dim), dtype=np.float32)
+    data = _C.build_bvh_batched_cooperative(dev(pts), with_accel=True)
+    L = _native.load()
+    nodes, sidx = data["node_aabbs"].clone(), data["sorted_indices"].clone()
+    accel = _native._accel_from_tree(nodes, sidx, dim)
+    torch.cuda.synchronize()
+    assert accel is not None and accel.numel() == data["accel"].numel()
+    assert _native._registered_accel(nodes, sidx) is accel
+    assert_same_accel(data["accel"], accel, [n] * B, dim)
+    del L
+
+
+def test_accel_from_tree_recovers_bounds_beyond_the_seeds():
+    """A cloud lying entirely above 1e30 on one axis: the build's bounds are
+    the seed (1e30) there, not the root box's minimum; the rebuilt accel
+    must use the same bounds, hence the same codes and tree."""
+    rng = np.random.default_rng(17)
+    pts = rng.random((1, 5000, 3), dtype=np.float32)
+    pts[..., 1] = 2e30 + pts[..., 1] * 1e30
+    data = _C.build_bvh_batched_cooperative(dev(pts), with_accel=True)
+    accel = _native._accel_from_tree(data["node_aabbs"].clone(), data["sorted_indices"].clone(), 3)
+    torch.cuda.synchronize()
+    assert_same_accel(data["accel"], accel, [5000], 3)

@@ -387,3 +387,50 @@ def test_reference_style_bindings_use_the_registered_accel():
         assert_same_f32(ad[b].cpu().numpy(), ed, f"cloud {b} distances")
     d["node_aabbs"].mul_(1.0)
     assert _native._registered_accel(d["node_aabbs"], d["sorted_indices"]) is None
+
+
+def test_reference_style_bindings_on_cloned_tensors_build_an_accel():
+    """The tensors a reference-style caller passes need not be the ones the
+    build returned: a clone (or copy, or reload) gets an accel built from
+    node_aabbs and sorted_indices alone on first use, registered for the
+    next calls.  cfg2's size: results equal the registered path's on every
+    row and the oracle's on a sample; the call takes the accel, not the
+    implicit tree (printed timings: first call with the accel build,
+    second from the registry)."""
+    import time
+
+    g = torch.Generator("cpu").manual_seed(2001)
+    p = torch.rand((1, 1 << 20, 3), generator=g)
+    q = torch.rand((1, 1 << 20, 3), generator=torch.Generator("cpu").manual_seed(2002))
+    pd, qd = p.to(DEV), q.to(DEV)
+    d = _C.build_bvh_batched_cooperative(pd)
+    order = _C.morton_sort_queries_narrow(qd, d["scene_min"], d["scene_max"])
+    args = (d["num_leaves"], d["num_real_nodes"], 3, 16)
+    ri, rd = _C.query_knn_batched_cached_bounds_ordered(d["node_aabbs"], d["sorted_indices"], qd, order, *args)
+    nodes, sidx = d["node_aabbs"].clone(), d["sorted_indices"].clone()
+    assert _native._registered_accel(nodes, sidx) is None
+    times = []
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ci, cd = _C.query_knn_batched_cached_bounds_ordered(nodes, sidx, qd, order, *args)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    print(f"cloned tensors: first call {times[0]:.3f} ms (accel built), second {times[1]:.3f} ms", flush=True)
+    assert _native._registered_accel(nodes, sidx) is not None
+    assert torch.equal(ci, ri) and torch.equal(cd, rd)
+    rows = np.random.default_rng(5).choice(1 << 20, 4096, replace=False)
+    ei, ed = oracle.knn_brute(p[0].numpy(), q[0].numpy()[rows], 16)
+    assert_same_int(ci[0].cpu().numpy()[rows], ei, "indices")
+    assert_same_f32(cd[0].cpu().numpy()[rows], ed, "distances")
+
+
+def test_explicit_accel_smaller_than_the_layout_is_rejected():
+    rng = np.random.default_rng(78)
+    p = dev(rng.random((2, 3000, 3), dtype=np.float32))
+    q = dev(rng.random((2, 100, 3), dtype=np.float32))
+    d = _C.build_bvh_batched_cooperative(p)
+    small = _C.build_bvh_batched_cooperative(p[:, :2000].contiguous(), with_accel=True)["accel"]
+    with pytest.raises(RuntimeError, match="need"):
+        _C.query_knn_batched_cached_bounds(d["node_aabbs"], d["sorted_indices"], q, d["num_leaves"],
+                                           d["num_real_nodes"], 3, 4, accel=small)

@@ -99,5 +99,23 @@ def test_morton_sort_points_matches_oracle(n, dim):
     assert order.shape == (3, n) and order.dtype == torch.int64
     got = order.cpu().numpy()
     for b in range(3):
-        assert_same_int(got[b], oracle.build(pts[b])["sorted_indices"], f"cloud {b}")
+        assert_same_int(got[b], oracle.morton_point_order(pts[b]), f"cloud {b}")
     assert torch.equal(order, _C.build_bvh_batched_cooperative(dev(pts))["sorted_indices"])
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_morton_sort_points_bounds_are_unseeded(dim):
+    """Clouds lying entirely beyond +-1e30 on one axis: the ordering's bounds
+    are the points' own min/max (so that axis still spreads over the Morton
+    grid), where the build's bounds stop at the 1e30 seed."""
+    rng = np.random.default_rng(900 + dim)
+    pts = rng.random((3, 5000, dim), dtype=np.float32)
+    pts[0, :, 0] = 2e30 + pts[0, :, 0] * 1e30
+    pts[1, :, dim - 1] = -(2e30 + pts[1, :, dim - 1] * 1e30)
+    got = _C.morton_sort_points_batched(dev(pts)).cpu().numpy()
+    built = _C.build_bvh_batched_cooperative(dev(pts))["sorted_indices"].cpu().numpy()
+    for b in range(3):
+        assert_same_int(got[b], oracle.morton_point_order(pts[b]), f"cloud {b}")
+        assert_same_int(built[b], oracle.build(pts[b])["sorted_indices"], f"cloud {b} (seeded build)")
+    assert not np.array_equal(got[0], built[0]) and not np.array_equal(got[1], built[1])
+    assert np.array_equal(got[2], built[2])

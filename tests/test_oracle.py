@@ -270,6 +270,44 @@ def test_bounds_match_numpy_and_seed_semantics():
     assert np.all(lo == np.float32(1e30)) and np.all(hi == np.float32(3e30))
 
 
+@pytest.mark.parametrize("dim", [2, 3])
+def test_point_order_equals_build_order_inside_the_seeds(dim):
+    """Within +-1e30 the plain min/max of the point ordering equals the
+    build's seeded bounds, so the two orders coincide."""
+    rng = np.random.default_rng(30 + dim)
+    for n in (1, 7, 5000):
+        p = (rng.standard_normal((n, dim)) * 10).astype(np.float32)
+        assert_same_int(oracle.morton_point_order(p), oracle.build(p)["sorted_indices"], f"n={n}")
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_point_order_spreads_clouds_beyond_the_seeds(dim):
+    """A cloud along axis 0 lying entirely above 1e30, other axes constant:
+    only axis 0 varies, so the codes order the points by their axis-0 cell
+    over the points' own extent [min, max]: the minimum lands in cell 0, the
+    maximum in the last cell, every cell step is at most one cell width of x,
+    and ties keep input order.  The build's bounds stop at the 1e30 seed,
+    which coarsens the cells and changes the order."""
+    rng = np.random.default_rng(40 + dim)
+    n = 4000
+    p = np.zeros((n, dim), np.float32)
+    p[:, 0] = (2e30 + rng.random(n) * 1e30).astype(np.float32)
+    order = oracle.morton_point_order(p)
+    x = p[order, 0].astype(np.float64)
+    width = (p[:, 0].max() - p[:, 0].min()) / (1024 if dim == 3 else 65536)
+    lo, hi = float(p[:, 0].min()), float(p[:, 0].max())
+    assert x[0] - lo <= width * 1.0001 and hi - x[-1] <= width * 1.0001  # first and last cells
+    assert np.all(np.diff(x) >= -width * 1.0001)
+    # Ties within a cell keep input order (cells well inside their bounds,
+    # so float64 rounding here cannot put a point in a neighbouring cell).
+    cells = (x - lo) / width
+    inner = np.abs(cells - np.round(cells)) > 1e-3
+    for c in np.unique(np.floor(cells[inner]))[:50]:
+        run = order[inner & (np.floor(cells) == c)]
+        assert np.all(np.diff(run) > 0)
+    assert not np.array_equal(order, oracle.build(p)["sorted_indices"])
+
+
 # ---------------------------------------------------------------------------
 # Build: reference invariants + brute-force subtree boxes
 # ---------------------------------------------------------------------------

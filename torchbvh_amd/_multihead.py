@@ -13,10 +13,10 @@ from __future__ import annotations
 import torch
 
 from ._constants import EXACT_DISTANCE_EPSILON, SUPPORTED_DIMS
-from ._handles import _temporary_bvh
+from ._handles import scoped_bvh
 from ._native import _C
 from ._query import _build_bvh_batched, _query_knn_batched
-from ._validation import _as_contiguous, _as_contiguous_int64, _validate_cuda_float32
+from ._validation import check_cuda_f32, dense, dense_offsets
 
 __all__ = ["query_displaced_knn", "gather_neighbor_values", "interpolate_displaced"]
 
@@ -39,8 +39,8 @@ def _check_displaced(pos: torch.Tensor, q: torch.Tensor, op: str) -> None:
     for ok, message in checks:
         if not ok:
             raise ValueError(f"{op}: {message}")
-    _validate_cuda_float32(op, pos, "pos")
-    _validate_cuda_float32(op, q, "q")
+    check_cuda_f32(op, pos, "pos")
+    check_cuda_f32(op, q, "q")
     if pos.device != q.device:
         raise ValueError(f"{op}: pos and q must be on the same device")
 
@@ -53,12 +53,12 @@ def query_displaced_knn(pos: torch.Tensor, q: torch.Tensor, k: int = 8, *,
     and, with ``return_positions``, the neighbours' coordinates
     ``(B, N, H, k, D)``."""
     _check_displaced(pos, q, "query_displaced_knn")
-    pos = _as_contiguous(pos)
-    q = _as_contiguous(q)
+    pos = dense(pos)
+    q = dense(q)
     B, N, H, D = q.shape
     queries = q.reshape(B, N * H, D).contiguous()
     sources = pos.detach().contiguous()
-    with _temporary_bvh(_build_bvh_batched, sources) as bvh:
+    with scoped_bvh(_build_bvh_batched, sources) as bvh:
         out = _query_knn_batched(bvh, queries, k,
                                  source_points=sources if return_positions else None,
                                  sort_queries=True)
@@ -79,13 +79,13 @@ def gather_neighbor_values(values: torch.Tensor, indices: torch.Tensor) -> torch
             raise ValueError(f"{op}: indices {what} must match values")
     if values.size(3) < 1:
         raise ValueError(f"{op}: values must have at least one channel")
-    _validate_cuda_float32(op, values, "values")
+    check_cuda_f32(op, values, "values")
     if indices.dtype != torch.int64:
         raise ValueError(f"{op}: indices must be int64")
     if values.device != indices.device:
         raise ValueError(f"{op}: values and indices must be on the same device")
-    values = _as_contiguous(values)
-    indices = _as_contiguous_int64(indices)
+    values = dense(values)
+    indices = dense_offsets(indices)
     if indices.numel() > 0:
         lo, hi = torch.aminmax(indices)
         if int(lo) < 0 or int(hi) >= values.size(1):
@@ -114,11 +114,11 @@ def interpolate_displaced(pos: torch.Tensor, q: torch.Tensor, values: torch.Tens
         raise ValueError(f"{op}: values head dimension must match q")
     if values.size(3) < 1:
         raise ValueError(f"{op}: values must have at least one channel")
-    _validate_cuda_float32(op, values, "values")
+    check_cuda_f32(op, values, "values")
     if values.device != pos.device:
         raise ValueError(f"{op}: values must be on the same device as pos")
-    values = _as_contiguous(values)
-    indices, d2 = query_displaced_knn(_as_contiguous(pos), _as_contiguous(q), k, return_positions=False)
+    values = dense(values)
+    indices, d2 = query_displaced_knn(dense(pos), dense(q), k, return_positions=False)
     eps = EXACT_DISTANCE_EPSILON
     exact = d2 <= eps
     weights = torch.reciprocal(d2 + eps)

@@ -89,6 +89,7 @@ def _declare(L) -> None:
     L.tbvh_accel_size.argtypes = [_i64, _i64, _int, _szp]
     L.tbvh_accel_workspace_size.argtypes = [_i64, _i64, _int, _szp]
     L.tbvh_accel_build.argtypes = [_vp] * 5 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
+    L.tbvh_accel_build_from_tree.argtypes = [_vp, _vp, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_accel_build_ragged.argtypes = (
         [_vp] * 6 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
     )
@@ -118,7 +119,7 @@ def _declare(L) -> None:
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
         "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
         "tbvh_morton_sort_points_workspace_size", "tbvh_morton_sort_points",
-        "tbvh_interpolate_neighbors", "tbvh_build_with_accel_noalloc",
+        "tbvh_interpolate_neighbors", "tbvh_build_with_accel_noalloc", "tbvh_accel_build_from_tree",
     ):
         getattr(L, name).restype = _int
 
@@ -216,8 +217,11 @@ MAX_ACCEL_CLOUD = 1 << 28
 # of all their elements: same data pointer while they are alive), unmodified
 # since (torch's version counters, which views share), traverses the accel
 # instead of the implicit tree - identical results, about 10x fewer node
-# visits.  accel=False forces the implicit tree.  Entries go when the
-# registered node_aabbs is freed.
+# visits.  Tensors it does not know (a clone, a copy, a reload) get an accel
+# built on the spot from node_aabbs and sorted_indices alone
+# (tbvh_accel_build_from_tree: the same bytes the build would have written)
+# and registered under them.  accel=False forces the implicit tree.  Entries
+# go when the registered node_aabbs is freed.
 # ---------------------------------------------------------------------------
 _accel_registry: dict[int, tuple] = {}
 
@@ -281,13 +285,49 @@ def _with_positions(indices, distances, positions, source_points):
     return indices, distances, positions
 
 
-def _pick_accel(accel, node_aabbs: torch.Tensor, sorted_indices: torch.Tensor):
-    """accel argument of the k-NN bindings: a tensor is used, False forces
-    the implicit tree, None looks up the registry."""
+def _check_accel(op: str, accel, clouds: int, total_points: int, dim: int, device: torch.device) -> None:
+    """An accel tensor handed in by the caller must be a contiguous 1-D
+    uint8 tensor on the queries' device, at least as large as the layout for
+    these clouds: the traversal then never reads outside it (it also
+    bounds-checks every child ref and parent link against its cloud)."""
+    _require(isinstance(accel, torch.Tensor) and accel.dtype == torch.uint8 and accel.dim() == 1
+             and accel.is_contiguous(), op, "accel must be a contiguous 1-D uint8 tensor")
+    _require(accel.is_cuda and accel.device == device, op, "accel must be on the queries' device")
+    need = _size(load().tbvh_accel_size, clouds, total_points, dim)
+    _require(accel.numel() >= need, op,
+             f"accel holds {accel.numel()} bytes; {clouds} cloud(s) of {total_points} points in total "
+             f"need {need}")
+
+
+def _accel_from_tree(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, dim: int):
+    """Build, register and return the accel of a batched BVH known only by its
+    node_aabbs [B, nr, 2D] and sorted_indices [B, N]; None when a cloud is
+    too large for one."""
+    B, N = int(sorted_indices.size(0)), int(sorted_indices.size(1))
+    if N > MAX_ACCEL_CLOUD:
+        return None
+    L = load()
+    dev = node_aabbs.device
+    with torch.cuda.device(dev):
+        accel = torch.empty(_size(L.tbvh_accel_size, B, B * N, dim), dtype=torch.uint8, device=dev)
+        ws = _workspace(_size(L.tbvh_accel_workspace_size, B, B * N, dim), dev)
+        _check(L.tbvh_accel_build_from_tree(_ptr(node_aabbs), _ptr(sorted_indices), B, N, int(dim),
+                                            _ptr(accel), _ptr(ws), ws.numel(), _stream(dev)))
+    _register_accel(node_aabbs, sorted_indices, accel)
+    return accel
+
+
+def _pick_accel(op: str, accel, node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, dim: int):
+    """accel argument of the batched k-NN bindings (inputs already checked):
+    False forces the implicit tree; a tensor is checked and used; None takes
+    the registered accel of these tensors, or builds one from them."""
     if accel is False:
         return None
+    B, N = int(sorted_indices.size(0)), int(sorted_indices.size(1))
     if accel is None:
-        return _registered_accel(node_aabbs, sorted_indices)
+        found = _registered_accel(node_aabbs, sorted_indices)
+        return found if found is not None else _accel_from_tree(node_aabbs, sorted_indices, dim)
+    _check_accel(op, accel, B, B * N, dim, sorted_indices.device)
     return accel
 
 
@@ -624,7 +664,7 @@ class _NativeOps:
         dev = query_points.device
         for t in (node_aabbs, sorted_indices) + ((query_order,) if query_order is not None else ()):
             _require(t.device == dev, op, "all inputs must share a device")
-        accel = _pick_accel(accel, node_aabbs, sorted_indices)
+        accel = _pick_accel(op, accel, node_aabbs, sorted_indices, int(dim))
         B, M = int(query_points.size(0)), int(query_points.size(1))
         indices = torch.empty((B, M, k), dtype=torch.int64, device=dev)
         distances = torch.empty((B, M, k), dtype=torch.float32, device=dev)
@@ -638,13 +678,11 @@ class _NativeOps:
         L = load()
         with torch.cuda.device(dev):
             if fused:
-                _require(accel.is_cuda and accel.device == dev, op, "accel must be on the queries' device")
                 _check(L.tbvh_knn_accel_positions(
                     _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
                     int(dim), int(k), _ptr(source_points), C, _ptr(indices), _ptr(distances),
                     _ptr(positions), _stream(dev)))
             elif accel is not None:
-                _require(accel.is_cuda and accel.device == dev, op, "accel must be on the queries' device")
                 fn = L.tbvh_knn_accel_spatial if spatial else L.tbvh_knn_accel
                 _check(fn(
                     _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
@@ -763,8 +801,8 @@ class _NativeOps:
         distances = torch.empty((B, M, k), dtype=torch.float32, device=dev)
         if M == 0:
             return indices, distances
-        true_accel = _pick_accel(true_accel, true_node_aabbs, true_sorted_indices)
-        false_accel = _pick_accel(false_accel, false_node_aabbs, false_sorted_indices)
+        true_accel = _pick_accel(op, true_accel, true_node_aabbs, true_sorted_indices, int(dim))
+        false_accel = _pick_accel(op, false_accel, false_node_aabbs, false_sorted_indices, int(dim))
         L = load()
         with torch.cuda.device(dev):
             if true_accel is not None and false_accel is not None:
@@ -796,6 +834,9 @@ class _NativeOps:
             _require_device_i64(op, t, name)
         T = int(query_points.size(0))
         dev = query_points.device
+        if accel is not None:
+            _require(total_points is not None, op, "total_points is required with an accel")
+            _check_accel(op, accel, int(batch_size), int(total_points), int(dim), dev)
         indices = torch.empty((T, k), dtype=torch.int64, device=dev)
         distances = torch.empty((T, k), dtype=torch.float32, device=dev)
         # Neighbour rows (packed like the points; indices are cloud-local):

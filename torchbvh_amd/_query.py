@@ -15,23 +15,9 @@ from collections.abc import Mapping
 import torch
 
 from ._constants import SUPPORTED_DIMS
-from ._handles import (
-    BVHHandle,
-    BatchedBVHHandle,
-    RaggedBVHHandle,
-    _batched_bvh_data,
-    _bvh_data,
-    _ragged_bvh_data,
-)
+from ._handles import BVHHandle, BatchedBVHHandle, RaggedBVHHandle, live_payload
 from ._native import _C
-from ._validation import (
-    _as_contiguous,
-    _as_contiguous_int64,
-    _validate_cuda_float32,
-    _validate_offsets,
-    _validate_ragged_points,
-    _validate_supported_k,
-)
+from ._validation import check_cuda_f32, check_k, check_offsets, check_ragged_points, dense, dense_offsets
 
 _INT32_MAX = 2**31 - 1
 
@@ -50,11 +36,11 @@ def _build_bvh_single(points: torch.Tensor) -> BVHHandle:
         raise ValueError("build_bvh: points must have shape (N, D)")
     if points.size(1) not in SUPPORTED_DIMS:
         raise ValueError("build_bvh: D must be 2 or 3")
-    _validate_cuda_float32("build_bvh", points, "points")
+    check_cuda_f32("build_bvh", points, "points")
     # Sizes only, before any copy (an expanded view is rejected without
     # materialising it).
     _validate_narrow_build_extent("build_bvh", points)
-    points = _as_contiguous(points)
+    points = dense(points)
     batched = points.unsqueeze(0)
     data = _C.build_bvh_batched_cooperative(batched, with_accel=True)
     accel = data.pop("accel")
@@ -70,20 +56,20 @@ def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
         raise ValueError("build_bvh: batched points must have shape (B, N, D)")
     if points.size(2) not in SUPPORTED_DIMS:
         raise ValueError("build_bvh: D must be 2 or 3")
-    _validate_cuda_float32("build_bvh", points, "points")
+    check_cuda_f32("build_bvh", points, "points")
     # Sizes only, before any copy (an expanded view is rejected without
     # materialising it).
     _validate_narrow_build_extent("build_bvh", points)
-    points = _as_contiguous(points)
+    points = dense(points)
     data = _C.build_bvh_batched_cooperative(points, with_accel=True)
     accel = data.pop("accel")
     return BatchedBVHHandle(data, aux={"accel": accel})
 
 
 def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> RaggedBVHHandle:
-    points = _as_contiguous(points)
-    batch_offsets = _as_contiguous_int64(batch_offsets)
-    offsets = _validate_ragged_points("build_bvh", points, batch_offsets)
+    points = dense(points)
+    batch_offsets = dense_offsets(batch_offsets)
+    offsets = check_ragged_points("build_bvh", points, batch_offsets)
     _validate_narrow_build_extent("build_bvh", points)
     counts = [b - a for a, b in zip(offsets, offsets[1:])]
     packed = _C.build_bvh_ragged(points, batch_offsets, counts, with_accel=True)
@@ -175,23 +161,23 @@ def _query_knn_single(
     source_points: torch.Tensor | None = None,
     sort_queries: bool = True,
 ):
-    _validate_supported_k("query_knn", k)
-    data = _bvh_data(bvh, "query_knn")
+    check_k("query_knn", k)
+    data = live_payload(bvh, BVHHandle, "query_knn")
     if query_points.dim() != 2:
         raise ValueError("query_knn: query_points must have shape (M, D)")
     if query_points.size(1) != data["dim"]:
         raise ValueError("query_knn: query_points second dimension must match BVH dim")
-    _validate_cuda_float32("query_knn", query_points, "query_points")
+    check_cuda_f32("query_knn", query_points, "query_points")
     if query_points.device != data["sorted_indices"].device:
         raise ValueError("query_knn: query_points must be on the same device as the BVH")
-    queries = _as_contiguous(query_points).unsqueeze(0)
+    queries = dense(query_points).unsqueeze(0)
     node_aabbs = data["node_aabbs"].unsqueeze(0)
     sorted_indices = data["sorted_indices"].unsqueeze(0)
     accel = bvh._aux.get("accel")
     src = None
     if source_points is not None:
         _validate_single_source_points("query_knn", data, source_points)
-        src = _as_contiguous(source_points).unsqueeze(0)
+        src = dense(source_points).unsqueeze(0)
     if _schedule(sort_queries, int(queries.size(1))):
         order = _C.morton_sort_queries_narrow(
             queries, data["scene_min"].unsqueeze(0), data["scene_max"].unsqueeze(0), schedule=True
@@ -215,7 +201,7 @@ def _validate_single_source_points(prefix: str, data: Mapping, source_points: to
         raise ValueError(f"{prefix}: source_points first dimension must match BVH num_leaves")
     if source_points.size(1) != data["dim"]:
         raise ValueError(f"{prefix}: source_points second dimension must match BVH dim")
-    _validate_cuda_float32(prefix, source_points, "source_points")
+    check_cuda_f32(prefix, source_points, "source_points")
     if source_points.device != data["sorted_indices"].device:
         raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
 
@@ -229,7 +215,7 @@ def _validate_batched_source_points(prefix: str, data: Mapping, source_points: t
         raise ValueError(f"{prefix}: source_points second dimension must match BVH num_leaves")
     if source_points.size(2) != data["dim"]:
         raise ValueError(f"{prefix}: source_points last dimension must match BVH dim")
-    _validate_cuda_float32(prefix, source_points, "source_points")
+    check_cuda_f32(prefix, source_points, "source_points")
     if source_points.device != data["sorted_indices"].device:
         raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
 
@@ -242,23 +228,23 @@ def _query_knn_batched(
     source_points: torch.Tensor | None = None,
     sort_queries: bool = True,
 ):
-    _validate_supported_k("query_knn", k)
-    data = _batched_bvh_data(bvh, "query_knn")
+    check_k("query_knn", k)
+    data = live_payload(bvh, BatchedBVHHandle, "query_knn")
     if query_points.dim() != 3:
         raise ValueError("query_knn: batched query_points must have shape (B, M, D)")
     if query_points.size(0) != data["batch_size"]:
         raise ValueError("query_knn: query_points batch size must match BVH batch_size")
     if query_points.size(2) != data["dim"]:
         raise ValueError("query_knn: query_points last dimension must match BVH dim")
-    _validate_cuda_float32("query_knn", query_points, "query_points")
+    check_cuda_f32("query_knn", query_points, "query_points")
     if query_points.device != data["sorted_indices"].device:
         raise ValueError("query_knn: query_points must be on the same device as the BVH")
-    queries = _as_contiguous(query_points)
+    queries = dense(query_points)
     accel = bvh._aux.get("accel")
     src = None
     if source_points is not None:
         _validate_batched_source_points("query_knn", data, source_points)
-        src = _as_contiguous(source_points)
+        src = dense(source_points)
     if _schedule(sort_queries, int(queries.size(0) * queries.size(1))):
         order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"],
                                               schedule=True)
@@ -279,7 +265,7 @@ def _validate_ragged_source_points(prefix, data, source_points, *, total_rows, d
         raise ValueError(f"{prefix}: source_points first dimension must match BVH total_N")
     if source_points.size(1) != data["dim"]:
         raise ValueError(f"{prefix}: source_points second dimension must match BVH dim")
-    _validate_cuda_float32(prefix, source_points, "source_points")
+    check_cuda_f32(prefix, source_points, "source_points")
     if source_points.device != device:
         raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
 
@@ -292,18 +278,18 @@ def _query_knn_ragged(
     *,
     source_points: torch.Tensor | None = None,
 ):
-    _validate_supported_k("query_knn", k)
-    data, _handles = _ragged_bvh_data(bvh, "query_knn")
+    check_k("query_knn", k)
+    data = live_payload(bvh, RaggedBVHHandle, "query_knn")
     if query_points.dim() != 2:
         raise ValueError("query_knn: ragged query_points must have shape (total_M, D)")
     if query_points.size(1) != data["dim"]:
         raise ValueError("query_knn: query_points second dimension must match BVH dim")
-    _validate_cuda_float32("query_knn", query_points, "query_points")
+    check_cuda_f32("query_knn", query_points, "query_points")
     if query_points.device != data["batch_offsets"].device:
         raise ValueError("query_knn: query_points must be on the same device as the BVH")
-    queries = _as_contiguous(query_points)
-    query_offsets = _as_contiguous_int64(query_offsets)
-    q_offsets = _validate_offsets(
+    queries = dense(query_points)
+    query_offsets = dense_offsets(query_offsets)
+    q_offsets = check_offsets(
         "query_knn", query_offsets, total_rows=int(queries.size(0)), device=queries.device
     )
     if len(q_offsets) - 1 != data["batch_size"]:
@@ -315,7 +301,7 @@ def _query_knn_ragged(
         _validate_ragged_source_points(
             "query_knn", data, source_points, total_rows=p_offsets[-1], device=queries.device
         )
-        source_points = _as_contiguous(source_points)
+        source_points = dense(source_points)
 
     packed = bvh._aux["packed"]
     order = None

@@ -1,79 +1,97 @@
-"""Argument validation with the reference's error types and messages
-(torchbvh/_validation.py:1-75); tests match these messages by regex."""
+"""Argument checks of the public API.
+
+What a caller can observe is the drop-in contract: the exception type
+(ValueError), each message and the order in which the checks run (the
+reference's tests match the messages by regex; they are defined in
+torchbvh/_validation.py:1-75).  Here the checks are data: ordered tables of
+(predicate, message) rules, walked by one function, so each table reads as
+the specification of one argument.
+"""
 
 from __future__ import annotations
+
+from collections.abc import Callable, Sequence
 
 import torch
 
 from ._constants import SUPPORTED_DIMS, SUPPORTED_K
 
-_K_MESSAGE = ", ".join(str(k) for k in SUPPORTED_K[:-1]) + f", or {SUPPORTED_K[-1]}"
+# The reference's wording ("k must be 4, 8, or 16", which its tests match)
+# stays a prefix of the message, and the one extension is named after it.
+K_MESSAGE = "k must be 4, 8, or 16 (32 is also supported)"
+
+Rule = tuple[Callable[..., bool], str]
 
 
-def _validate_supported_k(prefix: str, k: int) -> None:
+def _walk(prefix: str, rules: Sequence[Rule], *subject, **names) -> None:
+    """Raise ValueError for the first rule whose predicate fails."""
+    for holds, message in rules:
+        if not holds(*subject):
+            raise ValueError(f"{prefix}: {message.format(**names)}")
+
+
+# A float32 point/query tensor on the GPU; contiguity is a separate rule
+# because most entry points copy non-contiguous input instead of rejecting it.
+_CUDA_F32: Sequence[Rule] = (
+    (lambda t: t.is_cuda, "{name} must be a CUDA tensor"),
+    (lambda t: t.dtype == torch.float32, "{name} must be float32"),
+)
+_CONTIGUOUS: Sequence[Rule] = ((lambda t: t.is_contiguous(), "{name} must be contiguous"),)
+
+# Ragged offsets: first the tensor (shape, dtype, placement), then, read back
+# to the host once, the values.
+_OFFSETS_TENSOR: Sequence[Rule] = (
+    (lambda t, dev: t.dim() == 1, "offsets must have shape (B + 1,)"),
+    (lambda t, dev: t.numel() >= 2, "offsets must contain at least two entries"),
+    (lambda t, dev: t.dtype == torch.int64, "offsets must be int64"),
+    (lambda t, dev: t.is_cuda, "offsets must be a CUDA tensor"),
+    (lambda t, dev: t.is_contiguous(), "offsets must be contiguous"),
+    (lambda t, dev: t.device == dev, "offsets must be on the same device as the packed tensor"),
+)
+_OFFSETS_VALUES: Sequence[Rule] = (
+    (lambda v, total: v[0] == 0, "offsets must start at 0"),
+    (lambda v, total: v[-1] == total, "final offset must match the packed tensor length"),
+    (lambda v, total: all(b > a for a, b in zip(v, v[1:])), "offsets must be strictly increasing"),
+)
+
+# Packed ragged points (before their offsets).
+_RAGGED_POINTS: Sequence[Rule] = (
+    (lambda t: t.dim() == 2, "points must have shape (total_N, D)"),
+    (lambda t: t.size(1) in SUPPORTED_DIMS, "D must be 2 or 3"),
+    *_CUDA_F32,
+    *_CONTIGUOUS,
+)
+
+
+def check_k(prefix: str, k: int) -> None:
     if k not in SUPPORTED_K:
-        raise ValueError(f"{prefix}: k must be {_K_MESSAGE}")
+        raise ValueError(f"{prefix}: {K_MESSAGE}")
 
 
-def _as_contiguous(tensor: torch.Tensor) -> torch.Tensor:
-    return tensor if tensor.is_contiguous() else tensor.contiguous()
+def check_cuda_f32(prefix: str, tensor: torch.Tensor, name: str) -> None:
+    _walk(prefix, _CUDA_F32, tensor, name=name)
 
 
-def _as_contiguous_int64(tensor: torch.Tensor) -> torch.Tensor:
-    # Non-int64 offsets pass through untouched so validation reports the dtype.
-    if tensor.dtype != torch.int64:
-        return tensor
-    return _as_contiguous(tensor)
-
-
-def _validate_cuda_float32(prefix: str, tensor: torch.Tensor, name: str) -> None:
-    if not tensor.is_cuda:
-        raise ValueError(f"{prefix}: {name} must be a CUDA tensor")
-    if tensor.dtype != torch.float32:
-        raise ValueError(f"{prefix}: {name} must be float32")
-
-
-def _validate_cuda_float32_contiguous(prefix: str, tensor: torch.Tensor, name: str) -> None:
-    _validate_cuda_float32(prefix, tensor, name)
-    if not tensor.is_contiguous():
-        raise ValueError(f"{prefix}: {name} must be contiguous")
-
-
-def _validate_offsets(
-    prefix: str,
-    offsets: torch.Tensor,
-    *,
-    total_rows: int,
-    device: torch.device,
-) -> list[int]:
-    """Check a (B + 1,) int64 offsets tensor and return it as host ints (one
-    device-to-host read, as in the reference)."""
-    if offsets.dim() != 1:
-        raise ValueError(f"{prefix}: offsets must have shape (B + 1,)")
-    if offsets.numel() < 2:
-        raise ValueError(f"{prefix}: offsets must contain at least two entries")
-    if offsets.dtype != torch.int64:
-        raise ValueError(f"{prefix}: offsets must be int64")
-    if not offsets.is_cuda:
-        raise ValueError(f"{prefix}: offsets must be a CUDA tensor")
-    if not offsets.is_contiguous():
-        raise ValueError(f"{prefix}: offsets must be contiguous")
-    if offsets.device != device:
-        raise ValueError(f"{prefix}: offsets must be on the same device as the packed tensor")
+def check_offsets(prefix: str, offsets: torch.Tensor, *, total_rows: int, device: torch.device) -> list[int]:
+    """Validate a (B + 1,) int64 offsets tensor and return its values as host
+    ints (one device-to-host read)."""
+    _walk(prefix, _OFFSETS_TENSOR, offsets, device)
     values = [int(v) for v in offsets.detach().cpu().tolist()]
-    if values[0] != 0:
-        raise ValueError(f"{prefix}: offsets must start at 0")
-    if values[-1] != total_rows:
-        raise ValueError(f"{prefix}: final offset must match the packed tensor length")
-    if any(b <= a for a, b in zip(values, values[1:])):
-        raise ValueError(f"{prefix}: offsets must be strictly increasing")
+    _walk(prefix, _OFFSETS_VALUES, values, total_rows)
     return values
 
 
-def _validate_ragged_points(prefix: str, points: torch.Tensor, offsets: torch.Tensor) -> list[int]:
-    if points.dim() != 2:
-        raise ValueError(f"{prefix}: points must have shape (total_N, D)")
-    if points.size(1) not in SUPPORTED_DIMS:
-        raise ValueError(f"{prefix}: D must be 2 or 3")
-    _validate_cuda_float32_contiguous(prefix, points, "points")
-    return _validate_offsets(prefix, offsets, total_rows=int(points.size(0)), device=points.device)
+def check_ragged_points(prefix: str, points: torch.Tensor, offsets: torch.Tensor) -> list[int]:
+    _walk(prefix, _RAGGED_POINTS, points, name="points")
+    return check_offsets(prefix, offsets, total_rows=int(points.size(0)), device=points.device)
+
+
+def dense(tensor: torch.Tensor) -> torch.Tensor:
+    """The tensor itself when contiguous, else a contiguous copy."""
+    return tensor.contiguous()
+
+
+def dense_offsets(offsets: torch.Tensor) -> torch.Tensor:
+    """Like `dense` for int64 offsets; other dtypes pass through unchanged so
+    that check_offsets reports the dtype rather than a copy's."""
+    return offsets.contiguous() if offsets.dtype == torch.int64 else offsets

@@ -71,6 +71,42 @@ __global__ __launch_bounds__(kBlock) void accel_points_kernel(
     leaf_points[r] = v;
 }
 
+// Standalone pass 1 from a finished implicit tree alone (no points, no
+// bounds): leaf j of a cloud's tree is the degenerate box of its j-th point
+// in Morton order, so the leaf rows give the Morton-ordered points, and the
+// build's bounds follow exactly from the root box, which is the min / max
+// over the same points: the build seeds its min at +1e30 and its max at
+// -1e30 (bvh_build.cu:466-467), so scene_min = fminf(+1e30, root lo) and
+// scene_max = fmaxf(-1e30, root hi).  The codes, and so the radix tree and
+// every accel byte, are then the build's own.
+template <int D>
+__global__ __launch_bounds__(kBlock) void accel_points_from_tree_kernel(
+    const float* __restrict__ node_aabbs, const int64_t* __restrict__ sorted, const Segment* __restrict__ segs,
+    int S, int64_t total, float4* __restrict__ leaf_points, uint32_t* __restrict__ codes) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (r >= total) return;
+    const int s = find_segment([&](int i) { return segs[i].start; }, S, r);
+    const Segment g = segs[s];
+    const int j = static_cast<int>(r - g.start);
+    const float* nodes = node_aabbs + g.node_start * 2 * D;
+    const int64_t row = tree::memory_index(g.vl, g.leaf_level, tree::level_first(g.leaf_level) + j);
+    float p[D], lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        p[d] = nodes[row * 2 * D + d];
+        lo[d] = fminf(kSeedLo, nodes[d]);
+        hi[d] = fmaxf(kSeedHi, nodes[D + d]);
+    }
+    codes[r] = morton::encode<D>(p, lo, hi);
+    const int64_t idx = min(max(sorted[r], int64_t(0)), int64_t(g.n - 1));
+    float4 v;
+    v.x = p[0];
+    v.y = p[1];
+    v.z = D == 3 ? p[D - 1] : 0.0f;
+    v.w = __int_as_float(static_cast<int>(idx));
+    leaf_points[r] = v;
+}
+
 // Standalone pass 2: radix-tree internal nodes (Karras 2012, section 4), one
 // thread per node; nodes inside a bucket are not referenced and write nothing.  The
 // block first stages the sorted codes around its nodes in LDS (most nodes
@@ -228,6 +264,21 @@ hipError_t launch_accel_points(const float* points, const int64_t* sorted, const
     } else {
         accel_points_kernel<2><<<grid_for(total), kBlock, 0, stream>>>(
             points, sorted, segs, Si, total, scene_min, scene_max, leaf_points, codes);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_accel_points_from_tree(const float* node_aabbs, const int64_t* sorted, int D,
+                                         const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
+                                         void* accel, hipStream_t stream) {
+    float4* leaf_points = static_cast<float4*>(accel);
+    const int Si = static_cast<int>(S);
+    if (D == 3) {
+        accel_points_from_tree_kernel<3><<<grid_for(total), kBlock, 0, stream>>>(node_aabbs, sorted, segs, Si, total,
+                                                                                 leaf_points, codes);
+    } else {
+        accel_points_from_tree_kernel<2><<<grid_for(total), kBlock, 0, stream>>>(node_aabbs, sorted, segs, Si, total,
+                                                                                 leaf_points, codes);
     }
     return hipGetLastError();
 }

@@ -170,6 +170,7 @@ constexpr int kTileRows = kSortTile / kTileThreads;
 template <int D>
 __global__ __launch_bounds__(kTileThreads) void bounds_kernel(const float* __restrict__ points,
                                                               const Segment* __restrict__ segs, int S,
+                                                              float seed_lo, float seed_hi,
                                                               float* __restrict__ partials) {
     __shared__ int s_seg;
     __shared__ float s_red[kTileThreads / kWave][2 * D];
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(kTileThreads) void bounds_kernel(const float* __res
     }
     float lo[D], hi[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d) { lo[d] = kSeedLo; hi[d] = kSeedHi; }
+    for (int d = 0; d < D; ++d) { lo[d] = seed_lo; hi[d] = seed_hi; }
 #pragma unroll
     for (int i = 0; i < kTileRows; ++i) {
         if (i * kTileThreads + static_cast<int>(threadIdx.x) < count) {
@@ -581,20 +582,20 @@ hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S,
 
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles, float* partials, float* scene_min, float* scene_max,
-                         bool finalize, hipStream_t stream) {
+                         bool finalize, float seed_lo, float seed_hi, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const unsigned cgrid = static_cast<unsigned>(S);
     const int Si = static_cast<int>(S);
     if (D == 3) {
-        bounds_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, partials);
+        bounds_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, seed_lo, seed_hi, partials);
         if (finalize) {
-            bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi, scene_min,
+            bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, seed_lo, seed_hi, scene_min,
                                                                  scene_max);
         }
     } else {
-        bounds_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, partials);
+        bounds_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, seed_lo, seed_hi, partials);
         if (finalize) {
-            bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, kSeedLo, kSeedHi, scene_min,
+            bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, seed_lo, seed_hi, scene_min,
                                                                  scene_max);
         }
     }

@@ -167,11 +167,17 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
     // than kFuseBoundsTiles tiles (ragged: bounded by all rows).
     const int64_t cloud_bound = ragged ? rows : n_uniform;
     const bool fuse = (cloud_bound + kSortTile - 1) / kSortTile <= kFuseBoundsTiles;
+    // The point build seeds its bounds at +-1e30 (bvh_build.cu:466-467);
+    // the primitive build (the boxes' min/max, bvh_build.cu:60-93) and the
+    // point ordering (points.min(1) / max(1), bvh_build.cu:731-732) do not.
+    const bool seeded = V == 0 && !o.sort_only;
+    const float seed_lo = seeded ? kSeedLo : INFINITY;
+    const float seed_hi = seeded ? kSeedHi : -INFINITY;
     BoundsFinish fin;
     if (fuse) {
         fin.partials = partials;
-        fin.seed_lo = V > 0 ? INFINITY : kSeedLo;
-        fin.seed_hi = V > 0 ? -INFINITY : kSeedHi;
+        fin.seed_lo = seed_lo;
+        fin.seed_hi = seed_hi;
     }
     if (V > 0) {
         float* centers = carve<float>(ws, l.centers);
@@ -183,7 +189,7 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
         points = centers;
         boxes = leaf_boxes;
     } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max, !fuse,
-                                  stream)) != hipSuccess) {
+                                  seed_lo, seed_hi, stream)) != hipSuccess) {
         return e;
     }
     const SortBits bits = full_sort(D);
@@ -724,7 +730,7 @@ static int knn_batched(const char* op, const float* node_aabbs, const int64_t* s
                        int64_t num_leaves, int64_t num_real_nodes, int D, int k, bool spatial,
                        int64_t* out_indices, float* out_distances, void* stream_ptr) {
     if (int r = check_dim(op, D)) return r;
-    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, or 16 (32 is also supported), got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
     if (num_leaves < 1 || num_leaves > kMaxCloud) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_leaves must be in [1, 2^30]", op);
@@ -780,7 +786,7 @@ int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
                     float* out_distances, void* stream_ptr) {
     const char* op = "tbvh_knn_ragged";
     if (int r = check_dim(op, D)) return r;
-    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, or 16 (32 is also supported), got %d", op, k);
     if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
     if (total_q > kMaxRows) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
     if (total_q == 0) return ok();
@@ -863,6 +869,29 @@ int tbvh_accel_build(const float* points, const int64_t* sorted_indices, const f
     return ok();
 }
 
+int tbvh_accel_build_from_tree(const float* node_aabbs, const int64_t* sorted_indices, int64_t B, int64_t N,
+                               int D, void* accel, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+    const char* op = "tbvh_accel_build_from_tree";
+    if (int r = check_dim(op, D)) return r;
+    if (int r = check_batched_extent(op, B, N)) return r;
+    if (N > kMaxAccelCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: clouds may hold at most 2^28 points", op);
+    if (!node_aabbs || !sorted_indices || !accel) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    const int64_t total = B * N;
+    if (int r = check_workspace(op, workspace, workspace_bytes, accel_workspace_bytes(B, total))) return r;
+    if (reinterpret_cast<uintptr_t>(accel) % kAlign != 0) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    Segment* segs = carve<Segment>(workspace, 0);
+    uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
+    TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
+    TBVH_TRY(op, launch_accel_points_from_tree(node_aabbs, sorted_indices, D, segs, B, total, codes, accel, stream));
+    TBVH_TRY(op, launch_accel_nodes(node_aabbs, D, segs, B, total, codes, accel, stream));
+    return ok();
+}
+
 int tbvh_accel_build_ragged(const float* points, const int64_t* offsets, const int64_t* sorted_indices,
                             const float* node_aabbs, const float* scene_min, const float* scene_max,
                             int64_t B, int64_t total, int D, void* accel, void* workspace,
@@ -892,7 +921,7 @@ static int knn_accel_batched(const char* op, const void* accel, const float* que
                              void* stream_ptr, const float* source_points = nullptr, int source_cols = 0,
                              float* out_positions = nullptr) {
     if (int r = check_dim(op, D)) return r;
-    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, or 16 (32 is also supported), got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
     if (num_leaves < 1 || num_leaves > kMaxAccelCloud) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_leaves must be in [1, 2^28]", op);
@@ -943,7 +972,7 @@ static int knn_accel_ragged(const char* op, const void* accel, const int64_t* po
                             int64_t* out_indices, float* out_distances, void* stream_ptr,
                             const float* source_points, int source_cols, float* out_positions) {
     if (int r = check_dim(op, D)) return r;
-    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, or 16 (32 is also supported), got %d", op, k);
     if (B < 1 || total_q < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and total_q >= 0", op);
     if (total_q > kMaxRows || total_points > kMaxRows || total_points < B) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: counts must fit in signed int32 (and total_points >= B)", op);
@@ -1015,7 +1044,7 @@ int tbvh_knn_accel_ragged_positions(const void* accel, const int64_t* point_offs
 static int check_routed(const char* op, int64_t B, int64_t M, int64_t true_n, int64_t false_n, int64_t max_n,
                         int D, int k) {
     if (int r = check_dim(op, D)) return r;
-    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16, or 32, got %d", op, k);
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, or 16 (32 is also supported), got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
     if (true_n < 1 || true_n > max_n || false_n < 1 || false_n > max_n) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: leaf counts out of range", op);

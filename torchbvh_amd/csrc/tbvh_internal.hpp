@@ -124,7 +124,7 @@ hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S,
 // given the same partials in a BoundsFinish).
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles_bound, float* partials, float* scene_min, float* scene_max,
-                         bool finalize, hipStream_t stream);
+                         bool finalize, float seed_lo, float seed_hi, hipStream_t stream);
 
 // Clouds of at most this many tiles get their bounds reduced inside the
 // Morton kernel (each of a cloud's work-groups reads all its partial boxes,
@@ -220,6 +220,11 @@ size_t accel_bytes(int64_t total, int64_t S, int D);
 hipError_t launch_accel_points(const float* points, const int64_t* sorted, const float* scene_min,
                                const float* scene_max, int D, const Segment* segs, int64_t S,
                                int64_t total, uint32_t* codes, void* accel, hipStream_t stream);
+// Accel points + codes from a finished implicit tree alone (its leaf rows
+// and root box), identical to launch_accel_points' for the same build.
+hipError_t launch_accel_points_from_tree(const float* node_aabbs, const int64_t* sorted, int D,
+                                         const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
+                                         void* accel, hipStream_t stream);
 // Records of the nodes the fused first tree pass listed (after all tree
 // passes: their boxes need the upper levels).  `groups_bound` bounds the
 // first pass's work-group count.
