@@ -115,7 +115,16 @@ def build_bytes(n: int, D: int) -> int:
 
 
 def qsort_bytes(q: int, D: int) -> int:
+    """Full Morton sort of the queries (the reference binding): read the
+    queries, write 4-byte keys, four 8-bit LSD passes of 16 bytes per
+    (key, index) pair, write a 4-byte order."""
     return q * (4 * D + 72)
+
+
+def qschedule_bytes(q: int, D: int) -> int:
+    """The traversal schedule query_knn runs instead: the same terms with
+    two passes (the top 16 key bits) in place of four."""
+    return q * (4 * D + 40)
 
 
 def knn_bytes(q: int, D: int, k: int) -> int:
@@ -156,9 +165,79 @@ def job_clouds(w: dict) -> list:
     return [(pts, q)]
 
 
-def cpu_baseline(clouds: list, k: int, seconds: float) -> dict:
+def _cpu_model() -> str:
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return model
+
+
+def _query_sample(clouds: list, per_cloud: int, seed: int) -> list:
+    """A seeded sample of at most `per_cloud` queries of every cloud (local
+    indices, sorted)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    return [np.sort(rng.choice(len(q), min(per_cloud, len(q)), replace=False)) for _, q in clouds]
+
+
+def cpu_baseline(clouds: list, k: int, per_cloud: int = 4096, seconds: float = 20.0) -> dict:
+    """The reference's CPU path, which is its tests' brute force
+    (tests/test_knn.py:10-12: (q[:, None] - p[None]).square().sum(-1) then
+    top-k) with the (distance, index) tie rule (top-k of the int64 composite
+    float_bits(d) << 32 | index), on every host core this process may run
+    on.  Timed on a seeded sample of up to `per_cloud` queries per cloud
+    against all of that cloud's points (fewer when a short probe shows the
+    sample would take much more than `seconds`), in chunks of at most 2^26
+    pairs, and extrapolated to the job by (query, point) pairs: brute force
+    costs exactly that many distance evaluations."""
+    from oracle.torch_bruteforce import knn_bruteforce
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+
+    def run(samples) -> float:
+        t = time.perf_counter()
+        for (p, q), sel in zip(clouds, samples):
+            if len(sel):
+                chunk = max(1, min(256, (1 << 26) // max(len(p), 1)))
+                knn_bruteforce(torch.from_numpy(p), torch.from_numpy(q[sel]), k, chunk=chunk)
+        return time.perf_counter() - t
+
+    def pairs(samples) -> int:
+        return sum(len(sel) * len(p) for sel, (p, _) in zip(samples, clouds))
+
+    probe = _query_sample(clouds[:1], 32, 97) + [[]] * (len(clouds) - 1)
+    run(probe)  # warm-up: thread pool, allocator
+    rate = pairs(probe) / max(run(probe), 1e-9)  # pairs per second
+    while per_cloud > 16 and pairs(_query_sample(clouds, per_cloud, 98)) > 1.5 * rate * seconds:
+        per_cloud //= 2
+    samples = _query_sample(clouds, per_cloud, 98)
+    dt = run(samples)
+    Q = sum(len(q) for _, q in clouds)
+    n_sampled = sum(len(s) for s in samples)
+    total = dt * sum(len(q) * len(p) for p, q in clouds) / pairs(samples)
+    return {
+        "value": Q / total,
+        "unit": "queries/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"the reference tests' torch brute force (squared differences summed, top-k of the "
+                   f"(distance, index) composite), torch {torch.__version__} on {cores} threads "
+                   f"(os.sched_getaffinity; os.cpu_count() = {os.cpu_count()}); {n_sampled} of {Q} queries "
+                   f"(up to {per_cloud} per cloud, seeded) against all points in {dt:.3g} s, extrapolated "
+                   f"by (query, point) pairs to the job: {total:.3g} s; CPU: {_cpu_model()}"),
+    }
+
+
+def cpu_port_dfs(clouds: list, k: int, seconds: float) -> dict:
     """The whole job on the host with the C oracle, which restates the
-    reference's algorithm (implicit-tree build, DFS k-NN with the sorted
+    reference's GPU algorithm (implicit-tree build, DFS k-NN with the sorted
     candidate list).  Every cloud is built in full (one thread); the k-NN is
     timed on a uniform sample of the job's queries sized to about `seconds`
     (OpenMP over queries) and extrapolated to all of them."""
@@ -166,7 +245,7 @@ def cpu_baseline(clouds: list, k: int, seconds: float) -> dict:
 
     import oracle
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = len(os.sched_getaffinity(0))
     oracle.lib().orc_set_num_threads(threads)
     t0 = time.perf_counter()
     bvhs = [oracle.build(p) for p, _ in clouds]
@@ -196,15 +275,6 @@ def cpu_baseline(clouds: list, k: int, seconds: float) -> dict:
         if n == Q or dt >= 0.5 * seconds:
             break
     total = t_build + Q * per_query
-    cpu_model = platform.processor() or "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
         "value": Q / total,
         "unit": "queries/s",
@@ -213,7 +283,7 @@ def cpu_baseline(clouds: list, k: int, seconds: float) -> dict:
         "sample": (f"C oracle (restated reference build + DFS k-NN, gcc -O2): all {len(clouds)} "
                    f"cloud(s) built on 1 thread in {t_build:.3g} s; k-NN of {n} of {Q} queries "
                    f"(uniform sample) on {threads} threads in {dt:.3g} s; extrapolated job "
-                   f"time {total:.3g} s; CPU: {cpu_model}"),
+                   f"time {total:.3g} s; CPU: {_cpu_model()}"),
     }
 
 
@@ -377,8 +447,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-queries", type=int, default=4096,
+                    help="queries per cloud of the CPU baseline's sample (brute force)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="host time budget of the CPU baseline's sampled k-NN")
+                    help="host time budget of the C-oracle DFS's sampled k-NN")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--implicit-reps", type=int, default=1,
                     help="also time the traversal over the implicit tree (0 = skip)")
@@ -423,7 +495,8 @@ def main() -> int:
     else:
         total_q = qs.shape[0]
         b_bytes = build_bytes(pts.shape[0], D)
-    s_bytes = qsort_bytes(total_q, D)
+    s_bytes = qschedule_bytes(total_q, D)
+    full_sort_bytes = qsort_bytes(total_q, D)
     n_bytes = knn_bytes(total_q, D, k)
 
     from torchbvh_amd._native import _C
@@ -484,6 +557,26 @@ def main() -> int:
         sort_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
         trav_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
 
+    full_sort_ms = None
+    if kind != "ragged":
+        # The reference binding's full Morton sort of the queries (30 / 32
+        # key bits, four passes), which query_knn replaces with the two-pass
+        # schedule; timed on its own, outside the timed region.
+        bvh, _ = step()
+        one = kind == "single"
+        qb = qs.unsqueeze(0) if one else qs
+        smin = bvh["scene_min"].unsqueeze(0) if one else bvh["scene_min"]
+        smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
+        for _ in range(2):
+            _C.morton_sort_queries_narrow(qb, smin, smax)
+        ef = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ef[0].record()
+        for _ in range(10):
+            _C.morton_sort_queries_narrow(qb, smin, smax)
+        ef[1].record()
+        torch.cuda.synchronize()
+        full_sort_ms = ef[0].elapsed_time(ef[1]) / 10
+
     implicit_ms = None
     if kind != "ragged" and args.implicit_reps > 0:
         # The same query over the reference's implicit tree, for comparison
@@ -541,12 +634,19 @@ def main() -> int:
         "build_ms": build_ms,
         "query_ms": query_ms,
         "query_sort_ms": sort_ms,
+        "query_sort_what": "traversal schedule: stable 2-pass radix sort on the top 16 bits of Hilbert keys",
         "traversal_ms": trav_ms,
         "traversal_implicit_tree_ms": implicit_ms,
         "queries_per_s_excl_build": total_q / (query_ms * 1e-3) if query_ms > 0 else None,
         "build_hbm_frac_algorithmic": (b_bytes / (build_ms * 1e-3) / 1e9) / HBM_PEAK_GBS,
         "query_sort_hbm_frac_algorithmic": ((s_bytes / (sort_ms * 1e-3) / 1e9) / HBM_PEAK_GBS
                                             if sort_ms else None),
+        "query_sort_bytes_formula": "Q(4D+40): queries read, 4-B keys, 2 passes x 16 B, 4-B order",
+        "query_sort_full_ms": full_sort_ms,
+        "query_sort_full_what": "reference binding morton_sort_queries_narrow: 30/32-bit Morton keys, 4 passes",
+        "query_sort_full_hbm_frac_algorithmic": ((full_sort_bytes / (full_sort_ms * 1e-3) / 1e9) / HBM_PEAK_GBS
+                                                 if full_sort_ms else None),
+        "query_sort_full_bytes_formula": "Q(4D+72)",
         "roofline": {
             "bound": "hbm",
             "kernel": "knn_accel_kernel (traversal)",
@@ -558,7 +658,9 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(job_clouds(w), k, args.cpu_seconds)
+        clouds = job_clouds(w)
+        line["cpu_baseline"] = cpu_baseline(clouds, k, args.cpu_queries, args.cpu_seconds * 2)
+        line["cpu_port_bvh_dfs"] = cpu_port_dfs(clouds, k, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 
