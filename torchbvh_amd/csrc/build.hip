@@ -75,17 +75,44 @@ __device__ inline void fill_segment(Segment& g, int64_t start, int n, bool with_
     }
 }
 
+// Segment i of S equal clouds of n rows.
+__device__ inline Segment uniform_segment(int64_t i, int n, bool with_tree) {
+    Segment g;
+    fill_segment(g, i * n, n, with_tree);
+    g.tile_first = static_cast<int32_t>(i * g.tiles);
+    g.node_start = i * g.nr;
+    for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(i * g.groups[p]);
+    return g;
+}
+
+// Grid-stride store of the whole table of S equal clouds.
+__device__ inline void store_uniform_table(Segment* segs, int64_t S, int n, bool with_tree) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < S; i += stride) {
+        segs[i] = uniform_segment(i, n, with_tree);
+    }
+}
+
+// Segment of tile t in the first launch of a sequence (see UniformPlan):
+// computed for equal clouds (tiles past the last cloud's count as surplus
+// tiles of it), else looked up in the table.  Ends with a barrier either way.
+__device__ inline Segment first_launch_segment(const Segment* segs, int S, const UniformPlan& plan, int64_t t,
+                                               int* s_seg, int* seg_out) {
+    if (plan.n > 0) {
+        const int64_t per = (plan.n + kSortTile - 1) / kSortTile;
+        const int s = static_cast<int>(min(t / per, static_cast<int64_t>(S) - 1));
+        __syncthreads();
+        *seg_out = s;
+        return uniform_segment(s, plan.n, plan.tree);
+    }
+    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); }, S, t, s_seg);
+    *seg_out = s;
+    return segs[s];
+}
+
 __global__ __launch_bounds__(kBlock) void plan_uniform_kernel(Segment* segs, int64_t S, int n,
                                                               bool with_tree) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < S; i += stride) {
-        Segment g;
-        fill_segment(g, i * n, n, with_tree);
-        g.tile_first = static_cast<int32_t>(i * g.tiles);
-        g.node_start = i * g.nr;
-        for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(i * g.groups[p]);
-        segs[i] = g;
-    }
+    store_uniform_table(segs, S, n, with_tree);
 }
 
 // One work-group scans all segments in chunks of kBlock.
@@ -169,16 +196,16 @@ constexpr int kTileRows = kSortTile / kTileThreads;
 
 template <int D>
 __global__ __launch_bounds__(kTileThreads) void bounds_kernel(const float* __restrict__ points,
-                                                              const Segment* __restrict__ segs, int S,
+                                                              const Segment* segs, int S,
                                                               float seed_lo, float seed_hi,
-                                                              float* __restrict__ partials) {
+                                                              float* __restrict__ partials, UniformPlan plan) {
     __shared__ int s_seg;
     __shared__ float s_red[kTileThreads / kWave][2 * D];
     __shared__ float s_out[2 * D];
     const int64_t t = blockIdx.x;
-    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
-                                     S, t, &s_seg);
-    const Segment g = segs[s];
+    if (plan.table) store_uniform_table(plan.table, S, plan.n, plan.tree);
+    int s;
+    const Segment g = first_launch_segment(segs, S, plan, t, &s_seg, &s);
     const int lt = static_cast<int>(t - g.tile_first);
     if (lt >= g.tiles) return;
     const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
@@ -298,12 +325,13 @@ __global__ __launch_bounds__(kBlock) void primitive_prep_kernel(const float* __r
 // with LDS atomics and stored digit-major; surplus tiles store zeros.
 template <int D, bool kHilbert>
 __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __restrict__ points,
-                                                              const Segment* __restrict__ segs, int S,
+                                                              const Segment* segs, int S,
                                                               float* __restrict__ scene_min,
                                                               float* __restrict__ scene_max,
                                                               uint32_t* __restrict__ keys,
                                                               uint32_t* __restrict__ tile_hist, int64_t tstride,
-                                                              int first_bit, BoundsFinish fin) {
+                                                              int first_bit, BoundsFinish fin,
+                                                              UniformPlan plan) {
     static_assert(kTileThreads >= kRadix, "one thread per digit");
     __shared__ int s_seg;
     __shared__ uint32_t s_hist[kRadix];
@@ -311,9 +339,9 @@ __global__ __launch_bounds__(kTileThreads) void morton_kernel(const float* __res
     __shared__ float s_box[2 * D];
     const int64_t t = blockIdx.x;
     if (threadIdx.x < kRadix) s_hist[threadIdx.x] = 0u;
-    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); },
-                                     S, t, &s_seg);
-    const Segment g = segs[s];
+    if (plan.table) store_uniform_table(plan.table, S, plan.n, plan.tree);
+    int s;
+    const Segment g = first_launch_segment(segs, S, plan, t, &s_seg, &s);
     const int lt = static_cast<int>(t - g.tile_first);
     if (lt >= g.tiles) {
         if (tile_hist && threadIdx.x < kRadix) tile_hist[threadIdx.x * tstride + t] = 0u;
@@ -582,18 +610,18 @@ hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S,
 
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles, float* partials, float* scene_min, float* scene_max,
-                         bool finalize, float seed_lo, float seed_hi, hipStream_t stream) {
+                         bool finalize, float seed_lo, float seed_hi, UniformPlan plan, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const unsigned cgrid = static_cast<unsigned>(S);
     const int Si = static_cast<int>(S);
     if (D == 3) {
-        bounds_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, seed_lo, seed_hi, partials);
+        bounds_kernel<3><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, seed_lo, seed_hi, partials, plan);
         if (finalize) {
             bounds_final_kernel<3><<<cgrid, kBlock, 0, stream>>>(segs, partials, seed_lo, seed_hi, scene_min,
                                                                  scene_max);
         }
     } else {
-        bounds_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, seed_lo, seed_hi, partials);
+        bounds_kernel<2><<<grid, kTileThreads, 0, stream>>>(points, segs, Si, seed_lo, seed_hi, partials, plan);
         if (finalize) {
             bounds_final_kernel<2><<<cgrid, kBlock, 0, stream>>>(segs, partials, seed_lo, seed_hi, scene_min,
                                                                  scene_max);
@@ -628,12 +656,13 @@ hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment
 
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S, int64_t tiles,
                          float* scene_min, float* scene_max, uint32_t* keys, uint32_t* tile_hist,
-                         int64_t tstride, SortBits bits, BoundsFinish fin, hipStream_t stream) {
+                         int64_t tstride, SortBits bits, BoundsFinish fin, hipStream_t stream,
+                         UniformPlan plan) {
     const unsigned grid = static_cast<unsigned>(tiles);
     const int Si = static_cast<int>(S);
     auto run = [&](auto kernel) {
         kernel<<<grid, kTileThreads, 0, stream>>>(points, segs, Si, scene_min, scene_max, keys, tile_hist,
-                                                  tstride, bits.first_bit, fin);
+                                                  tstride, bits.first_bit, fin, plan);
     };
     if (D == 3) {
         bits.hilbert ? run(morton_kernel<3, true>) : run(morton_kernel<3, false>);

@@ -158,8 +158,17 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l);
     const bool ragged = offsets != nullptr;
-    hipError_t e = ragged ? launch_plan_offsets(segs, offsets, S, true, o.node_offsets, stream)
-                          : launch_plan_uniform(segs, S, n_uniform, true, stream);
+    // Equal clouds of points need no planning launch: the bounds kernel
+    // computes their segments and stores the table for the later launches.
+    UniformPlan plan;
+    hipError_t e = hipSuccess;
+    if (ragged) {
+        e = launch_plan_offsets(segs, offsets, S, true, o.node_offsets, stream);
+    } else if (V > 0) {
+        e = launch_plan_uniform(segs, S, n_uniform, true, stream);
+    } else {
+        plan = UniformPlan{segs, static_cast<int>(n_uniform), true};
+    }
     if (e != hipSuccess) return e;
     float* partials = carve<float>(ws, l.partials);
     const float* boxes = nullptr;
@@ -189,7 +198,7 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
         points = centers;
         boxes = leaf_boxes;
     } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max, !fuse,
-                                  seed_lo, seed_hi, stream)) != hipSuccess) {
+                                  seed_lo, seed_hi, plan, stream)) != hipSuccess) {
         return e;
     }
     const SortBits bits = full_sort(D);
@@ -238,14 +247,18 @@ hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t 
     const Layout l = make_layout(S, rows, D, false);
     Segment* segs = carve<Segment>(ws, l.segs);
     const SortBuffers sb = sort_buffers(ws, l);
-    hipError_t e = offsets ? launch_plan_offsets(segs, offsets, S, false, nullptr, stream)
-                           : launch_plan_uniform(segs, S, m_uniform, false, stream);
+    // Equal clouds need no planning launch: the Morton kernel computes their
+    // segments and stores the table for the sort.
+    UniformPlan plan;
+    hipError_t e = hipSuccess;
+    if (offsets) e = launch_plan_offsets(segs, offsets, S, false, nullptr, stream);
+    else plan = UniformPlan{segs, static_cast<int>(m_uniform), false};
     if (e != hipSuccess) return e;
     uint32_t* keys = codes_only ? codes_only : sb.keys_a;
     // Bounds given (BoundsFinish empty): the kernel only reads them.
     if ((e = launch_morton(queries, D, segs, S, l.tiles, const_cast<float*>(scene_min),
                            const_cast<float*>(scene_max), keys, codes_only ? nullptr : sb.tile_hist, sb.tstride,
-                           bits, BoundsFinish{}, stream)) != hipSuccess) {
+                           bits, BoundsFinish{}, stream, plan)) != hipSuccess) {
         return e;
     }
     if (codes_only) return hipSuccess;

@@ -113,6 +113,17 @@ struct SortPass {
     int shift;
 };
 
+// How the first launch of a sequence finds its segments: for S equal
+// clouds of n rows (n > 0) it computes each one in place, and also stores
+// the whole table into `table` for the launches after it (so no planning
+// launch runs first); with n == 0 it reads the table a planning launch
+// filled.
+struct UniformPlan {
+    Segment* table = nullptr;
+    int n = 0;
+    bool tree = false;
+};
+
 // Planning: fill the segment table.
 hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream);
 hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S, bool tree,
@@ -124,7 +135,7 @@ hipError_t launch_plan_offsets(Segment* segs, const int64_t* offsets, int64_t S,
 // given the same partials in a BoundsFinish).
 hipError_t launch_bounds(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles_bound, float* partials, float* scene_min, float* scene_max,
-                         bool finalize, float seed_lo, float seed_hi, hipStream_t stream);
+                         bool finalize, float seed_lo, float seed_hi, UniformPlan plan, hipStream_t stream);
 
 // Clouds of at most this many tiles get their bounds reduced inside the
 // Morton kernel (each of a cloud's work-groups reads all its partial boxes,
@@ -164,7 +175,7 @@ hipError_t launch_primitive_prep(const float* prims, int D, int V, const Segment
 hipError_t launch_morton(const float* points, int D, const Segment* segs, int64_t S,
                          int64_t tiles_bound, float* scene_min, float* scene_max,
                          uint32_t* keys, uint32_t* tile_hist, int64_t tstride, SortBits bits,
-                         BoundsFinish fin, hipStream_t stream);
+                         BoundsFinish fin, hipStream_t stream, UniformPlan plan = UniformPlan{});
 
 // Stable LSD sort of (key, local index) per segment on the digits of
 // `bits`; writes int64 local indices in key order into `order` and, if
