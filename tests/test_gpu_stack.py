@@ -1,7 +1,8 @@
-"""The accel traversal's bounded stack: inputs whose trees are deep enough,
-or whose boxes tie closely enough, that a lane's ring of LDS entries
-overflows, drops entries and must resume through the parent links.  Results
-must still be the oracle's k nearest (distance, index) pairs, bit for bit.
+"""The traversals' bounded stack: inputs whose trees are deep enough, or
+whose boxes tie closely enough, that a lane's ring of LDS entries overflows,
+drops entries and must resume through the parent links (the accel's stored
+links, the implicit tree's closed forms).  Results must still be the
+oracle's k nearest (distance, index) pairs, bit for bit.
 
 Measured on a CPU model of the traversal (16-entry ring, as in the 3-D
 k = 16 kernel): every query of the shell cloud drops entries and walks up
@@ -88,3 +89,31 @@ def test_ragged_clouds_with_deep_trees():
     ei, ed = oracle.knn_ragged(pts, po, q, qo, 4)
     assert_same_int(idx.cpu().numpy(), ei, "indices")
     assert_same_f32(dist.cpu().numpy(), ed, "distances")
+
+
+@pytest.mark.parametrize("k,dim,n", [(4, 3, 600_000), (16, 2, 600_000), (16, 3, 2_200_000)])
+def test_implicit_tree_ring_overflow(k, dim, n):
+    """The implicit-tree traversal (the reference's layout, no accel) uses
+    the same ring with the resume walk through closed-form parents.  A shell
+    cloud of n points has L - 1 levels of internal nodes above the leaves'
+    parents (19 for 600,000 points, 21 for 2,200,000), each of which defers
+    its far child for a query at the centre: more than the ring holds (16
+    entries for 3-D k = 4 and 2-D k = 16, 20 for 3-D k = 16).  Results must be
+    the brute force's bit for bit."""
+    from torchbvh_amd._native import _C
+
+    print(f"stack: implicit shell dim={dim} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(900 + 10 * k + dim)
+    pts = shell(rng, n, dim)
+    q = np.concatenate([np.full((64, dim), 0.5, np.float32),
+                        (0.5 + 0.02 * rng.standard_normal((128, dim))).astype(np.float32),
+                        rng.random((64, dim), dtype=np.float32)])
+    h = tb.build_bvh(dev(pts))
+    nodes, sidx = h["node_aabbs"][None], h["sorted_indices"][None]
+    idx, dist = _C.query_knn_batched_cached_bounds(nodes, sidx, dev(q)[None], h["num_leaves"],
+                                                    h["num_real_nodes"], h["dim"], k, accel=False)
+    torch.cuda.synchronize()
+    tb.destroy_bvh(h)
+    ei, ed = oracle.knn_brute(pts, q, k)
+    assert_same_int(idx[0].cpu().numpy(), ei, "indices")
+    assert_same_f32(dist[0].cpu().numpy(), ed, "distances")

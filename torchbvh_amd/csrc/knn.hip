@@ -1,11 +1,13 @@
-// Exact k-NN by branch-and-bound over the implicit BVH.
+// Exact k-NN by branch-and-bound over a BVH of one cloud.
 //
 // Follows the reference traversal (torchbvh/csrc/knn_query.cu:47-154): one
-// query per lane, launched in Morton order when an order is given; root box
-// distance first; at an internal node both real children's box distances are
-// evaluated, the far child is deferred on a stack with its distance cached if
-// it can still hold a candidate, and the near child is entered; nodes are
-// visited while their box distance is <= the current k-th distance.
+// query per lane, launched in Morton order when an order is given; at an
+// internal node both real children's box distances are evaluated, the far
+// child is deferred on a stack with its distance cached if it can still hold
+// a candidate, and the near child is entered; nodes are visited while their
+// box distance is <= the current k-th distance.  The same traversal runs over
+// two node sources: the reference's implicit tree (node_aabbs + sorted
+// indices) and the acceleration structure built beside it (accel.hip).
 //
 // The candidate list is where this kernel deliberately differs: entries are
 // 64-bit keys (float bits of the squared distance << 32 | point index) kept
@@ -28,7 +30,6 @@ namespace tbvh {
 namespace {
 
 constexpr float kFar = FLT_MAX;
-constexpr int kStackDepth = 32;
 
 template <int D>
 __device__ __forceinline__ float box_distance(const float* q, const float* box) {
@@ -130,108 +131,6 @@ __device__ __forceinline__ void write_results(const KnnArgs& a, int64_t out_row,
     }
 }
 
-template <int D, int K, bool kOrdered, bool kRagged>
-__global__ __launch_bounds__(kBlock) void knn_kernel(KnnArgs a) {
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (gid >= a.total_q) return;
-
-    int64_t seg, qbase, qcount, pstart, nstart;
-    int n;
-    if constexpr (kRagged) {
-        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
-        qbase = a.query_offsets[seg];
-        qcount = a.query_offsets[seg + 1] - qbase;
-        pstart = a.point_offsets[seg];
-        n = static_cast<int>(a.point_offsets[seg + 1] - pstart);
-        nstart = a.node_offsets[seg];
-    } else {
-        seg = gid / a.M;
-        qbase = seg * a.M;
-        qcount = a.M;
-        n = a.num_leaves;
-        pstart = seg * static_cast<int64_t>(n);
-        nstart = seg * static_cast<int64_t>(a.num_real_nodes);
-    }
-    const int64_t local = gid - qbase;
-    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
-    if (qi < 0 || qi >= qcount) return;  // a corrupt order never indexes out of range
-    const int64_t row = qbase + qi;
-    const float* node_base = a.node_aabbs;
-    const int64_t* sorted_base = a.sorted_indices;
-    int64_t index_offset = 0;
-    if (!kRagged && a.routes != nullptr && a.routes[row] == 0) {
-        // False route (knn_query.cu:205-217): the second tree, indices after
-        // the first tree's points.
-        index_offset = n;
-        n = a.num_leaves2;
-        pstart = seg * static_cast<int64_t>(n);
-        nstart = seg * static_cast<int64_t>(a.num_real_nodes2);
-        node_base = a.node_aabbs2;
-        sorted_base = a.sorted_indices2;
-    }
-    const float* nodes = node_base + nstart * 2 * D;
-    const int64_t* sorted = sorted_base + pstart;
-
-    float q[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) q[d] = a.queries[row * D + d];
-
-    const int L = tree::leaf_level(n);
-    const int vl = tree::virtual_leaves(n);
-    const int first_leaf = tree::level_first(L);
-
-    uint64_t best[K];
-#pragma unroll
-    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
-
-    uint64_t stack[kStackDepth];
-    int sp = 0;
-    int node = 0;
-    float nd = box_distance<D>(q, nodes);
-
-    while (true) {
-        const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
-        if (nd <= worst) {
-            if (node >= first_leaf) {
-                const uint32_t idx = static_cast<uint32_t>(sorted[node - first_leaf]);
-                const uint64_t key = candidate_key(nd, idx);
-                if (nd < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
-            } else {
-                const int lc = 2 * node + 1;
-                const int rc = lc + 1;
-                const bool right_real = !tree::is_virtual(vl, L, rc);
-                const int lrow = tree::memory_index(vl, L, lc);
-                const float* box = nodes + static_cast<int64_t>(lrow) * 2 * D;
-                const float ld = box_distance<D>(q, box);
-                const float rd = right_real ? box_distance<D>(q, box + 2 * D) : kFar;
-                const bool left_near = ld <= rd;
-                const int near_node = left_near ? lc : rc;
-                const int far_node = left_near ? rc : lc;
-                const float near_d = left_near ? ld : rd;
-                const float far_d = left_near ? rd : ld;
-                const bool far_real = left_near ? right_real : true;
-                const bool near_real = left_near ? true : right_real;
-                if (far_real && far_d <= worst) {
-                    stack[sp++] = (static_cast<uint64_t>(far_node) << 32) | __float_as_uint(far_d);
-                }
-                if (near_real && near_d <= worst) {
-                    node = near_node;
-                    nd = near_d;
-                    continue;
-                }
-            }
-        }
-        if (sp == 0) break;
-        const uint64_t e = stack[--sp];
-        node = static_cast<int>(e >> 32);
-        nd = __uint_as_float(static_cast<uint32_t>(e));
-    }
-
-    // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
-    const int64_t out_row = a.spatial_output ? qbase + local : row;
-    write_results<K, D>(a, out_row, best, index_offset, pstart);
-}
-
 // Exact distance to a point stored as float4, bit-identical to box_distance
 // on the point's degenerate box (lo = hi = p) for every input, NaN and inf
 // included.  There, delta = max(p - q, max(0, q - p)); IEEE subtraction is
@@ -255,15 +154,14 @@ __device__ __forceinline__ float point_distance(const float* q, const float4 p) 
 // One wave per work-group: measured against 256 threads, -3.5% at cfg2 and
 // -14% at cfg5, whose waves differ most in cost (finer-grained balancing
 // over the CUs); 128 falls between, 512 is 13-24% slower.
-constexpr int kAccelBlock = 64;
+constexpr int kKnnBlock = 64;
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 
 // Entries of a lane's deferred-node stack, all in LDS (6 bytes each: a
-// 32-bit child ref and a 16-bit distance, in columns of stride
-// kAccelBlock): as many as the LDS budget of each (D, k) holds.  The budgets
-// are the ones measured best for the earlier 8-byte entries: 7.5 KB per
-// work-group for 3-D k = 16, 10 KB for 3-D k = 32 and 2-D k = 8, 6 KB
-// otherwise.
+// 32-bit child ref and a 16-bit distance, in columns of stride kKnnBlock):
+// as many as the LDS budget of each (D, k) holds.  The budgets are the ones
+// measured best for the earlier 8-byte entries: 7.5 KB per work-group for
+// 3-D k = 16, 10 KB for 3-D k = 32 and 2-D k = 8, 6 KB otherwise.
 template <int D, int K>
 constexpr int lds_stack_entries() {
     if (D == 2 && K == 8) return 26;
@@ -282,10 +180,10 @@ constexpr int lds_stack_entries() {
 // be popped) and keeps the smallest dropped distance in `lost_min`.
 // Nothing is lost for correctness: when the ring empties with lost_min <=
 // the k-th distance, the traversal resumes through the parent links (see
-// knn_accel_kernel).
+// traverse).
 template <int L>
 struct RingStack {
-    uint32_t* refs;   // this lane's column: slot i at refs[i * kAccelBlock]
+    uint32_t* refs;   // this lane's column: slot i at refs[i * kKnnBlock]
     uint16_t* dists;  // likewise
     int top = 0;      // slot of the next push
     int count = 0;
@@ -293,69 +191,198 @@ struct RingStack {
     __device__ __forceinline__ void push(float d, int32_t ref) {
         if (count == L) {
             // Full: slot `top` holds the oldest entry.
-            lost_min = fminf(lost_min, __uint_as_float(static_cast<uint32_t>(dists[top * kAccelBlock]) << 16));
+            lost_min = fminf(lost_min, __uint_as_float(static_cast<uint32_t>(dists[top * kKnnBlock]) << 16));
         } else {
             ++count;
         }
-        refs[top * kAccelBlock] = static_cast<uint32_t>(ref);
-        dists[top * kAccelBlock] = static_cast<uint16_t>(__float_as_uint(d) >> 16);
+        refs[top * kKnnBlock] = static_cast<uint32_t>(ref);
+        dists[top * kKnnBlock] = static_cast<uint16_t>(__float_as_uint(d) >> 16);
         top = top == L - 1 ? 0 : top + 1;
     }
     __device__ __forceinline__ void pop(float& d, int32_t& ref) {
         top = top == 0 ? L - 1 : top - 1;
         --count;
-        ref = static_cast<int32_t>(refs[top * kAccelBlock]);
-        d = __uint_as_float(static_cast<uint32_t>(dists[top * kAccelBlock]) << 16);
+        ref = static_cast<int32_t>(refs[top * kKnnBlock]);
+        d = __uint_as_float(static_cast<uint32_t>(dists[top * kKnnBlock]) << 16);
     }
 };
 
-// Brute-forces one bucket (<= accel_bucket<D>() consecutive Morton-ordered
-// points, loaded together) into the candidate list.
-template <int D, int K>
-__device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int n, const float* q,
-                                            uint64_t (&best)[K]) {
-    const int first = ref & 0x0fffffff;
-    const int count = ((ref >> 28) & 7) + 1;
-    if (first + count > n) return;  // a corrupt ref never reads outside the cloud
-    constexpr int kBucket = accel_bucket<D>();
-    float4 p[kBucket];
-#pragma unroll
-    for (int j = 0; j < kBucket; ++j) {
-        p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+// ---------------------------------------------------------------------------
+// Node sources.  The traversal reaches a structure only through these
+// members: `root()`, `is_bucket(ref)`, `is_internal(ref)`, `children(ref,
+// ...)` (both child box distances and refs; an absent child has distance
+// +inf, which no k-th distance admits), `parent(ref)` (-1 above the root)
+// and `scan(bucket, ...)` (brute force of a bucket's points into the
+// candidate list), plus `kNone`, a ref that is never a bucket.
+// ---------------------------------------------------------------------------
+
+// The acceleration structure (accel.hip): an internal node's record holds
+// both child boxes, both child refs and its parent; a bucket (negative ref:
+// first position in the low 28 bits, count - 1 in bits 28-30) is up to
+// accel_bucket<D>() consecutive Morton-ordered points, loaded together.
+template <int D>
+struct AccelNodes {
+    static constexpr int R = 4 * D + 4;
+    static constexpr int32_t kNone = 0;  // bucket refs are negative
+    const float4* pts;                   // this cloud's points
+    const float* recs;                   // this cloud's record rows
+    int n;
+
+    __device__ __forceinline__ int32_t root() const {
+        return n <= accel_bucket<D>() ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
+                                      : 0;
     }
+    __device__ __forceinline__ bool is_bucket(int32_t ref) const { return ref < 0; }
+    __device__ __forceinline__ bool is_internal(int32_t ref) const { return ref < n - 1; }
+
+    __device__ __forceinline__ void children(int32_t ref, const float* q, float& ld, float& rd, int32_t& lref,
+                                             int32_t& rref) const {
+        const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
+        float rec[R];
 #pragma unroll
-    for (int j = 0; j < kBucket; ++j) {
-        if (j < count) {
-            const float d = point_distance<D>(q, p[j]);
-            const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
-            if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+        for (int v = 0; v < R / 4; ++v) {
+            const float4 x = r4[v];
+            rec[4 * v] = x.x;
+            rec[4 * v + 1] = x.y;
+            rec[4 * v + 2] = x.z;
+            rec[4 * v + 3] = x.w;
+        }
+        ld = box_distance<D>(q, rec);
+        rd = box_distance<D>(q, rec + 2 * D);
+        lref = __float_as_int(rec[4 * D]);
+        rref = __float_as_int(rec[4 * D + 1]);
+    }
+
+    // An internal node's parent is in its own row; a bucket's, in the last
+    // word of the row where it starts.  A link outside the cloud's internal
+    // nodes (which a well-formed accel never holds) ends the walk.
+    __device__ __forceinline__ int32_t parent(int32_t ref) const {
+        const int32_t par = __float_as_int(
+            recs[static_cast<int64_t>(ref >= 0 ? ref : ref & 0x0fffffff) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
+        return par >= 0 && par < n - 1 ? par : -1;
+    }
+
+    template <int K>
+    __device__ __forceinline__ void scan(int32_t ref, const float* q, uint64_t (&best)[K]) const {
+        const int first = ref & 0x0fffffff;
+        const int count = ((ref >> 28) & 7) + 1;
+        if (first + count > n) return;  // a corrupt ref never reads outside the cloud
+        constexpr int kBucket = accel_bucket<D>();
+        float4 p[kBucket];
+#pragma unroll
+        for (int j = 0; j < kBucket; ++j) {
+            p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int j = 0; j < kBucket; ++j) {
+            if (j < count) {
+                const float d = point_distance<D>(q, p[j]);
+                const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
+                if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
+            }
         }
     }
-}
+};
 
-// Branch-and-bound over the acceleration structure (see accel.hip): the
-// pruning rule, near-first order and cached far-child distances of the
-// implicit-tree kernel above; deferred nodes on a per-lane stack.
+// The reference's implicit tree (implicit_tree.cuh:26-127): refs are heap
+// indices, a node's children are 2i + 1 and 2i + 2 (the right one possibly
+// virtual) and its parent (i - 1) / 2.  The "buckets" are the leaves'
+// parents (level L - 1; the root when it is the only leaf): their scan
+// scores both leaves from their own (degenerate) boxes with box_distance,
+// exactly as the reference scores a leaf, near leaf first, each against the
+// k-th distance as it stands then; that is the reference's visit of the two
+// leaves (the far leaf is pushed, the near one entered, and the far one
+// popped straight after), with no stack entry.
+template <int D>
+struct HeapNodes {
+    static constexpr int32_t kNone = -1;
+    const float* nodes;     // this tree's rows of 2 * D floats
+    const int64_t* sorted;  // this cloud's sorted indices
+    int n;
+    int L;                  // leaf level
+    int vl;                 // virtual leaves
+    int bucket_first;       // heap index of the first node on the leaves' parents' level
+    int leaf_row0;          // storage row of leaf position 0
+
+    __device__ __forceinline__ void init(const float* nodes_, const int64_t* sorted_, int n_) {
+        nodes = nodes_;
+        sorted = sorted_;
+        n = n_;
+        L = tree::leaf_level(n);
+        vl = tree::virtual_leaves(n);
+        bucket_first = tree::level_first(L > 0 ? L - 1 : 0);
+        leaf_row0 = tree::memory_index(vl, L, tree::level_first(L));
+    }
+    __device__ __forceinline__ int32_t root() const { return 0; }
+    __device__ __forceinline__ bool is_bucket(int32_t ref) const { return ref >= bucket_first; }
+    __device__ __forceinline__ bool is_internal(int32_t) const { return true; }
+
+    __device__ __forceinline__ void children(int32_t ref, const float* q, float& ld, float& rd, int32_t& lref,
+                                             int32_t& rref) const {
+        lref = 2 * ref + 1;
+        rref = lref + 1;
+        // The real nodes of a level are consecutive rows, so a real right
+        // child is the row after the left one.
+        const float* box = nodes + static_cast<int64_t>(tree::memory_index(vl, L, lref)) * (2 * D);
+        ld = box_distance<D>(q, box);
+        rd = tree::is_virtual(vl, L, rref) ? INFINITY : box_distance<D>(q, box + 2 * D);
+    }
+
+    __device__ __forceinline__ int32_t parent(int32_t ref) const { return ref > 0 ? (ref - 1) >> 1 : -1; }
+
+    template <int K>
+    __device__ __forceinline__ void scan(int32_t ref, const float* q, uint64_t (&best)[K]) const {
+        // Leaf positions of the pair (a lone root leaf: position 0 only);
+        // the real leaves are positions < n.
+        const int p = L > 0 ? 2 * ref + 1 - tree::level_first(L) : 0;
+        const bool right_real = L > 0 && p + 1 < n;
+        const float* box = nodes + static_cast<int64_t>(leaf_row0 + p) * (2 * D);
+        const float ld = box_distance<D>(q, box);
+        const float rd = right_real ? box_distance<D>(q, box + 2 * D) : INFINITY;
+        const bool left_near = ld <= rd;
+        const int near_p = left_near ? p : p + 1;
+        const float near_d = left_near ? ld : rd;
+        const uint64_t near_key = candidate_key(near_d, static_cast<uint32_t>(sorted[near_p]));
+        if (near_d < kFar && near_key < best[K - 1]) insert_sorted<K>(best, near_key);
+        if (right_real) {
+            const int far_p = left_near ? p + 1 : p;
+            const float far_d = left_near ? rd : ld;
+            const uint64_t far_key = candidate_key(far_d, static_cast<uint32_t>(sorted[far_p]));
+            if (far_d < kFar && far_key < best[K - 1]) insert_sorted<K>(best, far_key);
+        }
+    }
+};
+
+// Branch-and-bound of one query over a node source: the reference's pruning
+// rule, near-first order (ties to the left child) and cached far-child
+// distances, with a bounded stack and postponed bucket scans.
 //
 // Bounded stack, exact resume.  The stack is a ring of lds_stack_entries
-// entries in LDS (RingStack); nothing lives in scratch.  When a push drops the oldest
-// entry, the lane records the smallest dropped distance.  When the ring
-// runs empty, nothing dropped can matter if that distance exceeds the k-th
-// distance (which only shrinks), and the lane is done.  Otherwise it walks
-// up from the last node it entered through the parent links: at each
-// ancestor it recomputes the two child distances, and if it came up from
-// the near child and the far child is within the k-th distance, the far
-// child is still pending (it was dropped: a far child pushed and not
+// entries in LDS (RingStack); nothing lives in scratch.  When a push drops
+// the oldest entry, the lane records the smallest dropped distance.  When
+// the ring runs empty, nothing dropped can matter if that distance exceeds
+// the k-th distance (which only shrinks), and the lane is done.  Otherwise
+// it walks up from the last node it entered through the parent links: at
+// each ancestor it recomputes the two child distances, and if it came up
+// from the near child and the far child is within the k-th distance, the
+// far child is still pending (it was dropped: a far child pushed and not
 // dropped is popped before the ring empties, after which the walk comes up
-// through it) and the traversal resumes there; otherwise it goes on up,
-// and at the root it is done.  The walk recomputes the same near/far
-// choice the descent made (same query, same boxes, ties to the left), so
-// no subtree is entered twice and no candidate is inserted twice.  Each
-// walk step costs two dependent loads (the parent link, then the parent's
+// through it) and the traversal resumes there; otherwise it goes on up, and
+// at the root it is done.  The walk recomputes the same near/far choice the
+// descent made (same query, same boxes, ties to the left), so no subtree is
+// entered twice and no candidate is inserted twice.  Nor does the ring
+// change the order of visits: the dropped entries are the bottom of the
+// stack, which an unbounded stack would also pop last, deepest first, and
+// the walk reaches them in that order and tests each with its exact
+// distance; a popped entry whose truncated distance passes but whose exact
+// one would not is entered and finds both children beyond the k-th distance
+// (a child's box lies inside its parent's, so its distance is no smaller),
+// as if it had been pruned.  A walk step over the
+// accel costs two dependent loads (the parent link, then the parent's
 // record), and one walking lane holds up its wave, so the ring is sized to
-// make drops rare: a CPU model of the traversal at cfg2 showed no query
-// deeper than 21 entries (a 16-entry ring of 8-byte entries made every
-// query drop and measured +20% traversal time).
+// make drops rare: a CPU model of the accel traversal at cfg2 showed no
+// query deeper than 21 entries (a 16-entry ring of 8-byte entries made
+// every query drop and measured +20% traversal time).
 //
 // Postponed buckets.  With one query per lane, the O(K) insertion into the
 // sorted list is the dominant cost, and the wave pays for it whenever any
@@ -370,77 +397,20 @@ __device__ __forceinline__ void scan_bucket(const float4* pts, int32_t ref, int 
 // distance, a valid (looser) bound, and a waiting lane re-tests its bucket
 // after the round, so results are unchanged; the end result is the k
 // smallest (distance, index) pairs whatever the order of visits.  Measured
-// on MI355X against immediate insertion: -20% at k = 16 (cfg2), -13% at
-// k = 8 (cfg4); a variant that buffered candidates in LDS and merged them
-// with sorting networks was slower (fewer waves fit).
+// on MI355X over the accel against immediate insertion: -20% at k = 16
+// (cfg2), -13% at k = 8 (cfg4); a variant that buffered candidates in LDS
+// and merged them with sorting networks was slower (fewer waves fit).
 //
-// Tile order: consecutive work-groups land on different XCDs, each with its
-// own L2; logical tile t = (block % 8) * (grid / 8) + block / 8 gives every
-// XCD a contiguous run of Morton-ordered queries, so one XCD's L2 serves a
-// compact region of the tree.
-template <int D, int K, bool kOrdered, bool kRagged>
-__global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
-    constexpr int R = 4 * D + 4;
-    constexpr int kLds = lds_stack_entries<D, K>();
-    __shared__ uint32_t lds_refs[kLds * kAccelBlock];
-    __shared__ uint16_t lds_dists[kLds * kAccelBlock];
-    const int64_t per_xcd = gridDim.x / kXcds;
-    const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    const int64_t gid = tile * kAccelBlock + threadIdx.x;
-    if (gid >= a.total_q) return;
-
-    int64_t seg, qbase, qcount, pstart;
-    int n;
-    if constexpr (kRagged) {
-        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
-        qbase = a.query_offsets[seg];
-        qcount = a.query_offsets[seg + 1] - qbase;
-        pstart = a.point_offsets[seg];
-        n = static_cast<int>(a.point_offsets[seg + 1] - pstart);
-    } else {
-        seg = gid / a.M;
-        qbase = seg * a.M;
-        qcount = a.M;
-        n = a.num_leaves;
-        pstart = seg * static_cast<int64_t>(n);
-    }
-    const int64_t local = gid - qbase;
-    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
-    if (qi < 0 || qi >= qcount) return;
-    const int64_t row = qbase + qi;
-    const void* accel = a.accel;
-    int64_t total_points = a.total_points;
-    int64_t index_offset = 0;
-    if (!kRagged && a.routes != nullptr && a.routes[row] == 0) {
-        // False route: the second structure, indices after the first's points.
-        index_offset = n;
-        n = a.num_leaves2;
-        pstart = seg * static_cast<int64_t>(n);
-        accel = a.accel2;
-        total_points = a.B * static_cast<int64_t>(n);
-    }
-    const float4* pts = static_cast<const float4*>(accel) + pstart;
-    const float* recs = reinterpret_cast<const float*>(static_cast<const char*>(accel) +
-                                                       accel_points_bytes(total_points)) +
-                        pstart * R;
-
-
-    float q[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) q[d] = a.queries[row * D + d];
-
-    uint64_t best[K];
-#pragma unroll
-    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
-
-    RingStack<kLds> stack;
-    stack.refs = lds_refs + threadIdx.x;
-    stack.dists = lds_dists + threadIdx.x;
-    int32_t ref = n <= accel_bucket<D>()
-                      ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
-                      : 0;
+// Without kPostpone, buckets are scanned when reached, so the traversal makes
+// the reference's visits in the reference's order.  The implicit tree runs
+// that way: where the result does depend on the order (points with a NaN
+// coordinate, whose distances the node boxes do not bound), it is then the
+// reference's result.
+template <bool kPostpone, int K, int L, class Nodes>
+__device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_t (&best)[K], RingStack<L>& stack) {
+    int32_t ref = t.root();
     float nd = 0.0f;
-    int32_t parked = 0;  // bucket refs are negative, so 0 means none
+    int32_t parked = Nodes::kNone;
     bool waiting = false;
     bool done = false;
 
@@ -448,46 +418,41 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
     // in a tight loop (a flag-driven single loop of the same work measured
     // 2x slower).
     while (true) {
-        const uint64_t holding = __ballot(parked != 0);
+        // Not in a scope of its own: a block here (an `if constexpr` body)
+        // reorders the loop's blocks and measured +5% traversal time.
+        const uint64_t holding = kPostpone ? __ballot(parked != Nodes::kNone) : 0;
         if (holding != 0) {
             const uint64_t live = __ballot(true);
             const uint64_t movable = __ballot(!waiting && !done);
             if (movable == 0 || __popcll(live) <= 2 * __popcll(holding)) {
-                if (parked != 0) scan_bucket<D>(pts, parked, n, q, best);
-                parked = 0;
+                if (parked != Nodes::kNone) t.scan(parked, q, best);
+                parked = Nodes::kNone;
                 waiting = false;
             }
         }
         if (done) {
-            if (parked == 0) break;
+            if (parked == Nodes::kNone) break;
             continue;
         }
         if (waiting) continue;
         const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
         if (nd <= worst) {
-            if (ref < 0) {
-                // Park the bucket; a lane already holding one waits and
-                // revisits this bucket after the next round.
-                if (parked != 0) {
-                    waiting = true;
-                    continue;
+            if (t.is_bucket(ref)) {
+                if constexpr (kPostpone) {
+                    // Park the bucket; a lane already holding one waits and
+                    // revisits this bucket after the next round.
+                    if (parked != Nodes::kNone) {
+                        waiting = true;
+                        continue;
+                    }
+                    parked = ref;
+                } else {
+                    t.scan(ref, q, best);
                 }
-                parked = ref;
-            } else if (ref < n - 1) {
-                const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
-                float rec[R];
-#pragma unroll
-                for (int v = 0; v < R / 4; ++v) {
-                    const float4 x = r4[v];
-                    rec[4 * v] = x.x;
-                    rec[4 * v + 1] = x.y;
-                    rec[4 * v + 2] = x.z;
-                    rec[4 * v + 3] = x.w;
-                }
-                const float ld = box_distance<D>(q, rec);
-                const float rd = box_distance<D>(q, rec + 2 * D);
-                const int32_t lref = __float_as_int(rec[4 * D]);
-                const int32_t rref = __float_as_int(rec[4 * D + 1]);
+            } else if (t.is_internal(ref)) {
+                float ld, rd;
+                int32_t lref, rref;
+                t.children(ref, q, ld, rd, lref, rref);
                 const bool left_near = ld <= rd;
                 const int32_t near_ref = left_near ? lref : rref;
                 const int32_t far_ref = left_near ? rref : lref;
@@ -508,29 +473,17 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
             }
             // One step of the resume walk from `ref`, the last node entered
             // (its subtree is finished), to its parent.
-            // An internal node's parent is in its own row; a bucket's, in the
-            // last word of the row where it starts.
-            const int32_t par = __float_as_int(
-                recs[static_cast<int64_t>(ref >= 0 ? ref : ref & 0x0fffffff) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
-            if (par < 0 || par >= n - 1) {
-                done = true;  // the root (or a link outside the cloud, which a well-formed accel never holds)
+            const int32_t par = t.parent(ref);
+            if (par < 0) {
+                done = true;
                 continue;
             }
-            const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(par) * R);
-            float rec[R];
-#pragma unroll
-            for (int v = 0; v < R / 4; ++v) {
-                const float4 x = r4[v];
-                rec[4 * v] = x.x;
-                rec[4 * v + 1] = x.y;
-                rec[4 * v + 2] = x.z;
-                rec[4 * v + 3] = x.w;
-            }
-            const float ld = box_distance<D>(q, rec);
-            const float rd = box_distance<D>(q, rec + 2 * D);
+            float ld, rd;
+            int32_t lref, rref;
+            t.children(par, q, ld, rd, lref, rref);
             const bool left_near = ld <= rd;
-            const int32_t near_ref = __float_as_int(rec[4 * D + (left_near ? 0 : 1)]);
-            const int32_t far_ref = __float_as_int(rec[4 * D + (left_near ? 1 : 0)]);
+            const int32_t near_ref = left_near ? lref : rref;
+            const int32_t far_ref = left_near ? rref : lref;
             const float far_d = left_near ? rd : ld;
             if (ref == near_ref && far_d <= worst) {
                 ref = far_ref;  // a dropped far child: resume there
@@ -543,60 +496,130 @@ __global__ __launch_bounds__(kAccelBlock) void knn_accel_kernel(KnnArgs a) {
         }
         stack.pop(nd, ref);
     }
+}
+
+// One query per lane over the implicit tree (kAccel false) or the accel;
+// the body of both kernels below.
+//
+// Tile order: consecutive work-groups land on different XCDs, each with its
+// own L2; logical tile t = (block % 8) * (grid / 8) + block / 8 gives every
+// XCD a contiguous run of Morton-ordered queries, so one XCD's L2 serves a
+// compact region of the tree.
+template <int D, int K, bool kOrdered, bool kRagged, bool kAccel>
+__device__ __forceinline__ void knn_query(const KnnArgs& a) {
+    constexpr int kLds = lds_stack_entries<D, K>();
+    __shared__ uint32_t lds_refs[kLds * kKnnBlock];
+    __shared__ uint16_t lds_dists[kLds * kKnnBlock];
+    const int64_t per_xcd = gridDim.x / kXcds;
+    const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    const int64_t gid = tile * kKnnBlock + threadIdx.x;
+    if (gid >= a.total_q) return;
+
+    int64_t seg, qbase, qcount, pstart, nstart;
+    int n;
+    if constexpr (kRagged) {
+        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
+        qbase = a.query_offsets[seg];
+        qcount = a.query_offsets[seg + 1] - qbase;
+        pstart = a.point_offsets[seg];
+        n = static_cast<int>(a.point_offsets[seg + 1] - pstart);
+        nstart = kAccel ? 0 : a.node_offsets[seg];
+    } else {
+        seg = gid / a.M;
+        qbase = seg * a.M;
+        qcount = a.M;
+        n = a.num_leaves;
+        pstart = seg * static_cast<int64_t>(n);
+        nstart = seg * static_cast<int64_t>(a.num_real_nodes);
+    }
+    const int64_t local = gid - qbase;
+    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
+    if (qi < 0 || qi >= qcount) return;  // a corrupt order never indexes out of range
+    const int64_t row = qbase + qi;
+    bool second = false;
+    int64_t index_offset = 0;
+    if (!kRagged && a.routes != nullptr && a.routes[row] == 0) {
+        // False route (knn_query.cu:205-217): the second structure, indices
+        // after the first's points.
+        second = true;
+        index_offset = n;
+        n = a.num_leaves2;
+        pstart = seg * static_cast<int64_t>(n);
+        nstart = seg * static_cast<int64_t>(a.num_real_nodes2);
+    }
+
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) q[d] = a.queries[row * D + d];
+
+    uint64_t best[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
+
+    RingStack<kLds> stack;
+    stack.refs = lds_refs + threadIdx.x;
+    stack.dists = lds_dists + threadIdx.x;
+    if constexpr (kAccel) {
+        const void* accel = second ? a.accel2 : a.accel;
+        const int64_t total_points = second ? a.B * static_cast<int64_t>(n) : a.total_points;
+        AccelNodes<D> t;
+        t.pts = static_cast<const float4*>(accel) + pstart;
+        t.recs = reinterpret_cast<const float*>(static_cast<const char*>(accel) + accel_points_bytes(total_points)) +
+                 pstart * AccelNodes<D>::R;
+        t.n = n;
+        traverse<true>(t, q, best, stack);
+    } else {
+        HeapNodes<D> t;
+        t.init((second ? a.node_aabbs2 : a.node_aabbs) + nstart * 2 * D,
+               (second ? a.sorted_indices2 : a.sorted_indices) + pstart, n);
+        traverse<false>(t, q, best, stack);
+    }
 
     // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
     const int64_t out_row = a.spatial_output ? qbase + local : row;
     write_results<K, D>(a, out_row, best, index_offset, pstart);
 }
 
-template <int D, int K>
-hipError_t launch_accel_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
-    // Whole XCD rounds (see knn_accel_kernel); surplus tiles exit at once.
-    const int64_t tiles = (a.total_q + kAccelBlock - 1) / kAccelBlock;
+// Separate names, so profiles tell the two traversals apart.
+template <int D, int K, bool kOrdered, bool kRagged>
+__global__ __launch_bounds__(kKnnBlock) void knn_kernel(KnnArgs a) {
+    knn_query<D, K, kOrdered, kRagged, false>(a);
+}
+
+template <int D, int K, bool kOrdered, bool kRagged>
+__global__ __launch_bounds__(kKnnBlock) void knn_accel_kernel(KnnArgs a) {
+    knn_query<D, K, kOrdered, kRagged, true>(a);
+}
+
+template <int D, int K, bool kOrdered, bool kRagged, bool kAccel>
+void launch_one(const KnnArgs& a, unsigned grid, hipStream_t stream) {
+    if constexpr (kAccel) knn_accel_kernel<D, K, kOrdered, kRagged><<<grid, kKnnBlock, 0, stream>>>(a);
+    else knn_kernel<D, K, kOrdered, kRagged><<<grid, kKnnBlock, 0, stream>>>(a);
+}
+
+template <int D, int K, bool kAccel>
+hipError_t launch_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
+    // Whole XCD rounds (see knn_query); surplus tiles exit at once.
+    const int64_t tiles = (a.total_q + kKnnBlock - 1) / kKnnBlock;
     const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
     const bool ordered = a.order != nullptr;
     if (ragged) {
-        if (ordered) knn_accel_kernel<D, K, true, true><<<grid, kAccelBlock, 0, stream>>>(a);
-        else knn_accel_kernel<D, K, false, true><<<grid, kAccelBlock, 0, stream>>>(a);
+        if (ordered) launch_one<D, K, true, true, kAccel>(a, grid, stream);
+        else launch_one<D, K, false, true, kAccel>(a, grid, stream);
     } else {
-        if (ordered) knn_accel_kernel<D, K, true, false><<<grid, kAccelBlock, 0, stream>>>(a);
-        else knn_accel_kernel<D, K, false, false><<<grid, kAccelBlock, 0, stream>>>(a);
+        if (ordered) launch_one<D, K, true, false, kAccel>(a, grid, stream);
+        else launch_one<D, K, false, false, kAccel>(a, grid, stream);
     }
     return hipGetLastError();
 }
 
-template <int D>
-hipError_t launch_accel_d(const KnnArgs& a, int K, bool ragged, hipStream_t stream) {
-    switch (K) {
-        case 4: return launch_accel_dk<D, 4>(a, ragged, stream);
-        case 8: return launch_accel_dk<D, 8>(a, ragged, stream);
-        case 16: return launch_accel_dk<D, 16>(a, ragged, stream);
-        case 32: return launch_accel_dk<D, 32>(a, ragged, stream);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-template <int D, int K>
-hipError_t launch_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
-    const unsigned grid = static_cast<unsigned>((a.total_q + kBlock - 1) / kBlock);
-    const bool ordered = a.order != nullptr;
-    if (ragged) {
-        if (ordered) knn_kernel<D, K, true, true><<<grid, kBlock, 0, stream>>>(a);
-        else knn_kernel<D, K, false, true><<<grid, kBlock, 0, stream>>>(a);
-    } else {
-        if (ordered) knn_kernel<D, K, true, false><<<grid, kBlock, 0, stream>>>(a);
-        else knn_kernel<D, K, false, false><<<grid, kBlock, 0, stream>>>(a);
-    }
-    return hipGetLastError();
-}
-
-template <int D>
+template <int D, bool kAccel>
 hipError_t launch_d(const KnnArgs& a, int K, bool ragged, hipStream_t stream) {
     switch (K) {
-        case 4: return launch_dk<D, 4>(a, ragged, stream);
-        case 8: return launch_dk<D, 8>(a, ragged, stream);
-        case 16: return launch_dk<D, 16>(a, ragged, stream);
-        case 32: return launch_dk<D, 32>(a, ragged, stream);
+        case 4: return launch_dk<D, 4, kAccel>(a, ragged, stream);
+        case 8: return launch_dk<D, 8, kAccel>(a, ragged, stream);
+        case 16: return launch_dk<D, 16, kAccel>(a, ragged, stream);
+        case 32: return launch_dk<D, 32, kAccel>(a, ragged, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -605,12 +628,12 @@ hipError_t launch_d(const KnnArgs& a, int K, bool ragged, hipStream_t stream) {
 
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream) {
     if (a.total_q == 0) return hipSuccess;
-    return D == 3 ? launch_d<3>(a, K, ragged, stream) : launch_d<2>(a, K, ragged, stream);
+    return D == 3 ? launch_d<3, false>(a, K, ragged, stream) : launch_d<2, false>(a, K, ragged, stream);
 }
 
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream) {
     if (a.total_q == 0) return hipSuccess;
-    return D == 3 ? launch_accel_d<3>(a, K, ragged, stream) : launch_accel_d<2>(a, K, ragged, stream);
+    return D == 3 ? launch_d<3, true>(a, K, ragged, stream) : launch_d<2, true>(a, K, ragged, stream);
 }
 
 }  // namespace tbvh
