@@ -9,6 +9,7 @@ HBM.  Prints one JSON line.
                     [--cpu-seconds S] [--no-cpu-baseline]
     python bench.py --published   # the reference's published latency rows
     python bench.py --extras      # spatial/routed k-NN, gather, primitive build, point order
+    python bench.py --copy-floor  # plain device copies at the build kernels' byte counts
 
 The synthetic workloads of every BASELINE config are defined here
 (``make_workload``) and shared with the parity tests.
@@ -212,7 +213,10 @@ def cpu_baseline(clouds: list, k: int, per_cloud: int = 4096, seconds: float = 2
     def pairs(samples) -> int:
         return sum(len(sel) * len(p) for sel, (p, _) in zip(samples, clouds))
 
-    probe = _query_sample(clouds[:1], 32, 97) + [[]] * (len(clouds) - 1)
+    # The probe runs on the largest cloud: on a small one the per-call cost
+    # dominates and the rate (hence the sample) comes out far too low.
+    big = max(range(len(clouds)), key=lambda b: len(clouds[b][0]))
+    probe = [_query_sample(clouds[b:b + 1], 32, 97)[0] if b == big else [] for b in range(len(clouds))]
     run(probe)  # warm-up: thread pool, allocator
     rate = pairs(probe) / max(run(probe), 1e-9)  # pairs per second
     while per_cloud > 16 and pairs(_query_sample(clouds, per_cloud, 98)) > 1.5 * rate * seconds:
@@ -441,6 +445,39 @@ def extras() -> int:
     return 0
 
 
+COPY_FLOOR_MB = (0.004, 2, 4, 8, 16, 32, 64, 128, 256, 512)
+
+
+def copy_floor() -> int:
+    """What a plain device copy reaches at the byte counts of the build
+    kernels: a copy moving `total` bytes (total / 2 read, total / 2
+    written), 200 back to back between two events, as the build's launches
+    run.  A kernel cannot beat the copy of its own bytes, so these are the
+    per-launch ceilings against which the build kernels' fractions of peak
+    are read.  One JSON line per size."""
+    dev = torch.device("cuda:0")
+    reps = 200
+    for mb in COPY_FLOOR_MB:
+        total = int(mb * 1e6) // 8 * 8
+        src = torch.ones(total // 8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / reps
+        gbs = total / (us * 1e-6) / 1e9
+        print(json.dumps({"copy_floor_total_bytes": total, "us_per_copy": round(us, 3),
+                          "gb_per_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+        del src, dst
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -460,6 +497,8 @@ def main() -> int:
                     help="instead: time the reference's published latency rows with its protocol")
     ap.add_argument("--extras", action="store_true",
                     help="instead: time the rows either side of the path (spatial, routed, gather, primitives)")
+    ap.add_argument("--copy-floor", action="store_true",
+                    help="instead: time plain device copies at the build kernels' byte counts")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -473,6 +512,8 @@ def main() -> int:
         return published_latencies()
     if args.extras:
         return extras()
+    if args.copy_floor:
+        return copy_floor()
 
     import torchbvh_amd as tb
 
