@@ -314,7 +314,13 @@ int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
  * needs only the BVH's node_aabbs and sorted_indices (a caller of the
  * reference's query bindings holds nothing else): the leaf rows are the
  * points in Morton order and the root box gives the build's bounds, so it
- * writes the same bytes as tbvh_accel_build. */
+ * writes the same bytes as tbvh_accel_build.
+ * Precondition of tbvh_knn_accel*: `accel` holds what one of these builders
+ * (or tbvh_build*_with_accel) wrote for the same clouds.  Its child and
+ * parent links are followed as stored; refs outside a cloud are skipped
+ * (no read leaves the cloud's rows), but links corrupted into a cycle would
+ * keep the traversal running without end, so an accel must never be
+ * modified or taken from another BVH. */
 int tbvh_accel_size(int64_t B, int64_t total_points, int D, size_t* bytes);
 int tbvh_accel_workspace_size(int64_t B, int64_t total_points, int D, size_t* bytes);
 int tbvh_accel_build(const float* points, const int64_t* sorted_indices,

@@ -289,7 +289,10 @@ def _check_accel(op: str, accel, clouds: int, total_points: int, dim: int, devic
     """An accel tensor handed in by the caller must be a contiguous 1-D
     uint8 tensor on the queries' device, at least as large as the layout for
     these clouds: the traversal then never reads outside it (it also
-    bounds-checks every child ref and parent link against its cloud)."""
+    bounds-checks every child ref and parent link against its cloud).  Its
+    contents are not checked: it must be what this library built for these
+    clouds, unmodified (links corrupted into a cycle would keep the
+    traversal running)."""
     _require(isinstance(accel, torch.Tensor) and accel.dtype == torch.uint8 and accel.dim() == 1
              and accel.is_contiguous(), op, "accel must be a contiguous 1-D uint8 tensor")
     _require(accel.is_cuda and accel.device == device, op, "accel must be on the queries' device")
