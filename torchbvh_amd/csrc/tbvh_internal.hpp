@@ -11,7 +11,7 @@
 namespace tbvh {
 
 constexpr int kWave = 64;     // CDNA wavefront width
-constexpr int kBlock = 256;   // threads per work-group for every kernel here
+constexpr int kBlock = 256;   // default threads per work-group (kernels with other shapes say so)
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr float kSeedLo = 1.0e30f;   // bounds seeds (reference: bvh_build.cu:466-467)
