@@ -544,10 +544,10 @@ def main() -> int:
 
     def step(events=None):
         """One pass of the hot path: build (BVH + accel), query ordering,
-        traversal.  Single and batched clouds call the native ops in the
-        order ``tb.query_knn`` does, with an event between each phase (all
-        on torch's current stream, the stream the kernels are launched on);
-        ragged input goes through the public API (one event pair)."""
+        traversal.  The build goes through the public API; the query calls
+        the native ops in the order ``tb.query_knn`` does, with an event
+        between each phase (all on torch's current stream, the stream the
+        kernels are launched on)."""
         if events:
             events[0].record()
         if kind == "ragged":
@@ -557,9 +557,15 @@ def main() -> int:
         if events:
             events[1].record()
         if kind == "ragged":
-            out = tb.query_knn(bvh, qs, k, query_offsets=qoff)
+            packed = bvh._aux["packed"]
+            order = _C.morton_sort_queries_ragged(qs, qoff, packed["scene_min"], packed["scene_max"],
+                                                  bvh["batch_size"], schedule=True)
             if events:
                 events[2].record()
+            out = _C.query_knn_ragged(
+                packed["node_aabbs"], packed["sorted_indices"], bvh["batch_offsets"], packed["node_offsets"],
+                qs, qoff, order, bvh["batch_size"], D, k, accel=bvh._aux["accel"],
+                total_points=bvh._aux["host_offsets"][-1])
         else:
             one = kind == "single"
             qb = qs.unsqueeze(0) if one else qs
@@ -591,32 +597,37 @@ def main() -> int:
     ms_per_step = wall * 1e3 / args.steps
     build_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     query_ms = sum(e[1].elapsed_time(e[3]) for e in evs) / args.steps
-    if kind == "ragged":
-        sort_ms = None
-        trav_ms = sum(e[1].elapsed_time(e[3]) for e in evs) / args.steps
-    else:
-        sort_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-        trav_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+    sort_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    trav_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
 
-    full_sort_ms = None
-    if kind != "ragged":
-        # The reference binding's full Morton sort of the queries (30 / 32
-        # key bits, four passes), which query_knn replaces with the two-pass
-        # schedule; timed on its own, outside the timed region.
-        bvh, _ = step()
+    # The reference binding's full Morton sort of the queries (30 / 32 key
+    # bits, four passes; for ragged input the segmented form of its
+    # per-cloud calls), which query_knn replaces with the two-pass schedule;
+    # timed on its own, outside the timed region.
+    bvh, _ = step()
+    if kind == "ragged":
+        packed = bvh._aux["packed"]
+
+        def full_sort():
+            return _C.morton_sort_queries_ragged(qs, qoff, packed["scene_min"], packed["scene_max"],
+                                                 bvh["batch_size"])
+    else:
         one = kind == "single"
         qb = qs.unsqueeze(0) if one else qs
         smin = bvh["scene_min"].unsqueeze(0) if one else bvh["scene_min"]
         smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
-        for _ in range(2):
-            _C.morton_sort_queries_narrow(qb, smin, smax)
-        ef = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ef[0].record()
-        for _ in range(10):
-            _C.morton_sort_queries_narrow(qb, smin, smax)
-        ef[1].record()
-        torch.cuda.synchronize()
-        full_sort_ms = ef[0].elapsed_time(ef[1]) / 10
+
+        def full_sort():
+            return _C.morton_sort_queries_narrow(qb, smin, smax)
+    for _ in range(2):
+        full_sort()
+    ef = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ef[0].record()
+    for _ in range(10):
+        full_sort()
+    ef[1].record()
+    torch.cuda.synchronize()
+    full_sort_ms = ef[0].elapsed_time(ef[1]) / 10
 
     implicit_ms = None
     if kind != "ragged" and args.implicit_reps > 0:
