@@ -7,7 +7,9 @@
   stability the reference's CUB sort has, bvh_build.cu:580-594).
 * Thousands of tiny ragged clouds (and clouds without queries): every
   segment-relative offset comes from scan[d][t] - scan[d][first tile],
-  checked bit-exact against the oracle cloud by cloud.
+  checked bit-exact against the oracle cloud by cloud; and the whole k-NN
+  path over thousands of clouds, whose tree-pass groups, span work-groups
+  and traversal waves mix clouds.
 """
 
 from __future__ import annotations
@@ -81,3 +83,34 @@ def test_ragged_query_order_many_segments_some_empty():
         if a == e:
             continue
         assert_same_int(order[a:e], oracle.query_order(q[a:e], lo[b], hi[b]), f"cloud {b}")
+
+
+@pytest.mark.parametrize("k,dim", [(16, 3), (8, 2)])
+def test_ragged_knn_thousands_of_small_clouds(k, dim):
+    """Ragged k-NN through the public API (fused accel build, span kernel,
+    Hilbert schedule, accel traversal) over 2,000 clouds: mostly small ones
+    (k to 600 points, so one tree-pass group or one span work-group holds
+    many clouds), a few above one sort tile and one above a tree-pass group
+    of 256 leaves per level.  (The public API, like the reference's, wants
+    strictly increasing offsets, so every cloud has a query.)  Every cloud's
+    rows must be the oracle's, bit for bit."""
+    import torchbvh_amd as tb
+
+    print(f"ragged knn: 2000 clouds k={k} dim={dim}", flush=True)
+    rng = np.random.default_rng(7000 + k + dim)
+    counts = rng.integers(k, 601, 2000)
+    counts[[5, 700, 1500]] = [4097, 20_000, 70_000]
+    qcounts = rng.integers(1, 40, 2000)
+    qcounts[1500] = 3000
+    pts = rng.random((int(counts.sum()), dim), dtype=np.float32)
+    po = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    qo = np.concatenate(([0], np.cumsum(qcounts))).astype(np.int64)
+    # Queries near each cloud's own points (each cloud sits in [0, 1)^D).
+    q = np.concatenate([rng.random((int(m), dim), dtype=np.float32) for m in qcounts])
+    h = tb.build_bvh(dev(pts), batch_offsets=dev(po))
+    idx, dist = tb.query_knn(h, dev(q), k, query_offsets=dev(qo))
+    idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+    for b in range(len(counts)):
+        ei, ed = oracle.knn(pts[po[b]:po[b + 1]], q[qo[b]:qo[b + 1]], k)
+        assert_same_int(idx[qo[b]:qo[b + 1]], ei, f"cloud {b} indices (n={counts[b]})")
+        assert_same_f32(dist[qo[b]:qo[b + 1]], ed, f"cloud {b} distances")
