@@ -114,3 +114,26 @@ def test_ragged_knn_thousands_of_small_clouds(k, dim):
         ei, ed = oracle.knn(pts[po[b]:po[b + 1]], q[qo[b]:qo[b + 1]], k)
         assert_same_int(idx[qo[b]:qo[b + 1]], ei, f"cloud {b} indices (n={counts[b]})")
         assert_same_f32(dist[qo[b]:qo[b + 1]], ed, f"cloud {b} distances")
+
+
+@pytest.mark.parametrize("use_accel", [True, False])
+def test_batched_knn_many_equal_clouds(use_accel):
+    """Batched input of 700 equal clouds: the segment table is computed in
+    closed form by the first launch of the build and of the query ordering
+    (no planning launch), for more clouds than work-groups of some passes;
+    both traversals, every cloud against the oracle."""
+    B, n, m, k = 700, 150, 24, 8
+    print(f"batched knn: B={B} n={n} m={m} k={k} accel={use_accel}", flush=True)
+    rng = np.random.default_rng(7100 + use_accel)
+    p = rng.random((B, n, 3), dtype=np.float32)
+    q = rng.random((B, m, 3), dtype=np.float32)
+    d = _C.build_bvh_batched_cooperative(dev(p))
+    order = _C.morton_sort_queries_narrow(dev(q), d["scene_min"], d["scene_max"])
+    idx, dist = _C.query_knn_batched_cached_bounds_ordered(
+        d["node_aabbs"], d["sorted_indices"], dev(q), order, d["num_leaves"], d["num_real_nodes"], 3, k,
+        accel=None if use_accel else False)
+    idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+    for b in range(B):
+        ei, ed = oracle.knn(p[b], q[b], k)
+        assert_same_int(idx[b], ei, f"cloud {b} indices")
+        assert_same_f32(dist[b], ed, f"cloud {b} distances")
