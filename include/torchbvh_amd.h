@@ -269,7 +269,10 @@ int tbvh_morton_codes(const float* rows, int64_t B, int64_t M, int D,
  * dispatch and checks :350-417).  `order` may be NULL (queries are launched in
  * input order).  k in {4, 8, 16, 32}; num_leaves >= k.  Results are the k
  * smallest (squared distance, index) pairs in lexicographic order, so exact
- * distance ties resolve to the lower point index. */
+ * distance ties resolve to the lower point index.  The traversal makes the
+ * reference's visits in the reference's order, so it also returns the
+ * reference's rows where they depend on that order (points with a NaN
+ * coordinate, which no node box bounds). */
 int tbvh_knn(const float* node_aabbs, const int64_t* sorted_indices,
              const float* queries, const int64_t* order,
              int64_t B, int64_t M, int64_t num_leaves, int64_t num_real_nodes,
