@@ -79,6 +79,60 @@ __device__ __forceinline__ void insert_sorted(uint64_t (&best)[K], uint64_t key)
     best[0] = key_min(best[0], key);
 }
 
+// The key of an empty slot, (FLT_MAX, -1): also what a candidate that may
+// not enter the list (distance FLT_MAX, inf or NaN) becomes before a merge.
+constexpr uint64_t kEmptyKey = (static_cast<uint64_t>(0x7f7fffffu) << 32) | 0xffffffffu;
+
+__device__ __forceinline__ void key_exchange(uint64_t& lo, uint64_t& hi) {
+    const uint64_t a = lo, b = hi;
+    lo = key_min(a, b);
+    hi = key_max(a, b);
+}
+
+// Ascending sort of a bucket's candidate keys by a fixed network: the
+// optimal 12-comparator network for 6 inputs, Batcher's 19-comparator
+// odd-even merge sort for 8 (Knuth, TAOCP vol. 3, 5.3.4).
+template <int B>
+__device__ __forceinline__ void sort_candidates(uint64_t (&c)[B]) {
+    static_assert(B == 6 || B == 8, "bucket sizes are 6 (3-D) and 8 (2-D)");
+    if constexpr (B == 6) {
+        constexpr int net[12][2] = {{0, 5}, {1, 3}, {2, 4}, {1, 2}, {3, 4}, {0, 3},
+                                    {2, 5}, {0, 1}, {2, 3}, {4, 5}, {1, 2}, {3, 4}};
+#pragma unroll
+        for (int s = 0; s < 12; ++s) key_exchange(c[net[s][0]], c[net[s][1]]);
+    } else {
+        constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6},
+                                    {3, 7}, {0, 1}, {2, 3}, {4, 5}, {6, 7}, {2, 4}, {3, 5},
+                                    {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+        for (int s = 0; s < 19; ++s) key_exchange(c[net[s][0]], c[net[s][1]]);
+    }
+}
+
+// Merge a bucket's candidates into the ascending list, keeping the K
+// smallest keys: with the candidates sorted ascending, slot K - m + i takes
+// min(best[K - m + i], c[m - 1 - i]) (a bitonic half-cleaner of the list
+// against the reversed candidates), which leaves the K smallest keys of both
+// as a bitonic sequence, and log2(K) rounds of compare-exchanges sort it
+// (Batcher's bitonic merge).  The same K keys as inserting the candidates
+// one by one, for (K/2)·log2(K) + m + the sort's comparators, with every
+// lane of the wave busy: one insertion per accepted candidate ran once per
+// candidate slot for the whole wave whenever any lane accepted that slot.
+template <int K, int B>
+__device__ __forceinline__ void merge_candidates(uint64_t (&best)[K], uint64_t (&c)[B]) {
+    sort_candidates<B>(c);
+    constexpr int m = K < B ? K : B;
+#pragma unroll
+    for (int i = 0; i < m; ++i) best[K - m + i] = key_min(best[K - m + i], c[m - 1 - i]);
+#pragma unroll
+    for (int h = K / 2; h >= 1; h /= 2) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if ((i & h) == 0) key_exchange(best[i], best[i + h]);
+        }
+    }
+}
+
 // Writes one result row: the K (index, distance) pairs and, when asked,
 // the neighbours' source rows.  `pstart` is the cloud's first point row,
 // `index_offset` what the routed traversal adds to false-route indices.
@@ -268,19 +322,18 @@ struct AccelNodes {
         const int count = ((ref >> 28) & 7) + 1;
         if (first + count > n) return;  // a corrupt ref never reads outside the cloud
         constexpr int kBucket = accel_bucket<D>();
+        // Every slot loads (past the bucket: a clamped row of this cloud,
+        // masked below), so the loads issue together.
         float4 p[kBucket];
 #pragma unroll
-        for (int j = 0; j < kBucket; ++j) {
-            p[j] = j < count ? pts[first + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+        for (int j = 0; j < kBucket; ++j) p[j] = pts[min(first + j, n - 1)];
+        uint64_t c[kBucket];
 #pragma unroll
         for (int j = 0; j < kBucket; ++j) {
-            if (j < count) {
-                const float d = point_distance<D>(q, p[j]);
-                const uint64_t key = candidate_key(d, __float_as_uint(p[j].w));
-                if (d < kFar && key < best[K - 1]) insert_sorted<K>(best, key);
-            }
+            const float d = point_distance<D>(q, p[j]);
+            c[j] = j < count && d < kFar ? candidate_key(d, __float_as_uint(p[j].w)) : kEmptyKey;
         }
+        merge_candidates<K, kBucket>(best, c);
     }
 };
 
@@ -384,22 +437,26 @@ struct HeapNodes {
 // query deeper than 21 entries (a 16-entry ring of 8-byte entries made
 // every query drop and measured +20% traversal time).
 //
-// Postponed buckets.  With one query per lane, the O(K) insertion into the
-// sorted list is the dominant cost, and the wave pays for it whenever any
-// lane inserts.  So a lane that reaches a bucket parks it and keeps
-// traversing; a lane that reaches a bucket while it holds one waits (one
-// parked bucket per lane: two measured 2% slower at k = 8 and no better at
-// k >= 16).
+// Postponed buckets.  With one query per lane, scoring a bucket and merging
+// its candidates into the sorted list (merge_candidates: a fixed network of
+// O(K log K) min/max) is the dominant cost, and the wave pays for it
+// whenever any lane scans.  So a lane that reaches a bucket parks it and
+// keeps traversing; a lane that reaches a bucket while it holds one waits
+// (one parked bucket per lane: two measured 2% slower at k = 8 and no
+// better at k >= 16, with one insertion per candidate).
 // At the loop head, which every lane of the wave passes each iteration, the
 // wave scans all parked buckets together once at least half of its live
-// lanes hold one, or no lane can move: the insertions then run with most
-// lanes active.  Meanwhile a lane prunes with its list's current k-th
-// distance, a valid (looser) bound, and a waiting lane re-tests its bucket
-// after the round, so results are unchanged; the end result is the k
-// smallest (distance, index) pairs whatever the order of visits.  Measured
-// on MI355X over the accel against immediate insertion: -20% at k = 16
-// (cfg2), -13% at k = 8 (cfg4); a variant that buffered candidates in LDS
-// and merged them with sorting networks was slower (fewer waves fit).
+// lanes hold one, or no lane can move: the merges then run with most lanes
+// active.  Meanwhile a lane prunes with its list's current k-th distance, a
+// valid (looser) bound, and a waiting lane re-tests its bucket after the
+// round, so results are unchanged; the end result is the k smallest
+// (distance, index) pairs whatever the order of visits.  Measured on MI355X
+// over the accel against immediate insertion (one insertion per accepted
+// candidate, then): -20% at k = 16 (cfg2), -13% at k = 8 (cfg4); a variant
+// that buffered candidates in LDS and merged them wave-wide with sorting
+// networks was slower (fewer waves fit).  The per-lane merge network in
+// place of one insertion per candidate: traversal -12% at cfg2, cfg3 and
+// cfg4, -6% at cfg5 (k = 32).
 //
 // Without kPostpone, buckets are scanned when reached, so the traversal makes
 // the reference's visits in the reference's order.  The implicit tree runs
