@@ -239,15 +239,30 @@ constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-ro
 
 // Entries of a lane's deferred-node stack, all in LDS (6 bytes each: a
 // 32-bit child ref and a 16-bit distance, in columns of stride kKnnBlock):
-// as many as the LDS budget of each (D, k) holds.  The budgets are the ones
-// measured best for the earlier 8-byte entries: 7.5 KB per work-group for
-// 3-D k = 16, 10 KB for 3-D k = 32 and 2-D k = 8, 6 KB otherwise.
+// as many as the LDS budget of each (D, k) holds.  7.5 KB per work-group for
+// 3-D k = 16 and 10 KB for 3-D k = 32, the budgets measured best for the
+// earlier 8-byte entries (a 17-entry ring at 3-D k = 16 measured +13%
+// traversal at cfg2: resume walks); 2-D k = 8 (cfg4) takes 15 entries, 5.6
+// KB, so that 7 one-wave work-groups fit per SIMD (see knn_waves_per_simd;
+// cfg4 traversal with 17 / 15 / 13 entries at 6 / 7 / 8 waves: 1.030 /
+// 1.010 / 1.020 ms); 6 KB otherwise.
 template <int D, int K>
 constexpr int lds_stack_entries() {
-    if (D == 2 && K == 8) return 26;
+    if (D == 2 && K == 8) return 15;
     if (D == 3 && K >= 32) return 26;
     if (D == 3 && K >= 16) return 20;
     return 16;
+}
+
+// Waves per SIMD the compiler must leave room for (at most 512 / waves
+// VGPRs per lane), where the LDS ring allows that many and the kernel fits
+// without spilling: 2-D k = 8 fits 72 VGPRs, so 7 waves (cfg4 traversal
+// 1.115 -> 1.010 ms with the 15-entry ring).  Elsewhere the compiler's own
+// choice: capping 3-D k = 16 at 80 measured +2% at cfg2 (the ring's LDS
+// holds it at 5 waves anyway), and 3-D k = 32 spills at 128.
+template <int D, int K>
+constexpr int knn_waves_per_simd() {
+    return D == 2 && K == 8 ? 7 : 1;
 }
 
 // Bounded deferred-node stack of one lane: a ring of L entries in LDS.  An
@@ -588,7 +603,57 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
 // own L2; logical tile t = (block % 8) * (grid / 8) + block / 8 gives every
 // XCD a contiguous run of Morton-ordered queries, so one XCD's L2 serves a
 // compact region of the tree.
-template <int D, int K, bool kOrdered, bool kRagged, bool kAccel>
+// Where query `gid` of the launch reads and writes: its cloud, its input row
+// and output row, and the structure it searches.
+struct QueryLoc {
+    int64_t row;           // input row (queries), -1 for a corrupt order entry
+    int64_t out_row;       // result row
+    int64_t pstart;        // the cloud's first point row
+    int64_t nstart;        // the cloud's first node row (implicit tree)
+    int64_t index_offset;  // added to result indices (false route)
+    int n;                 // the cloud's points
+    bool second;           // false route: the second structure
+};
+
+template <bool kOrdered, bool kRagged, bool kRouted, bool kAccel>
+__device__ __forceinline__ QueryLoc locate(const KnnArgs& a, int64_t gid) {
+    QueryLoc l;
+    int64_t seg, qbase, qcount;
+    if constexpr (kRagged) {
+        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
+        qbase = a.query_offsets[seg];
+        qcount = a.query_offsets[seg + 1] - qbase;
+        l.pstart = a.point_offsets[seg];
+        l.n = static_cast<int>(a.point_offsets[seg + 1] - l.pstart);
+        l.nstart = kAccel ? 0 : a.node_offsets[seg];
+    } else {
+        seg = gid / a.M;
+        qbase = seg * a.M;
+        qcount = a.M;
+        l.n = a.num_leaves;
+        l.pstart = seg * static_cast<int64_t>(l.n);
+        l.nstart = seg * static_cast<int64_t>(a.num_real_nodes);
+    }
+    const int64_t local = gid - qbase;
+    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
+    l.row = qi < 0 || qi >= qcount ? -1 : qbase + qi;  // a corrupt order never indexes out of range
+    // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
+    l.out_row = a.spatial_output ? gid : l.row;
+    l.second = false;
+    l.index_offset = 0;
+    if (kRouted && l.row >= 0 && a.routes[l.row] == 0) {
+        // False route (knn_query.cu:205-217): the second structure, indices
+        // after the first's points.
+        l.second = true;
+        l.index_offset = l.n;
+        l.n = a.num_leaves2;
+        l.pstart = seg * static_cast<int64_t>(l.n);
+        l.nstart = seg * static_cast<int64_t>(a.num_real_nodes2);
+    }
+    return l;
+}
+
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel>
 __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     constexpr int kLds = lds_stack_entries<D, K>();
     __shared__ uint32_t lds_refs[kLds * kKnnBlock];
@@ -597,43 +662,12 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     const int64_t gid = tile * kKnnBlock + threadIdx.x;
     if (gid >= a.total_q) return;
-
-    int64_t seg, qbase, qcount, pstart, nstart;
-    int n;
-    if constexpr (kRagged) {
-        seg = find_segment([&](int i) { return a.query_offsets[i]; }, static_cast<int>(a.B), gid);
-        qbase = a.query_offsets[seg];
-        qcount = a.query_offsets[seg + 1] - qbase;
-        pstart = a.point_offsets[seg];
-        n = static_cast<int>(a.point_offsets[seg + 1] - pstart);
-        nstart = kAccel ? 0 : a.node_offsets[seg];
-    } else {
-        seg = gid / a.M;
-        qbase = seg * a.M;
-        qcount = a.M;
-        n = a.num_leaves;
-        pstart = seg * static_cast<int64_t>(n);
-        nstart = seg * static_cast<int64_t>(a.num_real_nodes);
-    }
-    const int64_t local = gid - qbase;
-    const int64_t qi = kOrdered ? a.order[qbase + local] : local;
-    if (qi < 0 || qi >= qcount) return;  // a corrupt order never indexes out of range
-    const int64_t row = qbase + qi;
-    bool second = false;
-    int64_t index_offset = 0;
-    if (!kRagged && a.routes != nullptr && a.routes[row] == 0) {
-        // False route (knn_query.cu:205-217): the second structure, indices
-        // after the first's points.
-        second = true;
-        index_offset = n;
-        n = a.num_leaves2;
-        pstart = seg * static_cast<int64_t>(n);
-        nstart = seg * static_cast<int64_t>(a.num_real_nodes2);
-    }
+    const QueryLoc in = locate<kOrdered, kRagged, kRouted, kAccel>(a, gid);
+    if (in.row < 0) return;
 
     float q[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d) q[d] = a.queries[row * D + d];
+    for (int d = 0; d < D; ++d) q[d] = a.queries[in.row * D + d];
 
     uint64_t best[K];
 #pragma unroll
@@ -643,41 +677,48 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     stack.refs = lds_refs + threadIdx.x;
     stack.dists = lds_dists + threadIdx.x;
     if constexpr (kAccel) {
-        const void* accel = second ? a.accel2 : a.accel;
-        const int64_t total_points = second ? a.B * static_cast<int64_t>(n) : a.total_points;
+        const void* accel = in.second ? a.accel2 : a.accel;
+        const int64_t total_points = in.second ? a.B * static_cast<int64_t>(in.n) : a.total_points;
         AccelNodes<D> t;
-        t.pts = static_cast<const float4*>(accel) + pstart;
+        t.pts = static_cast<const float4*>(accel) + in.pstart;
         t.recs = reinterpret_cast<const float*>(static_cast<const char*>(accel) + accel_points_bytes(total_points)) +
-                 pstart * AccelNodes<D>::R;
-        t.n = n;
+                 in.pstart * AccelNodes<D>::R;
+        t.n = in.n;
         traverse<true>(t, q, best, stack);
     } else {
         HeapNodes<D> t;
-        t.init((second ? a.node_aabbs2 : a.node_aabbs) + nstart * 2 * D,
-               (second ? a.sorted_indices2 : a.sorted_indices) + pstart, n);
+        t.init((in.second ? a.node_aabbs2 : a.node_aabbs) + in.nstart * 2 * D,
+               (in.second ? a.sorted_indices2 : a.sorted_indices) + in.pstart, in.n);
         traverse<false>(t, q, best, stack);
     }
 
-    // Spatial output (knn_query.cu:147-148) keeps the launch (Morton) order.
-    const int64_t out_row = a.spatial_output ? qbase + local : row;
-    write_results<K, D>(a, out_row, best, index_offset, pstart);
+    // The output location is derived again from the lane's position (the
+    // work-group is one wave, so the lane id is threadIdx.x) instead of being
+    // held in registers through the traversal: the compiler cannot tell the
+    // two apart, so nothing of the first derivation stays live.
+    const int64_t gid_out = tile * kKnnBlock + __lane_id();
+    const QueryLoc out = locate<kOrdered, kRagged, kRouted, kAccel>(a, gid_out);
+    write_results<K, D>(a, out.out_row, best, out.index_offset, out.pstart);
 }
 
 // Separate names, so profiles tell the two traversals apart.
-template <int D, int K, bool kOrdered, bool kRagged>
+// The routed traversal (two structures, chosen per query) has kernels of its
+// own, so the plain ones carry none of its per-lane state.
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted>
 __global__ __launch_bounds__(kKnnBlock) void knn_kernel(KnnArgs a) {
-    knn_query<D, K, kOrdered, kRagged, false>(a);
+    knn_query<D, K, kOrdered, kRagged, kRouted, false>(a);
 }
 
-template <int D, int K, bool kOrdered, bool kRagged>
-__global__ __launch_bounds__(kKnnBlock) void knn_accel_kernel(KnnArgs a) {
-    knn_query<D, K, kOrdered, kRagged, true>(a);
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted>
+__global__ __launch_bounds__(kKnnBlock) __attribute__((amdgpu_waves_per_eu(knn_waves_per_simd<D, K>()))) void knn_accel_kernel(
+    KnnArgs a) {
+    knn_query<D, K, kOrdered, kRagged, kRouted, true>(a);
 }
 
-template <int D, int K, bool kOrdered, bool kRagged, bool kAccel>
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel>
 void launch_one(const KnnArgs& a, unsigned grid, hipStream_t stream) {
-    if constexpr (kAccel) knn_accel_kernel<D, K, kOrdered, kRagged><<<grid, kKnnBlock, 0, stream>>>(a);
-    else knn_kernel<D, K, kOrdered, kRagged><<<grid, kKnnBlock, 0, stream>>>(a);
+    if constexpr (kAccel) knn_accel_kernel<D, K, kOrdered, kRagged, kRouted><<<grid, kKnnBlock, 0, stream>>>(a);
+    else knn_kernel<D, K, kOrdered, kRagged, kRouted><<<grid, kKnnBlock, 0, stream>>>(a);
 }
 
 template <int D, int K, bool kAccel>
@@ -686,12 +727,16 @@ hipError_t launch_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
     const int64_t tiles = (a.total_q + kKnnBlock - 1) / kKnnBlock;
     const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
     const bool ordered = a.order != nullptr;
-    if (ragged) {
-        if (ordered) launch_one<D, K, true, true, kAccel>(a, grid, stream);
-        else launch_one<D, K, false, true, kAccel>(a, grid, stream);
+    if (a.routes != nullptr) {
+        // Routed launches are batched and always ordered (the routed sort).
+        if (ragged || !ordered) return hipErrorInvalidValue;
+        launch_one<D, K, true, false, true, kAccel>(a, grid, stream);
+    } else if (ragged) {
+        if (ordered) launch_one<D, K, true, true, false, kAccel>(a, grid, stream);
+        else launch_one<D, K, false, true, false, kAccel>(a, grid, stream);
     } else {
-        if (ordered) launch_one<D, K, true, false, kAccel>(a, grid, stream);
-        else launch_one<D, K, false, false, kAccel>(a, grid, stream);
+        if (ordered) launch_one<D, K, true, false, false, kAccel>(a, grid, stream);
+        else launch_one<D, K, false, false, false, kAccel>(a, grid, stream);
     }
     return hipGetLastError();
 }
