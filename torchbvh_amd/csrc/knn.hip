@@ -231,6 +231,38 @@ __device__ __forceinline__ float point_distance(const float* q, const float4 p) 
     return s;
 }
 
+// Two parked buckets of 6 (3-D) merged at once: each half sorted by the
+// 6-input network, then Batcher's odd-even merge of the two sorted halves
+// (the 8 + 8 merge with the padding's comparators removed: 17 exchanges),
+// after which sorted rank r is in register kRank12[r].  One merge of 12
+// candidates into the list, in place of two merges of 6: at K = 32, 41 +
+// 12 + 76 exchanges against 2 x (12 + 6 + 66).
+constexpr int kMerge66[17][2] = {{0, 6}, {4, 10}, {4, 6}, {2, 8}, {2, 4}, {8, 6}, {1, 7}, {5, 11}, {5, 7},
+                                 {3, 9}, {3, 5}, {9, 7}, {1, 2}, {3, 4}, {5, 8}, {9, 6}, {7, 10}};
+constexpr int kRank12[12] = {0, 1, 2, 3, 4, 5, 8, 9, 6, 7, 10, 11};
+
+template <int K>
+__device__ __forceinline__ void merge_candidates12(uint64_t (&best)[K], uint64_t (&c)[12]) {
+    uint64_t (&lo)[6] = *reinterpret_cast<uint64_t (*)[6]>(&c[0]);
+    uint64_t (&hi)[6] = *reinterpret_cast<uint64_t (*)[6]>(&c[6]);
+    sort_candidates<6>(lo);
+    sort_candidates<6>(hi);
+#pragma unroll
+    for (int s = 0; s < 17; ++s) key_exchange(c[kMerge66[s][0]], c[kMerge66[s][1]]);
+    constexpr int m = K < 12 ? K : 12;
+    constexpr MergePlan<K, m> plan{};
+#pragma unroll
+    for (int i = 0; i < m; ++i) best[K - m + i] = key_min(best[K - m + i], c[kRank12[m - 1 - i]]);
+#pragma unroll
+    for (int s = 0; s < MergePlan<K, m>::kStages; ++s) {
+        const int h = K >> (s + 1);
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if ((i & h) == 0 && ((plan.needed[s] >> i) & 1)) key_exchange(best[i], best[i + h]);
+        }
+    }
+}
+
 // One wave per work-group: measured against 256 threads, -3.5% at cfg2 and
 // -14% at cfg5, whose waves differ most in cost (finer-grained balancing
 // over the CUs); 128 falls between, 512 is 13-24% slower.
@@ -317,6 +349,7 @@ struct RingStack {
 // accel_bucket<D>() consecutive Morton-ordered points, loaded together.
 template <int D>
 struct AccelNodes {
+    static constexpr int kDims = D;
     static constexpr int R = 4 * D + 4;
     static constexpr int32_t kNone = 0;  // bucket refs are negative
     const float4* pts;                   // this cloud's points
@@ -376,6 +409,30 @@ struct AccelNodes {
         }
         merge_candidates<K, kBucket>(best, c);
     }
+
+    // Both parked buckets of a lane in one merge (3-D: 6 + 6 candidates);
+    // `ref2` is kNone when the lane holds one.
+    template <int K>
+    __device__ __forceinline__ void scan2(int32_t ref1, int32_t ref2, const float* q, uint64_t (&best)[K]) const {
+        static_assert(accel_bucket<D>() == 6, "two-bucket merges are for 6-point buckets");
+        uint64_t c[12];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int32_t ref = b == 0 ? ref1 : ref2;
+            const int first = ref & 0x0fffffff;
+            int count = ((ref >> 28) & 7) + 1;
+            if (ref == kNone || first + count > n) count = 0;  // absent, or a corrupt ref: no candidates
+            float4 p[6];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) p[j] = pts[min(first + j, n - 1)];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) {
+                const float d = point_distance<D>(q, p[j]);
+                c[6 * b + j] = j < count && d < kFar ? candidate_key(d, __float_as_uint(p[j].w)) : kEmptyKey;
+            }
+        }
+        merge_candidates12<K>(best, c);
+    }
 };
 
 // The reference's implicit tree (implicit_tree.cuh:26-127): refs are heap
@@ -389,6 +446,7 @@ struct AccelNodes {
 // popped straight after), with no stack entry.
 template <int D>
 struct HeapNodes {
+    static constexpr int kDims = D;
     static constexpr int32_t kNone = -1;
     const float* nodes;     // this tree's rows of 2 * D floats
     const int64_t* sorted;  // this cloud's sorted indices
@@ -497,7 +555,11 @@ struct HeapNodes {
 // that buffered candidates in LDS and merged them wave-wide with sorting
 // networks was slower (fewer waves fit).  The per-lane merge network in
 // place of one insertion per candidate: traversal -12% at cfg2, cfg3 and
-// cfg4, -6% at cfg5 (k = 32).
+// cfg4, -6% at cfg5 (k = 32).  3-D k = 32 parks two buckets per lane and
+// merges their 12 candidates at once (merge_candidates12), flushing when a
+// quarter of the live lanes hold two: half the flushes and 129 exchanges per
+// 12 candidates instead of 168; cfg5 traversal 22.5 -> 20.4 ms, at the same
+// 3 waves per SIMD.  At k = 16 two slots measured +1.5-2% (cfg2, cfg3).
 //
 // Without kPostpone, buckets are scanned when reached, so the traversal makes
 // the reference's visits in the reference's order.  The implicit tree runs
@@ -506,9 +568,12 @@ struct HeapNodes {
 // reference's result.
 template <bool kPostpone, int K, int L, class Nodes>
 __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_t (&best)[K], RingStack<L>& stack) {
+    // 3-D k = 32 parks two buckets per lane and merges them together.
+    constexpr bool kTwoSlots = kPostpone && K >= 32 && Nodes::kDims == 3;
     int32_t ref = t.root();
     float nd = 0.0f;
     int32_t parked = Nodes::kNone;
+    int32_t parked2 = Nodes::kNone;
     bool waiting = false;
     bool done = false;
 
@@ -522,9 +587,18 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
         if (holding != 0) {
             const uint64_t live = __ballot(true);
             const uint64_t movable = __ballot(!waiting && !done);
-            if (movable == 0 || __popcll(live) <= 2 * __popcll(holding)) {
-                if (parked != Nodes::kNone) t.scan(parked, q, best);
+            const uint64_t full = kTwoSlots ? __ballot(parked2 != Nodes::kNone) : holding;
+            // One slot: flush once half the live lanes hold a bucket; two
+            // slots: once a quarter of them hold two (cfg5 traversal with
+            // 1/2, 3/8, 5/16, 1/4: 21.3, 20.6, 20.4, 20.4 ms).
+            constexpr int kNum = 1, kDen = kTwoSlots ? 4 : 2;
+            if (movable == 0 || kNum * __popcll(live) <= kDen * __popcll(full)) {
+                if (parked != Nodes::kNone) {
+                    if constexpr (kTwoSlots) t.scan2(parked, parked2, q, best);
+                    else t.scan(parked, q, best);
+                }
                 parked = Nodes::kNone;
+                parked2 = Nodes::kNone;
                 waiting = false;
             }
         }
@@ -537,13 +611,16 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
         if (nd <= worst) {
             if (t.is_bucket(ref)) {
                 if constexpr (kPostpone) {
-                    // Park the bucket; a lane already holding one waits and
+                    // Park the bucket; a lane whose slots are taken waits and
                     // revisits this bucket after the next round.
-                    if (parked != Nodes::kNone) {
+                    if (parked == Nodes::kNone) {
+                        parked = ref;
+                    } else if (kTwoSlots && parked2 == Nodes::kNone) {
+                        parked2 = ref;
+                    } else {
                         waiting = true;
                         continue;
                     }
-                    parked = ref;
                 } else {
                     t.scan(ref, q, best);
                 }
