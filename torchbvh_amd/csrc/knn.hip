@@ -396,11 +396,16 @@ struct AccelNodes {
         const int count = ((ref >> 28) & 7) + 1;
         if (first + count > n) return;  // a corrupt ref never reads outside the cloud
         constexpr int kBucket = accel_bucket<D>();
-        // Every slot loads (past the bucket: a clamped row of this cloud,
-        // masked below), so the loads issue together.
+        // Every slot loads, so the loads issue together from one address.
+        // Slots past the bucket (masked below) read at most kBucket - 1 rows
+        // past `first + count - 1 < n`: the next cloud's points or, after the
+        // last cloud, the points area's padding to 256 bytes and the record
+        // rows behind it (>= 48 bytes per point), so every read stays inside
+        // the accel buffer (accel_bytes).
+        const float4* b = pts + first;
         float4 p[kBucket];
 #pragma unroll
-        for (int j = 0; j < kBucket; ++j) p[j] = pts[min(first + j, n - 1)];
+        for (int j = 0; j < kBucket; ++j) p[j] = b[j];
         uint64_t c[kBucket];
 #pragma unroll
         for (int j = 0; j < kBucket; ++j) {
@@ -419,12 +424,17 @@ struct AccelNodes {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int32_t ref = b == 0 ? ref1 : ref2;
-            const int first = ref & 0x0fffffff;
+            int first = ref & 0x0fffffff;
             int count = ((ref >> 28) & 7) + 1;
-            if (ref == kNone || first + count > n) count = 0;  // absent, or a corrupt ref: no candidates
+            if (ref == kNone || first + count > n) {
+                first = 0;  // absent, or a corrupt ref: no candidates
+                count = 0;
+            }
+            // Past the bucket: rows inside the accel buffer, as in scan.
+            const float4* row = pts + first;
             float4 p[6];
 #pragma unroll
-            for (int j = 0; j < 6; ++j) p[j] = pts[min(first + j, n - 1)];
+            for (int j = 0; j < 6; ++j) p[j] = row[j];
 #pragma unroll
             for (int j = 0; j < 6; ++j) {
                 const float d = point_distance<D>(q, p[j]);
