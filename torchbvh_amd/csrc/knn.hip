@@ -274,13 +274,13 @@ constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-ro
 // as many as the LDS budget of each (D, k) holds.  7.5 KB per work-group for
 // 3-D k = 16 and 10 KB for 3-D k = 32, the budgets measured best for the
 // earlier 8-byte entries (a 17-entry ring at 3-D k = 16 measured +13%
-// traversal at cfg2: resume walks); 2-D k = 8 (cfg4) takes 15 entries, 5.6
-// KB, so that 7 one-wave work-groups fit per SIMD (see knn_waves_per_simd;
-// cfg4 traversal with 17 / 15 / 13 entries at 6 / 7 / 8 waves: 1.030 /
-// 1.010 / 1.020 ms); 6 KB otherwise.
+// traversal at cfg2: resume walks); 2-D k = 8 (cfg4) takes 13 entries, 5
+// KB, so that 8 one-wave work-groups fit per SIMD (see knn_waves_per_simd;
+// cfg4 traversal with 17 / 15 / 13 entries at 6 / 7 / 8 waves: 0.965 /
+// 0.935 / 0.920 ms); 6 KB otherwise.
 template <int D, int K>
 constexpr int lds_stack_entries() {
-    if (D == 2 && K == 8) return 15;
+    if (D == 2 && K == 8) return 13;
     if (D == 3 && K >= 32) return 26;
     if (D == 3 && K >= 16) return 20;
     return 16;
@@ -288,13 +288,14 @@ constexpr int lds_stack_entries() {
 
 // Waves per SIMD the compiler must leave room for (at most 512 / waves
 // VGPRs per lane), where the LDS ring allows that many and the kernel fits
-// without spilling: 2-D k = 8 fits 72 VGPRs, so 7 waves (cfg4 traversal
-// 1.115 -> 1.010 ms with the 15-entry ring).  Elsewhere the compiler's own
+// without spilling: 2-D k = 8 fits 64 VGPRs, so 8 waves (cfg4 traversal
+// 1.115 -> 0.920 ms with the 13-entry ring, together with the unclamped
+// bucket loads).  Elsewhere the compiler's own
 // choice: capping 3-D k = 16 at 80 measured +2% at cfg2 (the ring's LDS
 // holds it at 5 waves anyway), and 3-D k = 32 spills at 128.
 template <int D, int K>
 constexpr int knn_waves_per_simd() {
-    return D == 2 && K == 8 ? 7 : 1;
+    return D == 2 && K == 8 ? 8 : 1;
 }
 
 // Bounded deferred-node stack of one lane: a ring of L entries in LDS.  An
