@@ -117,3 +117,58 @@ def test_implicit_tree_ring_overflow(k, dim, n):
     ei, ed = oracle.knn_brute(pts, q, k)
     assert_same_int(idx[0].cpu().numpy(), ei, "indices")
     assert_same_f32(dist[0].cpu().numpy(), ed, "distances")
+
+
+# The 3-D k = 16 accel traversal has two ring layouts: compact 5-byte entries
+# (24-bit refs) when every cloud has at most 2^20 points, full 6-byte entries
+# above that.  The tests above run the compact one; these cross the limit.
+COMPACT_CLOUD = 1 << 20
+
+
+def test_shell_above_compact_limit_full_ring():
+    """Shell cloud of 2^20 + 4096 points (full layout) queried from the
+    centre: every lane's ring overflows and resumes through parent links."""
+    print("stack: shell above the compact-ring limit, 3-D k=16", flush=True)
+    rng = np.random.default_rng(1101)
+    pts = shell(rng, COMPACT_CLOUD + 4096, 3)
+    q = np.concatenate([np.full((64, 3), 0.5, np.float32),
+                        (0.5 + 0.01 * rng.standard_normal((64, 3))).astype(np.float32)])
+    check(pts, q, 16)
+
+
+@pytest.mark.parametrize("n", [COMPACT_CLOUD, COMPACT_CLOUD + 1])
+def test_uniform_at_the_compact_limit(n):
+    """Exactly 2^20 points (compact ring, the widest 20-bit bucket starts and
+    node indices) and one more (full ring), 4096 queries, 3-D k = 16."""
+    print(f"stack: uniform n={n} 3-D k=16", flush=True)
+    rng = np.random.default_rng(1200 + n % 7)
+    pts = rng.random((n, 3), dtype=np.float32)
+    q = np.concatenate([rng.random((4032, 3), dtype=np.float32),
+                        pts[-64:] + np.float32(1e-4)]).astype(np.float32)
+    with tb.BVH(dev(pts)) as bvh:
+        idx, dist = bvh.knn(dev(q), 16)
+    torch.cuda.synchronize()
+    ei, ed = oracle.knn(pts, q, 16)
+    assert_same_int(idx.cpu().numpy(), ei, "indices")
+    assert_same_f32(dist.cpu().numpy(), ed, "distances")
+
+
+def test_ragged_total_above_compact_limit():
+    """Ragged 3-D k = 16 call whose clouds are each below 2^20 points but
+    whose total is above: the launch takes the full ring (the limit applies
+    to the call's total, which bounds every cloud)."""
+    print("stack: ragged total above the compact-ring limit", flush=True)
+    rng = np.random.default_rng(1301)
+    clouds = [rng.random((600_000, 3), dtype=np.float32), shell(rng, 500_000, 3)]
+    queries = [rng.random((1000, 3), dtype=np.float32),
+               np.concatenate([np.full((64, 3), 0.5, np.float32), rng.random((500, 3), dtype=np.float32)])]
+    pts = np.concatenate(clouds)
+    q = np.concatenate(queries)
+    po = np.concatenate(([0], np.cumsum([len(c) for c in clouds]))).astype(np.int64)
+    qo = np.concatenate(([0], np.cumsum([len(c) for c in queries]))).astype(np.int64)
+    with tb.BVH(dev(pts), batch_offsets=dev(po)) as bvh:
+        idx, dist = bvh.knn(dev(q), 16, query_offsets=dev(qo))
+    torch.cuda.synchronize()
+    ei, ed = oracle.knn_ragged(pts, po, q, qo, 16)
+    assert_same_int(idx.cpu().numpy(), ei, "indices")
+    assert_same_f32(dist.cpu().numpy(), ed, "distances")

@@ -293,9 +293,9 @@ constexpr int lds_stack_entries() {
 // bucket loads).  Elsewhere the compiler's own
 // choice: capping 3-D k = 16 at 80 measured +2% at cfg2 (the ring's LDS
 // holds it at 5 waves anyway), and 3-D k = 32 spills at 128.
-template <int D, int K>
+template <int D, int K, bool kCompact>
 constexpr int knn_waves_per_simd() {
-    return D == 2 && K == 8 ? 8 : 1;
+    return D == 2 && K == 8 ? 8 : kCompact && D == 3 && K == 16 ? 6 : 1;
 }
 
 // Bounded deferred-node stack of one lane: a ring of L entries in LDS.  An
@@ -309,29 +309,66 @@ constexpr int knn_waves_per_simd() {
 // Nothing is lost for correctness: when the ring empties with lost_min <=
 // the k-th distance, the traversal resumes through the parent links (see
 // traverse).
-template <int L>
+//
+// Two layouts.  Full (6 bytes per entry): the 32-bit ref in `refs`, the
+// distance in `dists`.  Compact (5 bytes; accel clouds of at most
+// kCompactCloud points): the ref as a 24-bit code, an internal node as its
+// index and a bucket as 1 << 23 | (count - 1) << 20 | first, with the
+// distance and the code's low 16 bits in one word of `refs` and its high 8
+// bits in `hi`.  At 3-D k = 16 the compact ring's 20 entries take 6.4 KB,
+// so 6 work-groups fit per SIMD instead of 5 (cfg2 traversal -2.6%, cfg3
+// -1.4%).
+constexpr int64_t kCompactCloud = int64_t(1) << 20;
+
+template <int L, bool kCompact>
 struct RingStack {
     uint32_t* refs;   // this lane's column: slot i at refs[i * kKnnBlock]
-    uint16_t* dists;  // likewise
+    uint16_t* dists;  // full layout, likewise
+    uint8_t* hi;      // compact layout, likewise
     int top = 0;      // slot of the next push
     int count = 0;
     float lost_min = INFINITY;
+
+    __device__ __forceinline__ static uint32_t encode(int32_t ref) {
+        const uint32_t r = static_cast<uint32_t>(ref);
+        return ref < 0 ? 0x800000u | (((r >> 28) & 7u) << 20) | (r & 0xFFFFFu) : r;
+    }
+    __device__ __forceinline__ static int32_t decode(uint32_t c) {
+        return (c & 0x800000u) ? static_cast<int32_t>(0x80000000u | (((c >> 20) & 7u) << 28) | (c & 0xFFFFFu))
+                                : static_cast<int32_t>(c);
+    }
+    __device__ __forceinline__ float dist_at(int slot) const {
+        if constexpr (kCompact) return __uint_as_float(refs[slot * kKnnBlock] & 0xFFFF0000u);
+        else return __uint_as_float(static_cast<uint32_t>(dists[slot * kKnnBlock]) << 16);
+    }
     __device__ __forceinline__ void push(float d, int32_t ref) {
         if (count == L) {
             // Full: slot `top` holds the oldest entry.
-            lost_min = fminf(lost_min, __uint_as_float(static_cast<uint32_t>(dists[top * kKnnBlock]) << 16));
+            lost_min = fminf(lost_min, dist_at(top));
         } else {
             ++count;
         }
-        refs[top * kKnnBlock] = static_cast<uint32_t>(ref);
-        dists[top * kKnnBlock] = static_cast<uint16_t>(__float_as_uint(d) >> 16);
+        if constexpr (kCompact) {
+            const uint32_t c = encode(ref);
+            refs[top * kKnnBlock] = (__float_as_uint(d) & 0xFFFF0000u) | (c & 0xFFFFu);
+            hi[top * kKnnBlock] = static_cast<uint8_t>(c >> 16);
+        } else {
+            refs[top * kKnnBlock] = static_cast<uint32_t>(ref);
+            dists[top * kKnnBlock] = static_cast<uint16_t>(__float_as_uint(d) >> 16);
+        }
         top = top == L - 1 ? 0 : top + 1;
     }
     __device__ __forceinline__ void pop(float& d, int32_t& ref) {
         top = top == 0 ? L - 1 : top - 1;
         --count;
-        ref = static_cast<int32_t>(refs[top * kKnnBlock]);
-        d = __uint_as_float(static_cast<uint32_t>(dists[top * kKnnBlock]) << 16);
+        if constexpr (kCompact) {
+            const uint32_t w = refs[top * kKnnBlock];
+            ref = decode((static_cast<uint32_t>(hi[top * kKnnBlock]) << 16) | (w & 0xFFFFu));
+            d = __uint_as_float(w & 0xFFFF0000u);
+        } else {
+            ref = static_cast<int32_t>(refs[top * kKnnBlock]);
+            d = __uint_as_float(static_cast<uint32_t>(dists[top * kKnnBlock]) << 16);
+        }
     }
 };
 
@@ -577,8 +614,9 @@ struct HeapNodes {
 // that way: where the result does depend on the order (points with a NaN
 // coordinate, whose distances the node boxes do not bound), it is then the
 // reference's result.
-template <bool kPostpone, int K, int L, class Nodes>
-__device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_t (&best)[K], RingStack<L>& stack) {
+template <bool kPostpone, int K, int L, bool kCompact, class Nodes>
+__device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_t (&best)[K],
+                                         RingStack<L, kCompact>& stack) {
     // 3-D k = 32 parks two buckets per lane and merges them together.
     constexpr bool kTwoSlots = kPostpone && K >= 32 && Nodes::kDims == 3;
     int32_t ref = t.root();
@@ -741,11 +779,12 @@ __device__ __forceinline__ QueryLoc locate(const KnnArgs& a, int64_t gid) {
     return l;
 }
 
-template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel>
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel, bool kCompact>
 __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     constexpr int kLds = lds_stack_entries<D, K>();
     __shared__ uint32_t lds_refs[kLds * kKnnBlock];
-    __shared__ uint16_t lds_dists[kLds * kKnnBlock];
+    __shared__ uint16_t lds_dists[kCompact ? 1 : kLds * kKnnBlock];
+    __shared__ uint8_t lds_hi[kCompact ? kLds * kKnnBlock : 1];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     const int64_t gid = tile * kKnnBlock + threadIdx.x;
@@ -761,9 +800,10 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
 #pragma unroll
     for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
 
-    RingStack<kLds> stack;
+    RingStack<kLds, kCompact> stack;
     stack.refs = lds_refs + threadIdx.x;
-    stack.dists = lds_dists + threadIdx.x;
+    stack.dists = lds_dists + (kCompact ? 0 : threadIdx.x);
+    stack.hi = lds_hi + (kCompact ? threadIdx.x : 0);
     if constexpr (kAccel) {
         const void* accel = in.second ? a.accel2 : a.accel;
         const int64_t total_points = in.second ? a.B * static_cast<int64_t>(in.n) : a.total_points;
@@ -794,18 +834,18 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
 // own, so the plain ones carry none of its per-lane state.
 template <int D, int K, bool kOrdered, bool kRagged, bool kRouted>
 __global__ __launch_bounds__(kKnnBlock) void knn_kernel(KnnArgs a) {
-    knn_query<D, K, kOrdered, kRagged, kRouted, false>(a);
+    knn_query<D, K, kOrdered, kRagged, kRouted, false, false>(a);
 }
 
-template <int D, int K, bool kOrdered, bool kRagged, bool kRouted>
-__global__ __launch_bounds__(kKnnBlock) __attribute__((amdgpu_waves_per_eu(knn_waves_per_simd<D, K>()))) void knn_accel_kernel(
-    KnnArgs a) {
-    knn_query<D, K, kOrdered, kRagged, kRouted, true>(a);
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kCompact>
+__global__ __launch_bounds__(kKnnBlock) __attribute__((amdgpu_waves_per_eu(knn_waves_per_simd<D, K, kCompact>()))) void
+knn_accel_kernel(KnnArgs a) {
+    knn_query<D, K, kOrdered, kRagged, kRouted, true, kCompact>(a);
 }
 
-template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel>
+template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel, bool kCompact = false>
 void launch_one(const KnnArgs& a, unsigned grid, hipStream_t stream) {
-    if constexpr (kAccel) knn_accel_kernel<D, K, kOrdered, kRagged, kRouted><<<grid, kKnnBlock, 0, stream>>>(a);
+    if constexpr (kAccel) knn_accel_kernel<D, K, kOrdered, kRagged, kRouted, kCompact><<<grid, kKnnBlock, 0, stream>>>(a);
     else knn_kernel<D, K, kOrdered, kRagged, kRouted><<<grid, kKnnBlock, 0, stream>>>(a);
 }
 
@@ -819,6 +859,25 @@ hipError_t launch_dk(const KnnArgs& a, bool ragged, hipStream_t stream) {
         // Routed launches are batched and always ordered (the routed sort).
         if (ragged || !ordered) return hipErrorInvalidValue;
         launch_one<D, K, true, false, true, kAccel>(a, grid, stream);
+    } else if constexpr (kAccel && D == 3 && K == 16) {
+        // The compact ring (RingStack) where every cloud has at most
+        // kCompactCloud points: a ragged call's clouds share its total.
+        const bool compact = (ragged ? a.total_points : static_cast<int64_t>(a.num_leaves)) <= kCompactCloud;
+        if (compact) {
+            if (ragged) {
+                if (ordered) launch_one<D, K, true, true, false, true, true>(a, grid, stream);
+                else launch_one<D, K, false, true, false, true, true>(a, grid, stream);
+            } else {
+                if (ordered) launch_one<D, K, true, false, false, true, true>(a, grid, stream);
+                else launch_one<D, K, false, false, false, true, true>(a, grid, stream);
+            }
+        } else if (ragged) {
+            if (ordered) launch_one<D, K, true, true, false, true>(a, grid, stream);
+            else launch_one<D, K, false, true, false, true>(a, grid, stream);
+        } else {
+            if (ordered) launch_one<D, K, true, false, false, true>(a, grid, stream);
+            else launch_one<D, K, false, false, false, true>(a, grid, stream);
+        }
     } else if (ragged) {
         if (ordered) launch_one<D, K, true, true, false, kAccel>(a, grid, stream);
         else launch_one<D, K, false, true, false, kAccel>(a, grid, stream);
