@@ -358,6 +358,35 @@ struct RingStack {
         }
         top = top == L - 1 ? 0 : top + 1;
     }
+    __device__ __forceinline__ void read(int slot, float& d, int32_t& ref) const {
+        if constexpr (kCompact) {
+            const uint32_t w = refs[slot * kKnnBlock];
+            ref = decode((static_cast<uint32_t>(hi[slot * kKnnBlock]) << 16) | (w & 0xFFFFu));
+            d = __uint_as_float(w & 0xFFFF0000u);
+        } else {
+            ref = static_cast<int32_t>(refs[slot * kKnnBlock]);
+            d = __uint_as_float(static_cast<uint32_t>(dists[slot * kKnnBlock]) << 16);
+        }
+    }
+    // Pop with a one-entry look-ahead: the top two entries are read together
+    // and the top one, if already beyond `worst` (the k-th distance, which
+    // would prune it at the next test), is dropped in the same step.  The
+    // same entries are discarded as by popping twice, one loop iteration
+    // sooner.  Used by the 2-D traversals, where pruned pops take 19% of the
+    // lane slots at cfg4 (traversal -1.6%; +2.3% at cfg5 in 3-D, not used).
+    __device__ __forceinline__ void pop_lookahead(float& d, int32_t& ref, float worst) {
+        const int t1 = top == 0 ? L - 1 : top - 1;
+        const int t2 = t1 == 0 ? L - 1 : t1 - 1;
+        float d1, d2;
+        int32_t r1, r2;
+        read(t1, d1, r1);
+        read(t2, d2, r2);
+        const bool skip = count >= 2 && !(d1 <= worst);
+        top = skip ? t2 : t1;
+        count -= skip ? 2 : 1;
+        d = skip ? d2 : d1;
+        ref = skip ? r2 : r1;
+    }
     __device__ __forceinline__ void pop(float& d, int32_t& ref) {
         top = top == 0 ? L - 1 : top - 1;
         --count;
@@ -718,7 +747,8 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
             }
             continue;
         }
-        stack.pop(nd, ref);
+        if constexpr (Nodes::kDims == 2) stack.pop_lookahead(nd, ref, worst);
+        else stack.pop(nd, ref);
     }
 }
 
