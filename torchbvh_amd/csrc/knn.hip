@@ -92,20 +92,22 @@ __device__ __forceinline__ void key_exchange(uint64_t& lo, uint64_t& hi) {
 // Ascending sort of a bucket's candidate keys by a fixed network: the
 // optimal 12-comparator network for 6 inputs, Batcher's 19-comparator
 // odd-even merge sort for 8 (Knuth, TAOCP vol. 3, 5.3.4).
-template <int B>
-__device__ __forceinline__ void sort_candidates(uint64_t (&c)[B]) {
+// Sorts c[O .. O + B).
+template <int B, int O = 0, int N>
+__device__ __forceinline__ void sort_candidates(uint64_t (&c)[N]) {
     static_assert(B == 6 || B == 8, "bucket sizes are 6 (3-D) and 8 (2-D)");
+    static_assert(O + B <= N, "range inside the array");
     if constexpr (B == 6) {
         constexpr int net[12][2] = {{0, 5}, {1, 3}, {2, 4}, {1, 2}, {3, 4}, {0, 3},
                                     {2, 5}, {0, 1}, {2, 3}, {4, 5}, {1, 2}, {3, 4}};
 #pragma unroll
-        for (int s = 0; s < 12; ++s) key_exchange(c[net[s][0]], c[net[s][1]]);
+        for (int s = 0; s < 12; ++s) key_exchange(c[O + net[s][0]], c[O + net[s][1]]);
     } else {
         constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6},
                                     {3, 7}, {0, 1}, {2, 3}, {4, 5}, {6, 7}, {2, 4}, {3, 5},
                                     {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
 #pragma unroll
-        for (int s = 0; s < 19; ++s) key_exchange(c[net[s][0]], c[net[s][1]]);
+        for (int s = 0; s < 19; ++s) key_exchange(c[O + net[s][0]], c[O + net[s][1]]);
     }
 }
 
@@ -243,10 +245,8 @@ constexpr int kRank12[12] = {0, 1, 2, 3, 4, 5, 8, 9, 6, 7, 10, 11};
 
 template <int K>
 __device__ __forceinline__ void merge_candidates12(uint64_t (&best)[K], uint64_t (&c)[12]) {
-    uint64_t (&lo)[6] = *reinterpret_cast<uint64_t (*)[6]>(&c[0]);
-    uint64_t (&hi)[6] = *reinterpret_cast<uint64_t (*)[6]>(&c[6]);
-    sort_candidates<6>(lo);
-    sort_candidates<6>(hi);
+    sort_candidates<6, 0>(c);
+    sort_candidates<6, 6>(c);
 #pragma unroll
     for (int s = 0; s < 17; ++s) key_exchange(c[kMerge66[s][0]], c[kMerge66[s][1]]);
     constexpr int m = K < 12 ? K : 12;
