@@ -158,6 +158,9 @@ __device__ __forceinline__ void merge_candidates(uint64_t (&best)[K], uint64_t (
         for (int i = 0; i < K; ++i) {
             if ((i & h) == 0 && ((plan.needed[s] >> i) & 1)) key_exchange(best[i], best[i + h]);
         }
+        // At K = 32 the scheduler would otherwise start the next stage's
+        // exchanges before this one's maxima, holding up to 32 more VGPRs.
+        if constexpr (K >= 32) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -260,6 +263,9 @@ __device__ __forceinline__ void merge_candidates12(uint64_t (&best)[K], uint64_t
         for (int i = 0; i < K; ++i) {
             if ((i & h) == 0 && ((plan.needed[s] >> i) & 1)) key_exchange(best[i], best[i + h]);
         }
+        // At K = 32 the scheduler would otherwise start the next stage's
+        // exchanges before this one's maxima, holding up to 32 more VGPRs.
+        if constexpr (K >= 32) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -414,14 +420,27 @@ struct RingStack {
 // both child boxes, both child refs and its parent; a bucket (negative ref:
 // first position in the low 28 bits, count - 1 in bits 28-30) is up to
 // accel_bucket<D>() consecutive Morton-ordered points, loaded together.
-template <int D>
+//
+// With kRows, `pts` and `recs` point at the call's first cloud (one address
+// for the whole launch, held in scalar registers) and `first_row` locates
+// this cloud; without it they point at this cloud (two 64-bit addresses per
+// lane, and no add per access).  3-D k = 32 takes kRows: with the merges'
+// stage barriers it then fits 126 VGPRs, 4 waves per SIMD instead of 3
+// (cfg5 traversal 20.26 -> 17.89 ms); elsewhere kRows measured +1% (cfg2,
+// cfg3) at unchanged occupancy.
+template <int D, bool kRows>
 struct AccelNodes {
     static constexpr int kDims = D;
     static constexpr int R = 4 * D + 4;
     static constexpr int32_t kNone = 0;  // bucket refs are negative
-    const float4* pts;                   // this cloud's points
-    const float* recs;                   // this cloud's record rows
+    const float4* pts;                   // points (see above)
+    const float* recs;                   // record rows
+    int first_row;                       // kRows: this cloud's first row (rows fit in int32)
     int n;
+
+    __device__ __forceinline__ int64_t row(int r) const {
+        return kRows ? static_cast<int64_t>(first_row + r) : static_cast<int64_t>(r);
+    }
 
     __device__ __forceinline__ int32_t root() const {
         return n <= accel_bucket<D>() ? static_cast<int32_t>(0x80000000u | (static_cast<uint32_t>(n - 1) << 28))
@@ -432,7 +451,7 @@ struct AccelNodes {
 
     __device__ __forceinline__ void children(int32_t ref, const float* q, float& ld, float& rd, int32_t& lref,
                                              int32_t& rref) const {
-        const float4* r4 = reinterpret_cast<const float4*>(recs + static_cast<int64_t>(ref) * R);
+        const float4* r4 = reinterpret_cast<const float4*>(recs + row(ref) * R);
         float rec[R];
 #pragma unroll
         for (int v = 0; v < R / 4; ++v) {
@@ -453,7 +472,7 @@ struct AccelNodes {
     // nodes (which a well-formed accel never holds) ends the walk.
     __device__ __forceinline__ int32_t parent(int32_t ref) const {
         const int32_t par = __float_as_int(
-            recs[static_cast<int64_t>(ref >= 0 ? ref : ref & 0x0fffffff) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
+            recs[row(ref >= 0 ? ref : ref & 0x0fffffff) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
         return par >= 0 && par < n - 1 ? par : -1;
     }
 
@@ -469,7 +488,7 @@ struct AccelNodes {
         // last cloud, the points area's padding to 256 bytes and the record
         // rows behind it (>= 48 bytes per point), so every read stays inside
         // the accel buffer (accel_bytes).
-        const float4* b = pts + first;
+        const float4* b = pts + row(first);
         float4 p[kBucket];
 #pragma unroll
         for (int j = 0; j < kBucket; ++j) p[j] = b[j];
@@ -498,10 +517,10 @@ struct AccelNodes {
                 count = 0;
             }
             // Past the bucket: rows inside the accel buffer, as in scan.
-            const float4* row = pts + first;
+            const float4* rows = pts + row(first);
             float4 p[6];
 #pragma unroll
-            for (int j = 0; j < 6; ++j) p[j] = row[j];
+            for (int j = 0; j < 6; ++j) p[j] = rows[j];
 #pragma unroll
             for (int j = 0; j < 6; ++j) {
                 const float d = point_distance<D>(q, p[j]);
@@ -837,10 +856,14 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     if constexpr (kAccel) {
         const void* accel = in.second ? a.accel2 : a.accel;
         const int64_t total_points = in.second ? a.B * static_cast<int64_t>(in.n) : a.total_points;
-        AccelNodes<D> t;
-        t.pts = static_cast<const float4*>(accel) + in.pstart;
-        t.recs = reinterpret_cast<const float*>(static_cast<const char*>(accel) + accel_points_bytes(total_points)) +
-                 in.pstart * AccelNodes<D>::R;
+        constexpr bool kRows = K >= 32;
+        AccelNodes<D, kRows> t;
+        const float4* pts = static_cast<const float4*>(accel);
+        const float* recs =
+            reinterpret_cast<const float*>(static_cast<const char*>(accel) + accel_points_bytes(total_points));
+        t.pts = kRows ? pts : pts + in.pstart;
+        t.recs = kRows ? recs : recs + in.pstart * AccelNodes<D, kRows>::R;
+        t.first_row = kRows ? static_cast<int>(in.pstart) : 0;
         t.n = in.n;
         traverse<true>(t, q, best, stack);
     } else {
