@@ -654,8 +654,8 @@ struct HeapNodes {
 // cfg4, -6% at cfg5 (k = 32).  3-D k = 32 parks two buckets per lane and
 // merges their 12 candidates at once (merge_candidates12), flushing when a
 // quarter of the live lanes hold two: half the flushes and 129 exchanges per
-// 12 candidates instead of 168; cfg5 traversal 22.5 -> 20.4 ms, at the same
-// 3 waves per SIMD.  At k = 16 two slots measured +1.5-2% (cfg2, cfg3).
+// 12 candidates instead of 168; cfg5 traversal 22.5 -> 20.4 ms (both at 3
+// waves per SIMD).  At k = 16 two slots measured +1.5-2% (cfg2, cfg3).
 //
 // Without kPostpone, buckets are scanned when reached, so the traversal makes
 // the reference's visits in the reference's order.  The implicit tree runs
@@ -686,8 +686,9 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
             const uint64_t movable = __ballot(!waiting && !done);
             const uint64_t full = kTwoSlots ? __ballot(parked2 != Nodes::kNone) : holding;
             // One slot: flush once half the live lanes hold a bucket; two
-            // slots: once a quarter of them hold two (cfg5 traversal with
-            // 1/2, 3/8, 5/16, 1/4: 21.3, 20.6, 20.4, 20.4 ms).
+            // slots: once a quarter of them hold two (cfg5 traversal at 4
+            // waves per SIMD with 3/8, 1/4, 3/16, 1/8: 18.15, 17.90, 18.26,
+            // 18.85 ms; at 3 waves 1/2 had measured 21.3 against 20.4).
             constexpr int kNum = 1, kDen = kTwoSlots ? 4 : 2;
             if (movable == 0 || kNum * __popcll(live) <= kDen * __popcll(full)) {
                 if (parked != Nodes::kNone) {
