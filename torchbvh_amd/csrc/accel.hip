@@ -158,13 +158,10 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
 
     const float* nodes = node_aabbs + g.node_start * 2 * D;
     float* rec = records + r * R;
-    float box[2 * D];
-    range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, box);
-#pragma unroll
-    for (int k = 0; k < 2 * D; ++k) rec[k] = box[k];
-    range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
-#pragma unroll
-    for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
+    float lbox[2 * D], rbox[2 * D];
+    range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, lbox);
+    range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, rbox);
+    store_boxes<D>(rec, lbox, rbox);
     link_record<D>(records + g.start * R, i, first, gamma, last);
 }
 
@@ -232,13 +229,10 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
         if (i != 0 && last - first + 1 <= accel_bucket<D>()) continue;
         const float* nodes = node_aabbs + g.node_start * 2 * D;
         float* rec = records + (g.start + i) * R;
-        float box[2 * D];
-        range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, box);
-#pragma unroll
-        for (int c = 0; c < 2 * D; ++c) rec[c] = box[c];
-        range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, box);
-#pragma unroll
-        for (int c = 0; c < 2 * D; ++c) rec[2 * D + c] = box[c];
+        float lbox[2 * D], rbox[2 * D];
+        range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, lbox);
+        range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, rbox);
+        store_boxes<D>(rec, lbox, rbox);
         link_record<D>(records + g.start * R, i, first, gamma, last);
     }
 }

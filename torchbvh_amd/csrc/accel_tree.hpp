@@ -160,6 +160,23 @@ __device__ __forceinline__ void karras_node(const CodeView& cv, int i, int& firs
     karras_range(cv, i, ci, dir, dmin, lmax, first, last, gamma);
 }
 
+// Both child boxes of a record, as D 16-byte stores (record rows are 64 B
+// in 3-D and 48 B in 2-D from a 256-byte aligned base, so every row is
+// 16-byte aligned); one lane's row in one instruction per 16 bytes instead
+// of one per float.
+template <int D>
+__device__ __forceinline__ void store_boxes(float* rec, const float* lbox, const float* rbox) {
+    float v[4 * D];
+#pragma unroll
+    for (int c = 0; c < 2 * D; ++c) {
+        v[c] = lbox[c];
+        v[2 * D + c] = rbox[c];
+    }
+    float4* r4 = reinterpret_cast<float4*>(rec);
+#pragma unroll
+    for (int u = 0; u < D; ++u) r4[u] = make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]);
+}
+
 template <int D>
 __device__ __forceinline__ int32_t child_ref(int first, int last, int internal) {
     const int count = last - first + 1;
@@ -182,8 +199,7 @@ __device__ __forceinline__ void link_record(float* records, int i, int first, in
     float* rec = records + static_cast<int64_t>(i) * R;
     const int32_t lref = child_ref<D>(first, gamma, gamma);
     const int32_t rref = child_ref<D>(gamma + 1, last, gamma + 1);
-    rec[4 * D] = __int_as_float(lref);
-    rec[4 * D + 1] = __int_as_float(rref);
+    *reinterpret_cast<float2*>(rec + 4 * D) = make_float2(__int_as_float(lref), __int_as_float(rref));
     if (i == 0) rec[4 * D + 2] = __int_as_float(-1);
     records[static_cast<int64_t>(lref >= 0 ? lref : first) * R + 4 * D + (lref >= 0 ? 2 : 3)] = __int_as_float(i);
     records[static_cast<int64_t>(rref >= 0 ? rref : gamma + 1) * R + 4 * D + (rref >= 0 ? 2 : 3)] =

@@ -567,13 +567,10 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
                 karras_range(cv, i, ci, dir, dmin, kSubtreeLeaves, first, last, gamma);
                 if (i == 0 || last - first + 1 > accel_bucket<D>()) {
                     float* rec = out.accel_records + (rec0 + i) * R;
-                    float box[2 * D];
-                    range_box_lds<D>(s_box, width, first - g0, gamma - g0, box);
-#pragma unroll
-                    for (int k = 0; k < 2 * D; ++k) rec[k] = box[k];
-                    range_box_lds<D>(s_box, width, gamma + 1 - g0, last - g0, box);
-#pragma unroll
-                    for (int k = 0; k < 2 * D; ++k) rec[2 * D + k] = box[k];
+                    float lbox[2 * D], rbox[2 * D];
+                    range_box_lds<D>(s_box, width, first - g0, gamma - g0, lbox);
+                    range_box_lds<D>(s_box, width, gamma + 1 - g0, last - g0, rbox);
+                    store_boxes<D>(rec, lbox, rbox);
                     link_record<D>(out.accel_records + rec0 * R, i, first, gamma, last);
                 }
             }
