@@ -674,6 +674,13 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
     bool waiting = false;
     bool done = false;
 
+    // Wave priority: between flushes a wave runs a chain of dependent record
+    // loads (visit, push, pop), and its next load should issue as soon as
+    // the last one returns; a flush is a long VALU run that can yield.  So
+    // the traversal runs at priority 1 and drops to 0 for each flush's
+    // merges (traversal -2.7% at cfg2 and cfg5, -1% at cfg3, -0.5% at cfg4;
+    // 1 and 3 measured the same).
+    if constexpr (kPostpone) __builtin_amdgcn_s_setprio(1);
     // Descents `continue` straight to the loop head; this shape keeps them
     // in a tight loop (a flag-driven single loop of the same work measured
     // 2x slower).
@@ -691,6 +698,7 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
             // 18.85 ms; at 3 waves 1/2 had measured 21.3 against 20.4).
             constexpr int kNum = 1, kDen = kTwoSlots ? 4 : 2;
             if (movable == 0 || kNum * __popcll(live) <= kDen * __popcll(full)) {
+                __builtin_amdgcn_s_setprio(0);
                 if (parked != Nodes::kNone) {
                     if constexpr (kTwoSlots) t.scan2(parked, parked2, q, best);
                     else t.scan(parked, q, best);
@@ -698,6 +706,7 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
                 parked = Nodes::kNone;
                 parked2 = Nodes::kNone;
                 waiting = false;
+                __builtin_amdgcn_s_setprio(1);
             }
         }
         if (done) {
@@ -770,6 +779,7 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
         if constexpr (Nodes::kDims == 2) stack.pop_lookahead(nd, ref, worst);
         else stack.pop(nd, ref);
     }
+    if constexpr (kPostpone) __builtin_amdgcn_s_setprio(0);
 }
 
 // One query per lane over the implicit tree (kAccel false) or the accel;
