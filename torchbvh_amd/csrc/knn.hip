@@ -492,6 +492,9 @@ struct AccelNodes {
         float4 p[kBucket];
 #pragma unroll
         for (int j = 0; j < kBucket; ++j) p[j] = b[j];
+        // The loads issue at the traversal's priority; the merge runs at 0.
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
         uint64_t c[kBucket];
 #pragma unroll
         for (int j = 0; j < kBucket; ++j) {
@@ -676,10 +679,10 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
 
     // Wave priority: between flushes a wave runs a chain of dependent record
     // loads (visit, push, pop), and its next load should issue as soon as
-    // the last one returns; a flush is a long VALU run that can yield.  So
-    // the traversal runs at priority 1 and drops to 0 for each flush's
-    // merges (traversal -2.7% at cfg2 and cfg5, -1% at cfg3, -0.5% at cfg4;
-    // 1 and 3 measured the same).
+    // the last one returns; a flush's merges are a long VALU run that can
+    // yield.  So the traversal runs at priority 1 and a scan drops to 0 once
+    // its bucket loads are issued, until the flush ends (traversal -5% at
+    // cfg2, -3% at cfg3 and cfg5, -1% at cfg4; 1 and 3 measured the same).
     if constexpr (kPostpone) __builtin_amdgcn_s_setprio(1);
     // Descents `continue` straight to the loop head; this shape keeps them
     // in a tight loop (a flag-driven single loop of the same work measured
@@ -698,7 +701,11 @@ __device__ __forceinline__ void traverse(const Nodes& t, const float* q, uint64_
             // 18.85 ms; at 3 waves 1/2 had measured 21.3 against 20.4).
             constexpr int kNum = 1, kDen = kTwoSlots ? 4 : 2;
             if (movable == 0 || kNum * __popcll(live) <= kDen * __popcll(full)) {
-                __builtin_amdgcn_s_setprio(0);
+                // One slot: the scan drops the priority once its loads are
+                // issued; two slots (k = 32) drop it here (inside the
+                // two-bucket scan the drop cost the fourth wave per SIMD:
+                // cfg5 +13%).
+                if constexpr (kTwoSlots) __builtin_amdgcn_s_setprio(0);
                 if (parked != Nodes::kNone) {
                     if constexpr (kTwoSlots) t.scan2(parked, parked2, q, best);
                     else t.scan(parked, q, best);
