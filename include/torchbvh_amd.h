@@ -45,7 +45,7 @@ enum {
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define TBVH_ABI_VERSION 1
+#define TBVH_ABI_VERSION 2
 int tbvh_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -315,15 +315,25 @@ int tbvh_knn_ragged(const float* node_aabbs, const int64_t* sorted_indices,
  *   workspace     : tbvh_accel_workspace_size(B, total_points, D)
  * For the batched form total_points = B * N.  tbvh_accel_build_from_tree
  * needs only the BVH's node_aabbs and sorted_indices (a caller of the
- * reference's query bindings holds nothing else): the leaf rows are the
- * points in Morton order and the root box gives the build's bounds, so it
- * writes the same bytes as tbvh_accel_build.
- * Precondition of tbvh_knn_accel*: `accel` holds what one of these builders
- * (or tbvh_build*_with_accel) wrote for the same clouds.  Its child and
- * parent links are followed as stored; refs outside a cloud are skipped
- * (no read leaves the cloud's rows), but links corrupted into a cycle would
- * keep the traversal running without end, so an accel must never be
- * modified or taken from another BVH. */
+ * reference's query bindings holds nothing else; num_real_nodes must be
+ * real_node_count(N)): the leaf rows are the points in Morton order and the
+ * root box gives the build's bounds, so it writes the same bytes as
+ * tbvh_accel_build.  That holds only for the point BVH the build writes, so
+ * it also checks the tensors on the device and stores into the device word
+ * *defects 0 when they are one (leaf rows degenerate boxes, lo and hi
+ * bitwise equal; every internal row the fminf/fmaxf merge of its children,
+ * a copy of the left child where the right one is virtual; leaf codes
+ * non-decreasing; sorted indices in [0, N)) and 1 otherwise (a primitive
+ * BVH, edited boxes, another Morton order): the accel is then not to be
+ * used, and tbvh_knn answers for those tensors.
+ * Precondition of tbvh_knn_accel*: `accel` (256-byte aligned, else
+ * TBVH_ERR_INVALID_ARGUMENT) holds what one of these builders (or
+ * tbvh_build*_with_accel) wrote for the same clouds.  Its child and parent
+ * links are followed as stored; refs outside a cloud are skipped (no read
+ * leaves the cloud's rows), but links corrupted into a cycle would keep
+ * the traversal running without end, so an accel must never be modified or
+ * taken from another BVH (the Python layer records which node_aabbs each
+ * accel it builds belongs to and refuses any other pairing). */
 int tbvh_accel_size(int64_t B, int64_t total_points, int D, size_t* bytes);
 int tbvh_accel_workspace_size(int64_t B, int64_t total_points, int D, size_t* bytes);
 int tbvh_accel_build(const float* points, const int64_t* sorted_indices,
@@ -332,7 +342,8 @@ int tbvh_accel_build(const float* points, const int64_t* sorted_indices,
                      void* accel, void* workspace, size_t workspace_bytes,
                      void* stream);
 int tbvh_accel_build_from_tree(const float* node_aabbs, const int64_t* sorted_indices,
-                               int64_t B, int64_t N, int D, void* accel,
+                               int64_t B, int64_t N, int64_t num_real_nodes, int D,
+                               void* accel, uint32_t* defects,
                                void* workspace, size_t workspace_bytes, void* stream);
 int tbvh_accel_build_ragged(const float* points, const int64_t* offsets,
                             const int64_t* sorted_indices, const float* node_aabbs,

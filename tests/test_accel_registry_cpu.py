@@ -62,3 +62,55 @@ def test_entry_goes_with_the_build_tensor():
     del nodes
     gc.collect()
     assert key not in _native._accel_registry
+
+
+def test_explicit_accels_belong_to_the_tensors_they_were_built_for():
+    """Every accel the library builds is recorded with the node_aabbs it
+    was built for and its point count; an explicit accel is accepted only
+    with those tensors (or views of all of them), unmodified."""
+    nodes = torch.rand(2, 7, 6)
+    order = torch.arange(8).repeat(2, 1)
+    accel = torch.zeros(64, dtype=torch.uint8)
+    _native._register_accel(nodes, order, accel)
+    assert _native._accel_belongs(accel, nodes, 16)
+    assert _native._accel_belongs(accel[:], nodes[None], 16)  # views of every element
+    assert not _native._accel_belongs(accel, nodes, 8)  # another point count
+    assert not _native._accel_belongs(accel, nodes.clone(), 16)  # a copy of the tensors
+    assert not _native._accel_belongs(accel.clone(), nodes, 16)  # a copy of the accel
+    other = torch.rand(2, 7, 6)  # another cloud of the same size
+    assert not _native._accel_belongs(accel, other, 16)
+    nodes.add_(0)  # modified since the build
+    assert not _native._accel_belongs(accel, nodes, 16)
+    unrecorded = torch.zeros(64, dtype=torch.uint8)
+    assert not _native._accel_belongs(unrecorded, other, 16)
+
+
+def test_the_registry_follows_views_of_the_build_tensors():
+    """The reference's single-cloud path squeezes the batch dimension at
+    build time and unsqueezes it for every query (_query.py:51-53,139): the
+    registered accel is found through such views while the handle holds them,
+    and the entry goes with the last of them."""
+    nodes = torch.rand(1, 7, 6)
+    order = torch.arange(8)[None]
+    accel = torch.zeros(16, dtype=torch.uint8)
+    _native._register_accel(nodes, order, accel)
+    held_nodes, held_order = nodes.squeeze(0), order.squeeze(0)
+    key = nodes.data_ptr()
+    del nodes, order
+    gc.collect()
+    assert _native._registered_accel(held_nodes.unsqueeze(0), held_order.unsqueeze(0)) is accel
+    del held_nodes, held_order
+    gc.collect()
+    assert key not in _native._accel_registry
+
+
+def test_tensors_registered_for_the_implicit_tree():
+    """Tensors the device check found not to be a point BVH are registered
+    with no accel: the bindings then take the implicit tree without
+    checking again."""
+    nodes = torch.rand(1, 7, 6)
+    order = torch.arange(4)[None]
+    _native._register_accel(nodes, order, None)
+    assert _native._registry_entry(nodes, order) is not None
+    assert _native._registered_accel(nodes, order) is None
+    assert _native._pick_accel("op", None, nodes, order, 3) is None

@@ -106,3 +106,41 @@ def test_handle_lifecycle_without_gpu():
     assert b["_batched"] is True
     with pytest.raises(RuntimeError, match="Batched BVH handle has been destroyed"):
         b.destroy() or b["dim"]
+
+
+@pytest.mark.parametrize("layout,good,cases", [
+    ("single", (6, 3), [((6,), "source_points must have shape \\(N, D\\)"),
+                        ((5, 3), "source_points first dimension must match BVH num_leaves"),
+                        ((6, 2), "source_points second dimension must match BVH dim")]),
+    ("batched", (2, 6, 3), [((6, 3), "source_points must have shape \\(B, N, D\\)"),
+                            ((3, 6, 3), "source_points batch size must match BVH batch_size"),
+                            ((2, 5, 3), "source_points second dimension must match BVH num_leaves"),
+                            ((2, 6, 2), "source_points last dimension must match BVH dim")]),
+    ("ragged", (9, 3), [((9,), "ragged source_points must have shape \\(total_N, D\\)"),
+                        ((8, 3), "source_points first dimension must match BVH total_N"),
+                        ((9, 2), "source_points second dimension must match BVH dim")]),
+])
+def test_source_points_rules_in_the_reference_order(layout, good, cases):
+    """The source_points checks of query_knn (_query.py:197-215, 261-271 in
+    the reference): shape against the handle first, then a CUDA float32
+    tensor, then the BVH's device; each failure is a ValueError with the
+    reference's message."""
+    from torchbvh_amd._validation import check_source_points
+
+    data = {"num_leaves": 6, "dim": 3, "batch_size": 2}
+    cpu = torch.device("cpu")
+    for shape, message in cases:
+        with pytest.raises(ValueError, match=f"^query_knn: {message}$"):
+            check_source_points("query_knn", layout, torch.zeros(shape), data, cpu, 9)
+    # Right shape: the next rule is the device (CUDA), then the dtype.
+    with pytest.raises(ValueError, match="source_points must be a CUDA tensor"):
+        check_source_points("query_knn", layout, torch.zeros(good), data, cpu, 9)
+
+
+def test_build_extent_rule_counts_every_row_without_materialising():
+    from torchbvh_amd._validation import check_build_extent
+
+    big = torch.zeros(1, 3).expand(1 << 16, 1 << 15, 3)  # 2^31 rows as a view
+    with pytest.raises(ValueError, match="build_bvh: total point count must fit in signed int32"):
+        check_build_extent("build_bvh", big)
+    check_build_extent("build_bvh", torch.zeros(1, 3).expand((1 << 31) - 1, 3))

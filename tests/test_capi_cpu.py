@@ -48,7 +48,7 @@ def test_library_exports_every_declared_symbol():
     L = _native.load()
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
-    assert L.tbvh_abi_version() == 1
+    assert L.tbvh_abi_version() == 2
 
 
 @pytest.mark.parametrize("n", list(range(1, 300)) + [10_000, 65_536, 1 << 20, 4_194_304, 200_000, 1 << 30])
@@ -148,6 +148,31 @@ def test_accel_argument_errors():
     assert L.tbvh_knn_accel(FAKE, FAKE, None, 1, 10, 3, 3, 4, FAKE, FAKE, None) == 1
     assert "num_leaves must be >= k" in _err(L)
     assert L.tbvh_knn_accel(None, None, None, 1, 0, 100, 3, 4, None, None, None) == 0
+
+
+def test_accel_from_tree_and_accel_alignment_errors():
+    """tbvh_accel_build_from_tree checks the node count against the tree
+    over N points and needs its defects word; every k-NN accel entry point
+    refuses an accel that is not 256-byte aligned.  All before any launch."""
+    L = _native.load()
+    size = ctypes.c_size_t()
+    assert L.tbvh_accel_workspace_size(2, 2000, 3, ctypes.byref(size)) == 0
+    need = size.value
+    nr = _native.real_node_count(1000)
+    assert L.tbvh_accel_build_from_tree(FAKE, FAKE, 2, 1000, nr - 1, 3, FAKE, FAKE, FAKE, need, None) == 1
+    assert "num_real_nodes does not match num_leaves" in _err(L)
+    assert L.tbvh_accel_build_from_tree(FAKE, FAKE, 2, 1000, nr, 3, FAKE, None, FAKE, need, None) == 1
+    assert "null" in _err(L)
+    mis = ctypes.c_void_p(0x100010)
+    assert L.tbvh_knn_accel(mis, FAKE, None, 1, 10, 100, 3, 4, FAKE, FAKE, None) == 1
+    assert "aligned" in _err(L)
+    assert L.tbvh_knn_accel_spatial(mis, FAKE, FAKE, 1, 10, 100, 3, 4, FAKE, FAKE, None) == 1
+    assert "aligned" in _err(L)
+    assert L.tbvh_knn_accel_ragged(mis, FAKE, 100, FAKE, FAKE, None, 1, 10, 3, 4, FAKE, FAKE, None) == 1
+    assert "aligned" in _err(L)
+    assert L.tbvh_knn_accel_routed_spatial(FAKE, mis, FAKE, FAKE, FAKE, 1, 10, 100, 100, 3, 4, FAKE, FAKE,
+                                           None) == 1
+    assert "aligned" in _err(L)
 
 
 def test_build_with_accel_argument_errors():

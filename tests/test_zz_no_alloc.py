@@ -103,6 +103,10 @@ def test_noalloc_accel_answers_knn_like_oracle():
 def test_noalloc_rejects_clouds_beyond_its_scratch():
     L = _native.load()
     pts = torch.zeros((1, 1 << 23, 3), dtype=torch.float32, device=DEV)
-    o = [ctypes.c_void_p(0x100000)] * 8  # never written: the size check fails first
+    # Null outputs and a small real accel: should the size check ever pass,
+    # the build's own null-pointer check still stops the call before any
+    # launch, so nothing is written.
+    accel = torch.empty(256, dtype=torch.uint8, device=DEV)
+    o = [None] * 7 + [_native._ptr(accel)]
     assert L.tbvh_build_with_accel_noalloc(_native._ptr(pts), 1, 1 << 23, 3, *o, _native._stream(DEV)) == 2
     assert "scratch array" in L.tbvh_last_error().decode()

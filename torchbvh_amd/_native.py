@@ -20,6 +20,7 @@ import ctypes
 import threading
 import weakref
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
@@ -32,6 +33,9 @@ _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _szp = ctypes.POINTER(ctypes.c_size_t)
+
+# TBVH_ABI_VERSION of include/torchbvh_amd.h that these declarations follow.
+ABI_VERSION = 2
 
 
 def _declare(L) -> None:
@@ -89,7 +93,7 @@ def _declare(L) -> None:
     L.tbvh_accel_size.argtypes = [_i64, _i64, _int, _szp]
     L.tbvh_accel_workspace_size.argtypes = [_i64, _i64, _int, _szp]
     L.tbvh_accel_build.argtypes = [_vp] * 5 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
-    L.tbvh_accel_build_from_tree.argtypes = [_vp, _vp, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
+    L.tbvh_accel_build_from_tree.argtypes = [_vp, _vp, _i64, _i64, _i64, _int, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_accel_build_ragged.argtypes = (
         [_vp] * 6 + [_i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp]
     )
@@ -143,6 +147,11 @@ def load():
                 )
             L = ctypes.CDLL(str(LIB_PATH))
             _declare(L)
+            if L.tbvh_abi_version() != ABI_VERSION:
+                raise RuntimeError(
+                    f"torchbvh_amd: {LIB_PATH} has ABI version {L.tbvh_abi_version()}, these bindings "
+                    f"need {ABI_VERSION}; rebuild it with `python -m torchbvh_amd._build`"
+                )
             _lib = L
     return _lib
 
@@ -213,46 +222,92 @@ MAX_ACCEL_CLOUD = 1 << 28
 # Accel registry: a reference-style caller builds with the batched binding
 # and later passes only the BVH's tensors to the k-NN bindings.  The build
 # registers its accel under its node_aabbs; a k-NN call with accel=None
-# whose node_aabbs and sorted_indices are those tensors (or contiguous views
-# of all their elements: same data pointer while they are alive), unmodified
-# since (torch's version counters, which views share), traverses the accel
-# instead of the implicit tree - identical results, about 10x fewer node
-# visits.  Tensors it does not know (a clone, a copy, a reload) get an accel
-# built on the spot from node_aabbs and sorted_indices alone
-# (tbvh_accel_build_from_tree: the same bytes the build would have written)
-# and registered under them.  accel=False forces the implicit tree.  Entries
-# go when the registered node_aabbs is freed.
+# whose node_aabbs and sorted_indices are those tensors or views of all
+# their elements (the reference's single-cloud path squeezes the batch
+# dimension at build time and unsqueezes it per query, _query.py:51-53,139),
+# unmodified since (torch's version counters, which views share), traverses
+# the accel instead of the implicit tree - identical results, about 10x
+# fewer node visits.  Tensors it does not know (a clone, a copy, a reload)
+# are checked on the device once (tbvh_accel_build_from_tree: leaf rows
+# degenerate boxes, internal rows the merges of their children, leaf codes
+# in order, indices in range - the point BVH the build writes) and get an
+# accel built from node_aabbs and sorted_indices alone (the same bytes the
+# build would have written); tensors that fail the check (a primitive BVH,
+# edited boxes, another Morton order) are registered for the implicit tree,
+# which answers for any boxes as the reference does.  accel=False forces
+# the implicit tree.  Entries go when the registered node_aabbs is freed.
 # ---------------------------------------------------------------------------
-_accel_registry: dict[int, tuple] = {}
+class _Held(NamedTuple):
+    """A tensor the registry refers to without keeping it alive: its root
+    (the tensor that owns the memory of a view), data pointer, element count
+    and version when it was recorded."""
+
+    root: weakref.ref
+    ptr: int
+    numel: int
+    version: int
+
+    def matches(self, t: torch.Tensor) -> bool:
+        return (_root(t) is self.root() and t.data_ptr() == self.ptr and t.numel() == self.numel
+                and t.is_contiguous() and t._version == self.version)
 
 
-def _register_accel(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, accel: torch.Tensor) -> None:
+def _root(t: torch.Tensor) -> torch.Tensor:
+    return t._base if t._base is not None else t
+
+
+def _held(t: torch.Tensor, callback=None) -> _Held:
+    return _Held(weakref.ref(_root(t), callback), t.data_ptr(), t.numel(), t._version)
+
+
+_accel_registry: dict[int, tuple] = {}  # node_aabbs data pointer -> (_Held nodes, _Held order, accel | None)
+
+
+def _register_accel(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, accel: torch.Tensor | None) -> None:
+    """Record which accel answers for these tensors (None: the implicit
+    tree).  A built accel is also recorded as belonging to them."""
     key = node_aabbs.data_ptr()
 
     def _drop(ref, key=key):
         entry = _accel_registry.get(key)
-        if entry is not None and entry[0] is ref:
+        if entry is not None and entry[0].root is ref:
             del _accel_registry[key]
 
-    _accel_registry[key] = (weakref.ref(node_aabbs, _drop), node_aabbs._version,
-                            weakref.ref(sorted_indices), sorted_indices._version, accel)
+    _accel_registry[key] = (_held(node_aabbs, _drop), _held(sorted_indices), accel)
+    if accel is not None:
+        _record_accel(accel, node_aabbs, int(sorted_indices.numel()))
 
 
-def _same_tensor(t: torch.Tensor, ref: torch.Tensor | None, version: int) -> bool:
-    return (ref is not None and t.device == ref.device and t.data_ptr() == ref.data_ptr()
-            and t.numel() == ref.numel() and t.dtype == ref.dtype and t.is_contiguous()
-            and t._version == version)
+def _registry_entry(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor):
+    entry = _accel_registry.get(node_aabbs.data_ptr())
+    if entry is None or not (entry[0].matches(node_aabbs) and entry[1].matches(sorted_indices)):
+        return None
+    return entry
 
 
 def _registered_accel(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor):
-    """The accel built together with these tensors, unmodified, or None."""
-    entry = _accel_registry.get(node_aabbs.data_ptr())
-    if entry is None:
-        return None
-    nref, nver, sref, sver, accel = entry
-    if not (_same_tensor(node_aabbs, nref(), nver) and _same_tensor(sorted_indices, sref(), sver)):
-        return None
-    return accel
+    """The accel registered for these tensors, unmodified, or None (also
+    when they are registered for the implicit tree)."""
+    entry = _registry_entry(node_aabbs, sorted_indices)
+    return None if entry is None else entry[2]
+
+
+# Provenance of every accel this library builds: the node_aabbs it was
+# built with and the point count it covers, so that an accel handed in
+# explicitly is used only with the BVH it belongs to (an accel of another
+# cloud of the same size would silently answer for that cloud).
+_accel_owners: dict[int, tuple] = {}  # accel data pointer -> (accel ref, _Held nodes, total points)
+
+
+def _record_accel(accel: torch.Tensor, node_aabbs: torch.Tensor, total_points: int) -> None:
+    key = accel.data_ptr()
+
+    def _drop(ref, key=key):
+        entry = _accel_owners.get(key)
+        if entry is not None and entry[0] is ref:
+            del _accel_owners[key]
+
+    _accel_owners[key] = (weakref.ref(accel, _drop), _held(node_aabbs), int(total_points))
 
 
 def _fusable_source(source_points, device, lead: tuple) -> bool:
@@ -285,37 +340,58 @@ def _with_positions(indices, distances, positions, source_points):
     return indices, distances, positions
 
 
-def _check_accel(op: str, accel, clouds: int, total_points: int, dim: int, device: torch.device) -> None:
+def _accel_belongs(accel: torch.Tensor, node_aabbs: torch.Tensor, total_points: int) -> bool:
+    """True when this library built `accel` (the tensor itself or a view of
+    all of it) for `node_aabbs` over `total_points` points, and node_aabbs
+    has not been modified since."""
+    owner = _accel_owners.get(accel.data_ptr())
+    return (owner is not None and owner[0]() is _root(accel) and owner[2] == total_points
+            and owner[1].matches(node_aabbs))
+
+
+def _check_accel(op: str, accel, clouds: int, total_points: int, dim: int, device: torch.device,
+                 node_aabbs: torch.Tensor) -> None:
     """An accel tensor handed in by the caller must be a contiguous 1-D
-    uint8 tensor on the queries' device, at least as large as the layout for
-    these clouds: the traversal then never reads outside it (it also
-    bounds-checks every child ref and parent link against its cloud).  Its
-    contents are not checked: it must be what this library built for these
-    clouds, unmodified (links corrupted into a cycle would keep the
-    traversal running)."""
+    uint8 tensor on the queries' device, 256-byte aligned (the kernels read
+    it in 16-byte rows), at least as large as the layout for these clouds
+    (the traversal then never reads outside it; it also bounds-checks every
+    child ref and parent link against its cloud), and one this library built
+    for exactly these node_aabbs, unmodified since: an accel of another
+    cloud would silently answer for that cloud, and links corrupted into a
+    cycle would keep the traversal running."""
     _require(isinstance(accel, torch.Tensor) and accel.dtype == torch.uint8 and accel.dim() == 1
              and accel.is_contiguous(), op, "accel must be a contiguous 1-D uint8 tensor")
     _require(accel.is_cuda and accel.device == device, op, "accel must be on the queries' device")
+    _require(accel.data_ptr() % 256 == 0, op, "accel must be 256-byte aligned")
     need = _size(load().tbvh_accel_size, clouds, total_points, dim)
     _require(accel.numel() >= need, op,
              f"accel holds {accel.numel()} bytes; {clouds} cloud(s) of {total_points} points in total "
              f"need {need}")
+    _require(_accel_belongs(accel, node_aabbs, total_points), op,
+             "accel was not built by this library for these node_aabbs (or they were modified since)")
 
 
 def _accel_from_tree(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, dim: int):
-    """Build, register and return the accel of a batched BVH known only by its
-    node_aabbs [B, nr, 2D] and sorted_indices [B, N]; None when a cloud is
-    too large for one."""
+    """The accel of a batched BVH known only by its node_aabbs [B, nr, 2D]
+    and sorted_indices [B, N], built and registered on first use; None (and
+    registered as such) when a cloud is too large for one or the tensors are
+    not the point BVH the build writes (checked on the device; the one host
+    synchronisation of this path)."""
     B, N = int(sorted_indices.size(0)), int(sorted_indices.size(1))
     if N > MAX_ACCEL_CLOUD:
+        _register_accel(node_aabbs, sorted_indices, None)
         return None
     L = load()
     dev = node_aabbs.device
     with torch.cuda.device(dev):
         accel = torch.empty(_size(L.tbvh_accel_size, B, B * N, dim), dtype=torch.uint8, device=dev)
+        defects = torch.empty(1, dtype=torch.int32, device=dev)
         ws = _workspace(_size(L.tbvh_accel_workspace_size, B, B * N, dim), dev)
-        _check(L.tbvh_accel_build_from_tree(_ptr(node_aabbs), _ptr(sorted_indices), B, N, int(dim),
-                                            _ptr(accel), _ptr(ws), ws.numel(), _stream(dev)))
+        _check(L.tbvh_accel_build_from_tree(_ptr(node_aabbs), _ptr(sorted_indices), B, N,
+                                            int(node_aabbs.size(1)), int(dim), _ptr(accel), _ptr(defects),
+                                            _ptr(ws), ws.numel(), _stream(dev)))
+        if int(defects.item()) != 0:
+            accel = None
     _register_accel(node_aabbs, sorted_indices, accel)
     return accel
 
@@ -323,14 +399,15 @@ def _accel_from_tree(node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, dim
 def _pick_accel(op: str, accel, node_aabbs: torch.Tensor, sorted_indices: torch.Tensor, dim: int):
     """accel argument of the batched k-NN bindings (inputs already checked):
     False forces the implicit tree; a tensor is checked and used; None takes
-    the registered accel of these tensors, or builds one from them."""
+    what the registry holds for these tensors (an accel, or the implicit
+    tree), or checks them and builds one from them."""
     if accel is False:
         return None
     B, N = int(sorted_indices.size(0)), int(sorted_indices.size(1))
     if accel is None:
-        found = _registered_accel(node_aabbs, sorted_indices)
-        return found if found is not None else _accel_from_tree(node_aabbs, sorted_indices, dim)
-    _check_accel(op, accel, B, B * N, dim, sorted_indices.device)
+        entry = _registry_entry(node_aabbs, sorted_indices)
+        return entry[2] if entry is not None else _accel_from_tree(node_aabbs, sorted_indices, dim)
+    _check_accel(op, accel, B, B * N, dim, sorted_indices.device, node_aabbs)
     return accel
 
 
@@ -507,6 +584,8 @@ class _NativeOps:
                     _ptr(sorted_indices), _ptr(scene_min), _ptr(scene_max), _ptr(left),
                     _ptr(right), _ptr(leaf), _ptr(node_offsets), total_nodes,
                     _ptr(ws), ws.numel(), _stream(dev)))
+        if accel is not None:
+            _record_accel(accel, node_aabbs, T)
         host_node_offsets = [0]
         for c in node_counts:
             host_node_offsets.append(host_node_offsets[-1] + c)
@@ -544,6 +623,7 @@ class _NativeOps:
                 _ptr(points), _ptr(data["sorted_indices"]), _ptr(data["node_aabbs"]),
                 _ptr(data["scene_min"]), _ptr(data["scene_max"]), B, N, D, _ptr(accel),
                 _ptr(ws), ws.numel(), _stream(dev)))
+        _record_accel(accel, data["node_aabbs"], B * N)
         return accel
 
     @staticmethod
@@ -566,6 +646,7 @@ class _NativeOps:
                 _ptr(points), _ptr(batch_offsets), _ptr(packed["sorted_indices"]),
                 _ptr(packed["node_aabbs"]), _ptr(packed["scene_min"]), _ptr(packed["scene_max"]),
                 B, T, D, _ptr(accel), _ptr(ws), ws.numel(), _stream(dev)))
+        _record_accel(accel, packed["node_aabbs"], T)
         return accel
 
     @staticmethod
@@ -664,6 +745,8 @@ class _NativeOps:
             _require(query_order.dim() == 2 and query_order.shape == query_points.shape[:2],
                      op, "query_order must have shape (B, M)")
         _require(num_leaves >= k, op, "num_leaves must be >= k")
+        _require(1 <= num_leaves <= 1 << 30 and num_real_nodes == real_node_count(num_leaves), op,
+                 "num_real_nodes does not match num_leaves")
         dev = query_points.device
         for t in (node_aabbs, sorted_indices) + ((query_order,) if query_order is not None else ()):
             _require(t.device == dev, op, "all inputs must share a device")
@@ -799,6 +882,8 @@ class _NativeOps:
             _require_device_i64(op, srt, name)
             _require(tuple(srt.shape) == (B, n), op, f"{name} has incompatible shape")
         _require(true_num_leaves >= k and false_num_leaves >= k, op, "both source counts must be >= k")
+        for n, nr in ((true_num_leaves, true_num_real_nodes), (false_num_leaves, false_num_real_nodes)):
+            _require(n <= 1 << 30 and nr == real_node_count(n), op, "num_real_nodes does not match num_leaves")
         dev = query_points.device
         indices = torch.empty((B, M, k), dtype=torch.int64, device=dev)
         distances = torch.empty((B, M, k), dtype=torch.float32, device=dev)
@@ -839,7 +924,7 @@ class _NativeOps:
         dev = query_points.device
         if accel is not None:
             _require(total_points is not None, op, "total_points is required with an accel")
-            _check_accel(op, accel, int(batch_size), int(total_points), int(dim), dev)
+            _check_accel(op, accel, int(batch_size), int(total_points), int(dim), dev, node_aabbs)
         indices = torch.empty((T, k), dtype=torch.int64, device=dev)
         distances = torch.empty((T, k), dtype=torch.float32, device=dev)
         # Neighbour rows (packed like the points; indices are cloud-local):

@@ -10,22 +10,21 @@ views into the packed result.
 
 from __future__ import annotations
 
-from collections.abc import Mapping
-
 import torch
 
 from ._constants import SUPPORTED_DIMS
 from ._handles import BVHHandle, BatchedBVHHandle, RaggedBVHHandle, live_payload
 from ._native import _C
-from ._validation import check_cuda_f32, check_k, check_offsets, check_ragged_points, dense, dense_offsets
-
-_INT32_MAX = 2**31 - 1
-
-
-def _validate_narrow_build_extent(prefix: str, points: torch.Tensor) -> None:
-    total = int(points.size(0)) if points.dim() == 2 else int(points.size(0)) * int(points.size(1))
-    if total > _INT32_MAX:
-        raise ValueError(f"{prefix}: total point count must fit in signed int32")
+from ._validation import (
+    check_build_extent,
+    check_cuda_f32,
+    check_k,
+    check_offsets,
+    check_ragged_points,
+    check_source_points,
+    dense,
+    dense_offsets,
+)
 
 
 # ---------------------------------------------------------------------------
@@ -39,7 +38,7 @@ def _build_bvh_single(points: torch.Tensor) -> BVHHandle:
     check_cuda_f32("build_bvh", points, "points")
     # Sizes only, before any copy (an expanded view is rejected without
     # materialising it).
-    _validate_narrow_build_extent("build_bvh", points)
+    check_build_extent("build_bvh", points)
     points = dense(points)
     batched = points.unsqueeze(0)
     data = _C.build_bvh_batched_cooperative(batched, with_accel=True)
@@ -59,7 +58,7 @@ def _build_bvh_batched(points: torch.Tensor) -> BatchedBVHHandle:
     check_cuda_f32("build_bvh", points, "points")
     # Sizes only, before any copy (an expanded view is rejected without
     # materialising it).
-    _validate_narrow_build_extent("build_bvh", points)
+    check_build_extent("build_bvh", points)
     points = dense(points)
     data = _C.build_bvh_batched_cooperative(points, with_accel=True)
     accel = data.pop("accel")
@@ -70,7 +69,7 @@ def _build_bvh_ragged(points: torch.Tensor, batch_offsets: torch.Tensor) -> Ragg
     points = dense(points)
     batch_offsets = dense_offsets(batch_offsets)
     offsets = check_ragged_points("build_bvh", points, batch_offsets)
-    _validate_narrow_build_extent("build_bvh", points)
+    check_build_extent("build_bvh", points)
     counts = [b - a for a, b in zip(offsets, offsets[1:])]
     packed = _C.build_bvh_ragged(points, batch_offsets, counts, with_accel=True)
     accel = packed["accel"]
@@ -176,7 +175,7 @@ def _query_knn_single(
     accel = bvh._aux.get("accel")
     src = None
     if source_points is not None:
-        _validate_single_source_points("query_knn", data, source_points)
+        check_source_points("query_knn", "single", source_points, data, data["sorted_indices"].device)
         src = dense(source_points).unsqueeze(0)
     if _schedule(sort_queries, int(queries.size(1))):
         order = _C.morton_sort_queries_narrow(
@@ -192,32 +191,6 @@ def _query_knn_single(
             data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel, source_points=src,
         )
     return tuple(t.squeeze(0) for t in out)
-
-
-def _validate_single_source_points(prefix: str, data: Mapping, source_points: torch.Tensor) -> None:
-    if source_points.dim() != 2:
-        raise ValueError(f"{prefix}: source_points must have shape (N, D)")
-    if source_points.size(0) != data["num_leaves"]:
-        raise ValueError(f"{prefix}: source_points first dimension must match BVH num_leaves")
-    if source_points.size(1) != data["dim"]:
-        raise ValueError(f"{prefix}: source_points second dimension must match BVH dim")
-    check_cuda_f32(prefix, source_points, "source_points")
-    if source_points.device != data["sorted_indices"].device:
-        raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
-
-
-def _validate_batched_source_points(prefix: str, data: Mapping, source_points: torch.Tensor) -> None:
-    if source_points.dim() != 3:
-        raise ValueError(f"{prefix}: source_points must have shape (B, N, D)")
-    if source_points.size(0) != data["batch_size"]:
-        raise ValueError(f"{prefix}: source_points batch size must match BVH batch_size")
-    if source_points.size(1) != data["num_leaves"]:
-        raise ValueError(f"{prefix}: source_points second dimension must match BVH num_leaves")
-    if source_points.size(2) != data["dim"]:
-        raise ValueError(f"{prefix}: source_points last dimension must match BVH dim")
-    check_cuda_f32(prefix, source_points, "source_points")
-    if source_points.device != data["sorted_indices"].device:
-        raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
 
 
 def _query_knn_batched(
@@ -243,7 +216,7 @@ def _query_knn_batched(
     accel = bvh._aux.get("accel")
     src = None
     if source_points is not None:
-        _validate_batched_source_points("query_knn", data, source_points)
+        check_source_points("query_knn", "batched", source_points, data, data["sorted_indices"].device)
         src = dense(source_points)
     if _schedule(sort_queries, int(queries.size(0) * queries.size(1))):
         order = _C.morton_sort_queries_narrow(queries, data["scene_min"], data["scene_max"],
@@ -256,18 +229,6 @@ def _query_knn_batched(
         data["node_aabbs"], data["sorted_indices"], queries,
         data["num_leaves"], data["num_real_nodes"], data["dim"], k, accel=accel, source_points=src,
     )
-
-
-def _validate_ragged_source_points(prefix, data, source_points, *, total_rows, device) -> None:
-    if source_points.dim() != 2:
-        raise ValueError(f"{prefix}: ragged source_points must have shape (total_N, D)")
-    if source_points.size(0) != total_rows:
-        raise ValueError(f"{prefix}: source_points first dimension must match BVH total_N")
-    if source_points.size(1) != data["dim"]:
-        raise ValueError(f"{prefix}: source_points second dimension must match BVH dim")
-    check_cuda_f32(prefix, source_points, "source_points")
-    if source_points.device != device:
-        raise ValueError(f"{prefix}: source_points must be on the same device as the BVH")
 
 
 def _query_knn_ragged(
@@ -298,9 +259,7 @@ def _query_knn_ragged(
     if any(b - a < k for a, b in zip(p_offsets, p_offsets[1:])):
         raise ValueError("query_knn: each source sample must contain at least k points")
     if source_points is not None:
-        _validate_ragged_source_points(
-            "query_knn", data, source_points, total_rows=p_offsets[-1], device=queries.device
-        )
+        check_source_points("query_knn", "ragged", source_points, data, queries.device, p_offsets[-1])
         source_points = dense(source_points)
 
     packed = bvh._aux["packed"]

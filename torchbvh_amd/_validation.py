@@ -63,6 +63,66 @@ _RAGGED_POINTS: Sequence[Rule] = (
 )
 
 
+# Build extent (sizes only, checked before any copy so that an expanded view
+# is rejected without materialising it): every row of the call must have a
+# signed 32-bit index.
+_INT32_MAX = 2**31 - 1
+_BUILD_EXTENT: Sequence[Rule] = (
+    (lambda t: (t.size(0) if t.dim() == 2 else t.size(0) * t.size(1)) <= _INT32_MAX,
+     "total point count must fit in signed int32"),
+)
+
+
+def _first_only(rules: Sequence[Rule]) -> Sequence[Rule]:
+    """Rules on one tensor, restated for a subject of (tensor, *context)."""
+    return tuple((lambda t, *_, holds=holds: holds(t), message) for holds, message in rules)
+
+
+# source_points of a k-NN call, per handle layout; the subject is (tensor,
+# payload, BVH device, packed point count): shape against the payload
+# first, then dtype and placement.
+_SOURCE_TAIL: Sequence[Rule] = (
+    *_first_only(_CUDA_F32),
+    (lambda t, data, dev, total: t.device == dev, "{name} must be on the same device as the BVH"),
+)
+_SOURCE_POINTS: dict[str, Sequence[Rule]] = {
+    "single": (
+        (lambda t, data, dev, total: t.dim() == 2, "{name} must have shape (N, D)"),
+        (lambda t, data, dev, total: t.size(0) == data["num_leaves"],
+         "{name} first dimension must match BVH num_leaves"),
+        (lambda t, data, dev, total: t.size(1) == data["dim"], "{name} second dimension must match BVH dim"),
+        *_SOURCE_TAIL,
+    ),
+    "batched": (
+        (lambda t, data, dev, total: t.dim() == 3, "{name} must have shape (B, N, D)"),
+        (lambda t, data, dev, total: t.size(0) == data["batch_size"],
+         "{name} batch size must match BVH batch_size"),
+        (lambda t, data, dev, total: t.size(1) == data["num_leaves"],
+         "{name} second dimension must match BVH num_leaves"),
+        (lambda t, data, dev, total: t.size(2) == data["dim"], "{name} last dimension must match BVH dim"),
+        *_SOURCE_TAIL,
+    ),
+    "ragged": (
+        (lambda t, data, dev, total: t.dim() == 2, "ragged {name} must have shape (total_N, D)"),
+        (lambda t, data, dev, total: t.size(0) == total, "{name} first dimension must match BVH total_N"),
+        (lambda t, data, dev, total: t.size(1) == data["dim"], "{name} second dimension must match BVH dim"),
+        *_SOURCE_TAIL,
+    ),
+}
+
+
+def check_build_extent(prefix: str, points: torch.Tensor) -> None:
+    _walk(prefix, _BUILD_EXTENT, points)
+
+
+def check_source_points(prefix: str, layout: str, source_points: torch.Tensor, data, device: torch.device,
+                        total_rows: int | None = None) -> None:
+    """`source_points` of a k-NN call on a handle of `layout` ("single",
+    "batched" or "ragged") with payload `data` on `device`; `total_rows` is
+    the packed point count of a ragged BVH."""
+    _walk(prefix, _SOURCE_POINTS[layout], source_points, data, device, total_rows, name="source_points")
+
+
 def check_k(prefix: str, k: int) -> None:
     if k not in SUPPORTED_K:
         raise ValueError(f"{prefix}: {K_MESSAGE}")

@@ -107,6 +107,72 @@ __global__ __launch_bounds__(kBlock) void accel_points_from_tree_kernel(
     leaf_points[r] = v;
 }
 
+// Whether a batched BVH known only by its node_aabbs and sorted_indices is a
+// point BVH as the build writes it, which is what the pass above assumes:
+// every leaf row a degenerate box (lo and hi bitwise equal, NaN included),
+// every internal row the fminf/fmaxf merge of its children in the build's
+// argument order (a copy of the left child where the right one is
+// virtual), leaf codes non-decreasing against the root box's bounds, and
+// sorted indices inside the cloud.  Then every accel child box is the exact
+// box of its points and the accel answers exactly what the implicit tree
+// answers.  One thread per node row (grid.y = cloud); any failure stores 1
+// into *defects (every writer stores the same value), which the caller
+// cleared first.
+template <int D>
+__global__ __launch_bounds__(kBlock) void tree_defects_kernel(const float* __restrict__ node_aabbs,
+                                                              const int64_t* __restrict__ sorted, int n, int nr,
+                                                              uint32_t* __restrict__ defects) {
+    const int row = static_cast<int>(blockIdx.x) * kBlock + static_cast<int>(threadIdx.x);
+    if (row >= nr) return;
+    const int64_t b = blockIdx.y;
+    const int L = tree::leaf_level(n);
+    const int vl = tree::virtual_leaves(n);
+    const float* nodes = node_aabbs + b * nr * 2 * D;
+    // Rows hold the real nodes level by level; find this row's level.
+    int level = 0;
+    int level_row = 0;
+    while (level < L && level_row + tree::real_at_level(vl, L, level) <= row) {
+        level_row += tree::real_at_level(vl, L, level);
+        ++level;
+    }
+    const float* box = nodes + static_cast<int64_t>(row) * 2 * D;
+    bool bad = false;
+    if (level == L) {
+        const int j = row - level_row;
+        float lo[D], hi[D], p[D], q[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            p[d] = box[d];
+            bad |= __float_as_uint(box[d]) != __float_as_uint(box[D + d]);
+            lo[d] = fminf(kSeedLo, nodes[d]);
+            hi[d] = fmaxf(kSeedHi, nodes[D + d]);
+        }
+        const int64_t idx = sorted[b * n + j];
+        bad |= idx < 0 || idx >= n;
+        if (j > 0) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) q[d] = box[d - 2 * D];
+            bad |= morton::encode<D>(q, lo, hi) > morton::encode<D>(p, lo, hi);
+        }
+    } else {
+        const int i = tree::level_first(level) + (row - level_row);
+        const int left = 2 * i + 1;
+        const bool right_real = !tree::is_virtual(vl, L, left + 1);
+        const float* a = nodes + static_cast<int64_t>(tree::memory_index(vl, L, left)) * 2 * D;
+        const float* c = a + 2 * D;  // the right sibling's row follows the left one's
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const float want_lo = right_real ? fminf(a[d], c[d]) : a[d];
+            const float want_hi = right_real ? fmaxf(a[D + d], c[D + d]) : a[D + d];
+            bad |= __float_as_uint(box[d]) != __float_as_uint(want_lo);
+            bad |= __float_as_uint(box[D + d]) != __float_as_uint(want_hi);
+        }
+    }
+    if (bad) *defects = 1u;
+}
+
+__global__ void clear_word_kernel(uint32_t* word) { *word = 0u; }
+
 // Standalone pass 2: radix-tree internal nodes (Karras 2012, section 4), one
 // thread per node; nodes inside a bucket are not referenced and write nothing.  The
 // block first stages the sorted codes around its nodes in LDS (most nodes
@@ -273,6 +339,18 @@ hipError_t launch_accel_points_from_tree(const float* node_aabbs, const int64_t*
     } else {
         accel_points_from_tree_kernel<2><<<grid_for(total), kBlock, 0, stream>>>(node_aabbs, sorted, segs, Si, total,
                                                                                  leaf_points, codes);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_tree_defects(const float* node_aabbs, const int64_t* sorted, int D, int64_t B, int n, int nr,
+                               uint32_t* defects, hipStream_t stream) {
+    clear_word_kernel<<<1, 1, 0, stream>>>(defects);
+    const dim3 grid(grid_for(nr), static_cast<unsigned>(B));
+    if (D == 3) {
+        tree_defects_kernel<3><<<grid, kBlock, 0, stream>>>(node_aabbs, sorted, n, nr, defects);
+    } else {
+        tree_defects_kernel<2><<<grid, kBlock, 0, stream>>>(node_aabbs, sorted, n, nr, defects);
     }
     return hipGetLastError();
 }

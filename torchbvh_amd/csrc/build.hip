@@ -472,7 +472,11 @@ __global__ __launch_bounds__(kBlock) void tree_pass_kernel(const float* __restri
             const int heap = tree::level_first(lvl_in) + j;
             const int64_t row = tree::memory_index(vl, L, heap);
             if constexpr (kFromPoints) {
-                // Clamped so a corrupt permutation cannot read outside the cloud.
+                // `sorted` is this build's own sort output, a permutation of
+                // [0, n) (pass 0 synthesises the values 0..n-1 and every pass
+                // moves key/value pairs bijectively, tests/test_sort_model.py),
+                // so the clamp never binds; it only keeps a corrupt
+                // permutation from reading outside the cloud.
                 const int64_t idx = min(max(sorted[g.start + j], int64_t(0)), int64_t(g.n - 1));
                 if (out.leaf_boxes) {
                     // Primitive BVH: the leaf is the primitive's box.

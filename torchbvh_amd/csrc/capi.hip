@@ -883,12 +883,16 @@ int tbvh_accel_build(const float* points, const int64_t* sorted_indices, const f
 }
 
 int tbvh_accel_build_from_tree(const float* node_aabbs, const int64_t* sorted_indices, int64_t B, int64_t N,
-                               int D, void* accel, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+                               int64_t num_real_nodes, int D, void* accel, uint32_t* defects, void* workspace,
+                               size_t workspace_bytes, void* stream_ptr) {
     const char* op = "tbvh_accel_build_from_tree";
     if (int r = check_dim(op, D)) return r;
     if (int r = check_batched_extent(op, B, N)) return r;
     if (N > kMaxAccelCloud) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: clouds may hold at most 2^28 points", op);
-    if (!node_aabbs || !sorted_indices || !accel) {
+    if (num_real_nodes != tree::real_node_count(static_cast<int>(N))) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_real_nodes does not match num_leaves", op);
+    }
+    if (!node_aabbs || !sorted_indices || !accel || !defects) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }
     const int64_t total = B * N;
@@ -899,6 +903,8 @@ int tbvh_accel_build_from_tree(const float* node_aabbs, const int64_t* sorted_in
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     Segment* segs = carve<Segment>(workspace, 0);
     uint32_t* codes = carve<uint32_t>(workspace, align_up(static_cast<size_t>(B) * sizeof(Segment)));
+    TBVH_TRY(op, launch_tree_defects(node_aabbs, sorted_indices, D, B, static_cast<int>(N),
+                                     static_cast<int>(num_real_nodes), defects, stream));
     TBVH_TRY(op, launch_plan_uniform(segs, B, N, true, stream));
     TBVH_TRY(op, launch_accel_points_from_tree(node_aabbs, sorted_indices, D, segs, B, total, codes, accel, stream));
     TBVH_TRY(op, launch_accel_nodes(node_aabbs, D, segs, B, total, codes, accel, stream));
@@ -946,6 +952,7 @@ static int knn_accel_batched(const char* op, const void* accel, const float* que
     if (!accel || !queries || !out_indices || !out_distances || (spatial && !order)) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }
+    if (!aligned(accel)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
     KnnArgs a{};
     a.queries = queries;
     a.order = order;
@@ -994,6 +1001,7 @@ static int knn_accel_ragged(const char* op, const void* accel, const int64_t* po
     if (!accel || !point_offsets || !queries || !query_offsets || !out_indices || !out_distances) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
     }
+    if (!aligned(accel)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accel must be %zu-byte aligned", op, kAlign);
     KnnArgs a{};
     a.queries = queries;
     a.order = order;
@@ -1118,6 +1126,9 @@ int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_acce
     if (M == 0) return ok();
     if (!true_accel || !false_accel || !queries || !routes || !order || !out_indices || !out_distances) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null input or output pointer", op);
+    }
+    if (!aligned(true_accel) || !aligned(false_accel)) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accels must be %zu-byte aligned", op, kAlign);
     }
     KnnArgs a{};
     a.queries = queries;

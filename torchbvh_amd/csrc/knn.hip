@@ -468,19 +468,30 @@ struct AccelNodes {
     }
 
     // An internal node's parent is in its own row; a bucket's, in the last
-    // word of the row where it starts.  A link outside the cloud's internal
-    // nodes (which a well-formed accel never holds) ends the walk.
+    // word of the row where it starts; -1 above the root.  A ref outside the
+    // cloud is not read, and it or a stored link outside the cloud's
+    // internal nodes (neither of which a well-formed accel holds) returns
+    // kCorruptLink.
+    static constexpr int32_t kCorruptLink = -2;
     __device__ __forceinline__ int32_t parent(int32_t ref) const {
-        const int32_t par = __float_as_int(
-            recs[row(ref >= 0 ? ref : ref & 0x0fffffff) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
-        return par >= 0 && par < n - 1 ? par : -1;
+        if (ref == root()) return -1;
+        const int first = ref & 0x0fffffff;
+        if (ref >= 0 ? ref >= n - 1 : first + ((ref >> 28) & 7) + 1 > n) return kCorruptLink;
+        const int32_t par = __float_as_int(recs[row(ref >= 0 ? ref : first) * R + 4 * D + (ref >= 0 ? 2 : 3)]);
+        return par >= 0 && par < n - 1 ? par : kCorruptLink;
     }
 
     template <int K>
     __device__ __forceinline__ void scan(int32_t ref, const float* q, uint64_t (&best)[K]) const {
         const int first = ref & 0x0fffffff;
         const int count = ((ref >> 28) & 7) + 1;
-        if (first + count > n) return;  // a corrupt ref never reads outside the cloud
+        // Only an accel this library did not build for these clouds holds
+        // such a ref (the Python layer refuses any other pairing; the C ABI
+        // states it as a precondition): nothing outside the cloud is read.
+        // Marking the row instead measured +27 VGPRs at 3-D k = 32 (a wave
+        // per SIMD less) and spills at 3-D k = 16, so the row is left as
+        // the traversal found it.
+        if (first + count > n) return;
         constexpr int kBucket = accel_bucket<D>();
         // Every slot loads, so the loads issue together from one address.
         // Slots past the bucket (masked below) read at most kBucket - 1 rows

@@ -196,6 +196,11 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const Segment* __rest
         const int pos = wave * kWave * kItems + i * kWave + lane;
         if (pos < count) {
             const uint32_t digit = (key[i] >> shift) & (kRadix - 1);
+            // The tile's keys of smaller digits, this digit's keys in earlier
+            // waves and in earlier slots of this wave: a bijection onto
+            // [0, count), so the clamp never binds (restated term by term and
+            // checked on the CPU in tests/test_sort_model.py); it only keeps an
+            // inconsistent count from writing outside LDS.
             const uint32_t at = min(s_start[digit] + s_cnt[wave][digit] + rank[i],
                                     static_cast<uint32_t>(kSortTile - 1));
             s_keys[at] = key[i];
@@ -207,7 +212,14 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const Segment* __rest
         const uint32_t k = s_keys[j];
         const uint32_t digit = (k >> shift) & (kRadix - 1);
         const uint32_t rel = s_base[digit] + (j - s_start[digit]);
-        if (rel >= static_cast<uint32_t>(g.n)) continue;  // unreachable when counts agree
+        // rel counts the segment's keys that precede this one in the stable
+        // order (smaller digits, then this digit in earlier tiles, then in
+        // this tile): a bijection onto [0, n) whenever the scan holds the
+        // exclusive sums of the counts this tile ranked, which the count and
+        // scan kernels compute from the same keys (tests/test_sort_model.py
+        // restates the arithmetic).  The test never fires; it only keeps an
+        // inconsistent scan from writing outside the segment.
+        if (rel >= static_cast<uint32_t>(g.n)) continue;
         const int64_t row = g.start + rel;
         if constexpr (kLast) {
             pass.idx_out[row] = static_cast<int64_t>(s_vals[j]);

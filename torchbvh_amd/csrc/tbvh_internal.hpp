@@ -236,6 +236,11 @@ hipError_t launch_accel_points(const float* points, const int64_t* sorted, const
 hipError_t launch_accel_points_from_tree(const float* node_aabbs, const int64_t* sorted, int D,
                                          const Segment* segs, int64_t S, int64_t total, uint32_t* codes,
                                          void* accel, hipStream_t stream);
+// Clears *defects, then sets it to 1 unless the B clouds' node_aabbs
+// ([B, nr, 2D]) and sorted_indices ([B, n]) form the point BVH the build
+// writes (what launch_accel_points_from_tree assumes).
+hipError_t launch_tree_defects(const float* node_aabbs, const int64_t* sorted, int D, int64_t B, int n, int nr,
+                               uint32_t* defects, hipStream_t stream);
 // Records of the nodes the fused first tree pass listed (after all tree
 // passes: their boxes need the upper levels).  `groups_bound` bounds the
 // first pass's work-group count.
