@@ -16,7 +16,7 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC = PACKAGE_DIR / "csrc"
 LIB_NAME = "libtorchbvh_amd.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
-SOURCES = ("build.hip", "sort.hip", "accel.hip", "knn.hip", "route.hip", "interp.hip", "capi.hip")
+SOURCES = ("build.hip", "sort.hip", "small.hip", "accel.hip", "knn.hip", "route.hip", "interp.hip", "capi.hip")
 ARCH = "gfx950"
 
 

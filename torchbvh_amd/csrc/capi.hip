@@ -197,18 +197,27 @@ hipError_t run_build(const float* points, const int64_t* offsets, int64_t S, int
         }
         points = centers;
         boxes = leaf_boxes;
-    } else if ((e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max, !fuse,
-                                  seed_lo, seed_hi, plan, stream)) != hipSuccess) {
-        return e;
     }
     const SortBits bits = full_sort(D);
-    if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.tile_hist,
-                           sb.tstride, bits, fin, stream)) != hipSuccess) {
-        return e;
-    }
     uint32_t* sorted_keys = o.accel ? last_pass_keys(sb) : nullptr;
-    if ((e = launch_sort(segs, S, l.tiles, bits, sb, o.sorted_indices, sorted_keys, stream)) != hipSuccess) {
-        return e;
+    if (V == 0 && cloud_bound <= kSmallCloud) {
+        // Small clouds: bounds, codes and the whole sort in one launch.
+        if ((e = launch_small_sort(points, D, segs, S, plan, cloud_bound, o.scene_min, o.scene_max, true, seed_lo,
+                                   seed_hi, bits, o.sorted_indices, sorted_keys, stream)) != hipSuccess) {
+            return e;
+        }
+    } else {
+        if (V == 0 && (e = launch_bounds(points, D, segs, S, l.tiles, partials, o.scene_min, o.scene_max, !fuse,
+                                         seed_lo, seed_hi, plan, stream)) != hipSuccess) {
+            return e;
+        }
+        if ((e = launch_morton(points, D, segs, S, l.tiles, o.scene_min, o.scene_max, sb.keys_a, sb.tile_hist,
+                               sb.tstride, bits, fin, stream)) != hipSuccess) {
+            return e;
+        }
+        if ((e = launch_sort(segs, S, l.tiles, bits, sb, o.sorted_indices, sorted_keys, stream)) != hipSuccess) {
+            return e;
+        }
     }
     if (o.sort_only) return hipSuccess;
     TreeOutputs to;
@@ -254,6 +263,12 @@ hipError_t run_query_sort(const float* queries, const int64_t* offsets, int64_t 
     if (offsets) e = launch_plan_offsets(segs, offsets, S, false, nullptr, stream);
     else plan = UniformPlan{segs, static_cast<int>(m_uniform), false};
     if (e != hipSuccess) return e;
+    const int64_t m_bound = offsets ? rows : m_uniform;  // bounds every cloud's query count
+    if (!codes_only && m_bound >= 1 && m_bound <= kSmallCloud) {
+        // Small query sets: codes and the whole sort in one launch.
+        return launch_small_sort(queries, D, segs, S, plan, m_bound, const_cast<float*>(scene_min),
+                                 const_cast<float*>(scene_max), false, 0.0f, 0.0f, bits, order, nullptr, stream);
+    }
     uint32_t* keys = codes_only ? codes_only : sb.keys_a;
     // Bounds given (BoundsFinish empty): the kernel only reads them.
     if ((e = launch_morton(queries, D, segs, S, l.tiles, const_cast<float*>(scene_min),

@@ -36,19 +36,6 @@ static_assert(kThreads >= kRadix && kSortTile % kThreads == 0, "sort tiling");
 constexpr int kScanThreads = 1024;
 constexpr int kScanItems = 4;
 
-// Lanes of the current wave holding the same digit as this lane (among
-// `valid` lanes).
-__device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
-    uint64_t peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < kRadixBits; ++b) {
-        const bool bit = (digit >> b) & 1u;
-        const uint64_t m = __ballot(bit);
-        peers &= bit ? m : ~m;
-    }
-    return peers;
-}
-
 // Digit counts of one tile of `keys` (a pass after the first).  Surplus
 // tiles (past their segment's last) count nothing.
 __global__ __launch_bounds__(kThreads) void tile_count_kernel(const Segment* __restrict__ segs, int S,

@@ -81,6 +81,127 @@ __device__ __forceinline__ int block_find_segment(F firsts, int S, int64_t x, in
 }
 
 // ---------------------------------------------------------------------------
+// Segment tables (device): each cloud's rows, tiles, tree sizes and the
+// work-groups of each tree pass, filled in closed form for equal clouds.
+// ---------------------------------------------------------------------------
+// How the first launch of a sequence finds its segments: for S equal
+// clouds of n rows (n > 0) it computes each one in place, and also stores
+// the whole table into `table` for the launches after it (so no planning
+// launch runs first); with n == 0 it reads the table a planning launch
+// filled.
+struct UniformPlan {
+    Segment* table = nullptr;
+    int n = 0;
+    bool tree = false;
+};
+
+// Work-groups of tree pass p for one cloud: pass p merges up to
+// kSubtreeLevels levels starting at level L - p*kSubtreeLevels; one group per
+// real node of the level it stops at.  Inactive passes have zero groups.
+__host__ __device__ inline int tree_pass_groups(int L, int vl, int p) {
+    const int lvl_in = L - p * kSubtreeLevels;
+    if (p > 0 && lvl_in <= 0) return 0;
+    const int top = lvl_in > kSubtreeLevels ? lvl_in - kSubtreeLevels : 0;
+    return tree::real_at_level(vl, L, top);
+}
+
+__device__ inline void fill_segment(Segment& g, int64_t start, int n, bool with_tree) {
+    g.start = start;
+    g.n = n;
+    g.tiles = (n + kSortTile - 1) / kSortTile;
+    if (with_tree) {
+        g.leaf_level = tree::leaf_level(n);
+        g.vl = tree::virtual_leaves(n);
+        g.nr = tree::real_node_count(n);
+        for (int p = 0; p < kMaxTreePasses; ++p) g.groups[p] = tree_pass_groups(g.leaf_level, g.vl, p);
+    } else {
+        g.leaf_level = 0;
+        g.vl = 0;
+        g.nr = 0;
+        for (int p = 0; p < kMaxTreePasses; ++p) g.groups[p] = 0;
+    }
+}
+
+// Segment i of S equal clouds of n rows.
+__device__ inline Segment uniform_segment(int64_t i, int n, bool with_tree) {
+    Segment g;
+    fill_segment(g, i * n, n, with_tree);
+    g.tile_first = static_cast<int32_t>(i * g.tiles);
+    g.node_start = i * g.nr;
+    for (int p = 0; p < kMaxTreePasses; ++p) g.group_first[p] = static_cast<int32_t>(i * g.groups[p]);
+    return g;
+}
+
+// Grid-stride store of the whole table of S equal clouds.
+__device__ inline void store_uniform_table(Segment* segs, int64_t S, int n, bool with_tree) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < S; i += stride) {
+        segs[i] = uniform_segment(i, n, with_tree);
+    }
+}
+
+// Segment of tile t in the first launch of a sequence (see UniformPlan):
+// computed for equal clouds (tiles past the last cloud's count as surplus
+// tiles of it), else looked up in the table.  Ends with a barrier either way.
+__device__ inline Segment first_launch_segment(const Segment* segs, int S, const UniformPlan& plan, int64_t t,
+                                               int* s_seg, int* seg_out) {
+    if (plan.n > 0) {
+        const int64_t per = (plan.n + kSortTile - 1) / kSortTile;
+        const int s = static_cast<int>(min(t / per, static_cast<int64_t>(S) - 1));
+        __syncthreads();
+        *seg_out = s;
+        return uniform_segment(s, plan.n, plan.tree);
+    }
+    const int s = block_find_segment([&](int i) { return static_cast<int64_t>(segs[i].tile_first); }, S, t, s_seg);
+    *seg_out = s;
+    return segs[s];
+}
+
+// Block-wide min (c < D) / max (c >= D) of per-thread boxes; the result for
+// component c lands in out[c] for threads c < 2D.
+template <int D, int kThreads = kBlock>
+__device__ __forceinline__ void block_box(float (&lo)[D], float (&hi)[D], float (*s_red)[2 * D],
+                                          float* out) {
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        lo[d] = wave_min(lo[d]);
+        hi[d] = wave_max(hi[d]);
+    }
+    if (lane_id() == 0) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) { s_red[wave][d] = lo[d]; s_red[wave][D + d] = hi[d]; }
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * D) {
+        const int c = threadIdx.x;
+        float v = s_red[0][c];
+        for (int w = 1; w < kThreads / kWave; ++w) v = c < D ? fminf(v, s_red[w][c]) : fmaxf(v, s_red[w][c]);
+        out[c] = v;
+    }
+}
+
+// Whole points as one load per lane (dwordx3 / dwordx2: a wave reads 64
+// consecutive points).
+template <int D>
+struct PointRow {
+    float v[D];
+};
+
+// Lanes of the current wave holding the same digit as this lane (among
+// `valid` lanes).
+__device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) {
+        const bool bit = (digit >> b) & 1u;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    return peers;
+}
+
+// ---------------------------------------------------------------------------
 // Launchers (host).  Every launcher enqueues on `stream` and returns the
 // launch status.
 // ---------------------------------------------------------------------------
@@ -113,16 +234,6 @@ struct SortPass {
     int shift;
 };
 
-// How the first launch of a sequence finds its segments: for S equal
-// clouds of n rows (n > 0) it computes each one in place, and also stores
-// the whole table into `table` for the launches after it (so no planning
-// launch runs first); with n == 0 it reads the table a planning launch
-// filled.
-struct UniformPlan {
-    Segment* table = nullptr;
-    int n = 0;
-    bool tree = false;
-};
 
 // Planning: fill the segment table.
 hipError_t launch_plan_uniform(Segment* segs, int64_t S, int64_t n, bool tree, hipStream_t stream);
@@ -160,6 +271,18 @@ struct SortBits {
     bool hilbert = false;
     int passes() const { return (end_bit - first_bit + kRadixBits - 1) / kRadixBits; }
 };
+
+// Clouds of at most kSmallCloud rows (small.hip): one work-group per cloud
+// computes its bounds (with `bounds`, from the seeds; else reads
+// scene_min/max), its keys (the curve of `bits`) and the whole stable sort in
+// LDS, and writes the cloud-local order and, if given, the sorted keys:
+// what launch_bounds + launch_morton + launch_sort produce, in one launch.
+// `max_n` bounds every cloud's row count (>= 1).
+constexpr int64_t kSmallCloud = 12288;
+hipError_t launch_small_sort(const float* rows, int D, const Segment* segs, int64_t S, UniformPlan plan,
+                             int64_t max_n, float* scene_min, float* scene_max, bool bounds, float seed_lo,
+                             float seed_hi, SortBits bits, int64_t* order, uint32_t* sorted_keys,
+                             hipStream_t stream);
 
 // Primitive BVH input: every primitive's box and centre, and each cloud's
 // bounds over the boxes (partials as in launch_bounds).
