@@ -541,6 +541,11 @@ def main() -> int:
     n_bytes = knn_bytes(total_q, D, k)
 
     from torchbvh_amd._native import _C
+    from torchbvh_amd._query import SCHEDULE_MIN_QUERIES
+
+    # query_knn schedules the traversal only above SCHEDULE_MIN_QUERIES
+    # queries (below it, input order is faster, schedule included).
+    scheduled = total_q > SCHEDULE_MIN_QUERIES
 
     def step(events=None):
         """One pass of the hot path: build (BVH + accel), query ordering,
@@ -558,8 +563,9 @@ def main() -> int:
             events[1].record()
         if kind == "ragged":
             packed = bvh._aux["packed"]
-            order = _C.morton_sort_queries_ragged(qs, qoff, packed["scene_min"], packed["scene_max"],
-                                                  bvh["batch_size"], schedule=True)
+            order = (_C.morton_sort_queries_ragged(qs, qoff, packed["scene_min"], packed["scene_max"],
+                                                   bvh["batch_size"], schedule=True)
+                     if scheduled else None)
             if events:
                 events[2].record()
             out = _C.query_knn_ragged(
@@ -573,12 +579,17 @@ def main() -> int:
             smax = bvh["scene_max"].unsqueeze(0) if one else bvh["scene_max"]
             nodes = bvh["node_aabbs"].unsqueeze(0) if one else bvh["node_aabbs"]
             sidx = bvh["sorted_indices"].unsqueeze(0) if one else bvh["sorted_indices"]
-            order = _C.morton_sort_queries_narrow(qb, smin, smax, schedule=True)
+            if scheduled:
+                order = _C.morton_sort_queries_narrow(qb, smin, smax, schedule=True)
             if events:
                 events[2].record()
-            out = _C.query_knn_batched_cached_bounds_ordered(
-                nodes, sidx, qb, order, bvh["num_leaves"], bvh["num_real_nodes"], D, k,
-                accel=bvh._aux["accel"])
+            if scheduled:
+                out = _C.query_knn_batched_cached_bounds_ordered(
+                    nodes, sidx, qb, order, bvh["num_leaves"], bvh["num_real_nodes"], D, k,
+                    accel=bvh._aux["accel"])
+            else:
+                out = _C.query_knn_batched_cached_bounds(
+                    nodes, sidx, qb, bvh["num_leaves"], bvh["num_real_nodes"], D, k, accel=bvh._aux["accel"])
         if events:
             events[3].record()
         return bvh, out
@@ -686,13 +697,14 @@ def main() -> int:
         "build_ms": build_ms,
         "query_ms": query_ms,
         "query_sort_ms": sort_ms,
-        "query_sort_what": "traversal schedule: stable 2-pass radix sort on the top 16 bits of Hilbert keys",
+        "query_sort_what": ("traversal schedule: stable 2-pass radix sort on the top 16 bits of Hilbert keys"
+                            if scheduled else "none: at most SCHEDULE_MIN_QUERIES queries run in input order"),
         "traversal_ms": trav_ms,
         "traversal_implicit_tree_ms": implicit_ms,
         "queries_per_s_excl_build": total_q / (query_ms * 1e-3) if query_ms > 0 else None,
         "build_hbm_frac_algorithmic": (b_bytes / (build_ms * 1e-3) / 1e9) / HBM_PEAK_GBS,
         "query_sort_hbm_frac_algorithmic": ((s_bytes / (sort_ms * 1e-3) / 1e9) / HBM_PEAK_GBS
-                                            if sort_ms else None),
+                                            if sort_ms and scheduled else None),
         "query_sort_bytes_formula": "Q(4D+40): queries read, 4-B keys, 2 passes x 16 B, 4-B order",
         "query_sort_full_ms": full_sort_ms,
         "query_sort_full_what": "reference binding morton_sort_queries_narrow: 30/32-bit Morton keys, 4 passes",

@@ -358,6 +358,27 @@ int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order
 int tbvh_knn_accel_spatial(const void* accel, const float* queries, const int64_t* order,
                            int64_t B, int64_t M, int64_t num_leaves, int D, int k,
                            int64_t* out_indices, float* out_distances, void* stream);
+/* tbvh_knn_accel with a workspace, for the same bindings
+ * (`query_knn_batched_cached_bounds(_ordered)`, torchbvh/csrc/bindings.cpp:
+ * 197-198, knn_query.cu:419-446): the same results, found by a cell-block
+ * search first.  The accel's points are cut into Morton cells against each
+ * cloud's root box (row 0 of its node_aabbs, num_real_nodes rows per cloud,
+ * which must be real_node_count(num_leaves)); each query scans the 3^D
+ * cells around its own and keeps that result when its k-th distance lies
+ * inside the block's margin (then no point outside can enter the list);
+ * the others, and every query of a cloud that is not near-uniform (a long
+ * empty run of cells, a non-finite point, cells out of the points' order),
+ * run the accel traversal seeded with that k-th distance.  Workspace:
+ * tbvh_knn_accel_grid_workspace_size (0 for clouds too small for a grid:
+ * then this is tbvh_knn_accel); a null workspace also runs
+ * tbvh_knn_accel. */
+int tbvh_knn_accel_grid_workspace_size(int64_t B, int64_t M, int64_t num_leaves, int D, int k,
+                                       size_t* bytes);
+int tbvh_knn_accel_grid(const void* accel, const float* node_aabbs, int64_t num_real_nodes,
+                        const float* queries, const int64_t* order,
+                        int64_t B, int64_t M, int64_t num_leaves, int D, int k,
+                        int64_t* out_indices, float* out_distances,
+                        void* workspace, size_t workspace_bytes, void* stream);
 int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets,
                           int64_t total_points, const float* queries,
                           const int64_t* query_offsets, const int64_t* order,

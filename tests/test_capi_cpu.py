@@ -150,6 +150,42 @@ def test_accel_argument_errors():
     assert L.tbvh_knn_accel(None, None, None, 1, 0, 100, 3, 4, None, None, None) == 0
 
 
+def test_grid_knn_workspace_and_argument_errors():
+    L = _native.load()
+    size = ctypes.c_size_t()
+    # Too small for a grid of 4 cells per axis: no workspace (then the call is tbvh_knn_accel).
+    assert L.tbvh_knn_accel_grid_workspace_size(1, 10, 20, 3, 4, ctypes.byref(size)) == 0 and size.value == 0
+    # 2^20 points, k = 16 in 3-D: 4 points per cell, 2^18 cells; then flags, a count, one
+    # 64-bit mask and one offset per 64 queries, a total per 1024 masks, the list, the bounds.
+    M = 1000
+    up = lambda x: (x + 255) // 256 * 256
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 16, ctypes.byref(size)) == 0
+    table = (1 << 18) + 1
+    tiles = (M + 63) // 64
+    expect = up(up(up(up(up(up(up(table * 4) + 4) + 4) + tiles * 8) + tiles * 4) + (tiles + 1023) // 1024 * 4)
+                + M * 4)
+    assert size.value == up(expect + M * 4)
+    # k = 32 keeps the traversal: no workspace.
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 32, ctypes.byref(size)) == 0 and size.value == 0
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 4, 16, ctypes.byref(size)) == 1
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 5, ctypes.byref(size)) == 1
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 16, None) == 1
+    N = 1 << 16
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, N, 3, 4, ctypes.byref(size)) == 0 and size.value > 0
+    need = size.value
+    nr = _native.real_node_count(N)
+    args = lambda nr_, ws, ws_bytes: (FAKE, FAKE, nr_, FAKE, None, 1, M, N, 3, 4, FAKE, FAKE, ws, ws_bytes, None)
+    assert L.tbvh_knn_accel_grid(*args(nr + 1, FAKE, need)) == 1
+    assert "num_real_nodes" in _err(L)
+    assert L.tbvh_knn_accel_grid(*args(nr, FAKE, need - 1)) == 2
+    assert "workspace" in _err(L)
+    assert L.tbvh_knn_accel_grid(*args(nr, ctypes.c_void_p(0x100008), need)) == 1
+    assert "aligned" in _err(L)
+    assert L.tbvh_knn_accel_grid(FAKE, None, nr, FAKE, None, 1, M, N, 3, 4, FAKE, FAKE, FAKE, need, None) == 1
+    assert "node_aabbs" in _err(L)
+    assert L.tbvh_knn_accel_grid(None, None, 0, None, None, 1, 0, N, 3, 4, None, None, None, 0, None) == 0
+
+
 def test_accel_from_tree_and_accel_alignment_errors():
     """tbvh_accel_build_from_tree checks the node count against the tree
     over N points and needs its defects word; every k-NN accel entry point

@@ -99,6 +99,10 @@ def _declare(L) -> None:
     )
     L.tbvh_knn_accel.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
     L.tbvh_knn_accel_spatial.argtypes = L.tbvh_knn_accel.argtypes
+    L.tbvh_knn_accel_grid_workspace_size.argtypes = [_i64, _i64, _i64, _int, _int, _vp]
+    L.tbvh_knn_accel_grid.argtypes = (
+        [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    )
     L.tbvh_knn_accel_ragged.argtypes = (
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp]
     )
@@ -118,6 +122,7 @@ def _declare(L) -> None:
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
         "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
+        "tbvh_knn_accel_grid_workspace_size", "tbvh_knn_accel_grid",
         "tbvh_knn_accel_positions", "tbvh_knn_accel_ragged_positions",
         "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
@@ -216,6 +221,11 @@ def real_node_count(n: int) -> int:
 
 # Largest cloud the acceleration structure supports (28-bit bucket starts).
 MAX_ACCEL_CLOUD = 1 << 28
+
+# Batched accel k-NN calls with more queries than this take the cell-block
+# search (tbvh_knn_accel_grid); below it its three extra launches cost more
+# than it saves.
+GRID_MIN_QUERIES = 1 << 17
 
 
 # ---------------------------------------------------------------------------
@@ -768,6 +778,17 @@ class _NativeOps:
                     _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
                     int(dim), int(k), _ptr(source_points), C, _ptr(indices), _ptr(distances),
                     _ptr(positions), _stream(dev)))
+            elif accel is not None and not spatial and B * M > GRID_MIN_QUERIES:
+                # The cell-block search first (same results; see
+                # tbvh_knn_accel_grid); its workspace is 0 for small clouds.
+                need = ctypes.c_size_t(0)
+                _check(L.tbvh_knn_accel_grid_workspace_size(B, M, int(num_leaves), int(dim), int(k),
+                                                            ctypes.byref(need)))
+                ws = torch.empty(max(int(need.value), 1), dtype=torch.uint8, device=dev)
+                _check(L.tbvh_knn_accel_grid(
+                    _ptr(accel), _ptr(node_aabbs), int(num_real_nodes), _ptr(query_points), _ptr(query_order),
+                    B, M, int(num_leaves), int(dim), int(k), _ptr(indices), _ptr(distances),
+                    _ptr(ws) if need.value else None, int(need.value), _stream(dev)))
             elif accel is not None:
                 fn = L.tbvh_knn_accel_spatial if spatial else L.tbvh_knn_accel
                 _check(fn(

@@ -953,7 +953,8 @@ static int knn_accel_batched(const char* op, const void* accel, const float* que
                              const int64_t* order, int64_t B, int64_t M, int64_t num_leaves, int D,
                              int k, bool spatial, int64_t* out_indices, float* out_distances,
                              void* stream_ptr, const float* source_points = nullptr, int source_cols = 0,
-                             float* out_positions = nullptr) {
+                             float* out_positions = nullptr, const float* node_aabbs = nullptr,
+                             int64_t num_real_nodes = 0, void* ws = nullptr, size_t ws_bytes = 0) {
     if (int r = check_dim(op, D)) return r;
     if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, or 16 (32 is also supported), got %d", op, k);
     if (B < 1 || M < 0) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1 and M >= 0", op);
@@ -983,8 +984,46 @@ static int knn_accel_batched(const char* op, const void* accel, const float* que
     a.source_points = source_points;
     a.source_cols = source_cols;
     a.out_positions = out_positions;
+    const int level = ws ? grid_level(num_leaves, D, k) : 0;
+    if (level > 0) {
+        if (!node_aabbs) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null node_aabbs", op);
+        if (num_real_nodes != tree::real_node_count(static_cast<int>(num_leaves))) {
+            return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_real_nodes does not match num_leaves", op);
+        }
+        if (!aligned(ws)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: workspace must be %zu-byte aligned", op, kAlign);
+        const size_t need = grid_workspace_bytes(B, B * M, level, D);
+        if (ws_bytes < need) {
+            return fail(TBVH_ERR_WORKSPACE_TOO_SMALL, "%s: workspace of %zu bytes is smaller than the %zu needed", op,
+                        ws_bytes, need);
+        }
+        TBVH_TRY(op, launch_grid_knn(a, node_aabbs, num_real_nodes, level, D, k, ws,
+                                     static_cast<hipStream_t>(stream_ptr)));
+        return ok();
+    }
     TBVH_TRY(op, launch_knn_accel(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
     return ok();
+}
+
+int tbvh_knn_accel_grid_workspace_size(int64_t B, int64_t M, int64_t num_leaves, int D, int k, size_t* bytes) {
+    const char* op = "tbvh_knn_accel_grid_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null output pointer", op);
+    if (int r = check_dim(op, D)) return r;
+    if (!supported_k(k)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: k must be 4, 8, 16 or 32, got %d", op, k);
+    if (B < 1 || M < 0 || num_leaves < 1 || num_leaves > kMaxAccelCloud) {
+        return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: need B >= 1, M >= 0 and num_leaves in [1, 2^28]", op);
+    }
+    if (M > 0 && B > kMaxRows / M) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: total query count must fit in signed int32", op);
+    const int level = grid_level(num_leaves, D, k);
+    *bytes = level > 0 ? grid_workspace_bytes(B, B * M, level, D) : 0;
+    return ok();
+}
+
+int tbvh_knn_accel_grid(const void* accel, const float* node_aabbs, int64_t num_real_nodes, const float* queries,
+                        const int64_t* order, int64_t B, int64_t M, int64_t num_leaves, int D, int k,
+                        int64_t* out_indices, float* out_distances, void* ws, size_t ws_bytes, void* stream_ptr) {
+    return knn_accel_batched("tbvh_knn_accel_grid", accel, queries, order, B, M, num_leaves, D, k, false,
+                             out_indices, out_distances, stream_ptr, nullptr, 0, nullptr, node_aabbs,
+                             num_real_nodes, ws ? ws : nullptr, ws_bytes);
 }
 
 int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order, int64_t B,

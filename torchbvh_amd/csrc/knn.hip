@@ -24,6 +24,9 @@
 // degenerate box this is the exact point distance with delta = |q - p|.
 #include <float.h>
 
+#include <algorithm>
+#include <cmath>
+
 #include "tbvh_internal.hpp"
 
 namespace tbvh {
@@ -144,7 +147,7 @@ struct MergePlan {
     }
 };
 
-template <int K, int B>
+template <int K, int B, int kBarrierFromK = 32>
 __device__ __forceinline__ void merge_candidates(uint64_t (&best)[K], uint64_t (&c)[B]) {
     sort_candidates<B>(c);
     constexpr int m = K < B ? K : B;
@@ -159,8 +162,9 @@ __device__ __forceinline__ void merge_candidates(uint64_t (&best)[K], uint64_t (
             if ((i & h) == 0 && ((plan.needed[s] >> i) & 1)) key_exchange(best[i], best[i + h]);
         }
         // At K = 32 the scheduler would otherwise start the next stage's
-        // exchanges before this one's maxima, holding up to 32 more VGPRs.
-        if constexpr (K >= 32) __builtin_amdgcn_sched_barrier(0);
+        // exchanges before this one's maxima, holding up to 32 more VGPRs
+        // (the cell-block search asks for this from K = 16).
+        if constexpr (K >= kBarrierFromK) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -863,9 +867,29 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     __shared__ uint32_t lds_refs[kLds * kKnnBlock];
     __shared__ uint16_t lds_dists[kCompact ? 1 : kLds * kKnnBlock];
     __shared__ uint8_t lds_hi[kCompact ? kLds * kKnnBlock : 1];
-    const int64_t per_xcd = gridDim.x / kXcds;
+    int64_t per_xcd = gridDim.x / kXcds;
+    // The cell-block search's fallback pass: its list names the launch
+    // positions left to search, in launch order, and bounds the k-th
+    // distance of each (at least k points lie within it, so slots seeded
+    // (bound, 0xffffffff) are all displaced by points, the bound's own
+    // included: the result is exact).  The grid is sized for every query;
+    // the tile map spreads the list's tiles over the XCDs like a launch of
+    // its own length.
+    const bool fallback = kAccel && !kRouted && a.fb_list != nullptr;
+    int64_t listed = 0;
+    if (fallback) {
+        listed = *a.fb_count;
+        per_xcd = ((listed + kKnnBlock - 1) / kKnnBlock + kXcds - 1) / kXcds;
+        if (blockIdx.x / kXcds >= per_xcd) return;
+    }
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    const int64_t gid = tile * kKnnBlock + threadIdx.x;
+    int64_t gid = tile * kKnnBlock + threadIdx.x;
+    float seed = kFar;
+    if (fallback) {
+        if (gid >= listed) return;
+        gid = a.fb_list[gid];
+        seed = a.fb_bound[gid];
+    }
     if (gid >= a.total_q) return;
     const QueryLoc in = locate<kOrdered, kRagged, kRouted, kAccel>(a, gid);
     if (in.row < 0) return;
@@ -876,7 +900,7 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
 
     uint64_t best[K];
 #pragma unroll
-    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(seed, 0xffffffffu);
 
     RingStack<kLds, kCompact> stack;
     stack.refs = lds_refs + threadIdx.x;
@@ -906,7 +930,8 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     // work-group is one wave, so the lane id is threadIdx.x) instead of being
     // held in registers through the traversal: the compiler cannot tell the
     // two apart, so nothing of the first derivation stays live.
-    const int64_t gid_out = tile * kKnnBlock + __lane_id();
+    int64_t gid_out = tile * kKnnBlock + __lane_id();
+    if (fallback) gid_out = a.fb_list[gid_out];
     const QueryLoc out = locate<kOrdered, kRagged, kRouted, kAccel>(a, gid_out);
     write_results<K, D>(a, out.out_row, best, out.index_offset, out.pstart);
 }
@@ -923,6 +948,312 @@ template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kCompact
 __global__ __launch_bounds__(kKnnBlock) __attribute__((amdgpu_waves_per_eu(knn_waves_per_simd<D, K, kCompact>()))) void
 knn_accel_kernel(KnnArgs a) {
     knn_query<D, K, kOrdered, kRagged, kRouted, true, kCompact>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Cell-block search (batched accel calls, near-uniform clouds).
+//
+// The accel's points are in Morton order, so the points of any level-l
+// Morton cell (the code's top D*l bits) are one contiguous run of them;
+// `table` holds each cell's first point (cell c's run is [table[c],
+// table[c + 1])).  A query scans the 3^D cells around its own (its
+// coordinates quantised as the points' were) and merges their points into
+// its list with the bucket merge.  Every point outside the block lies
+// beyond the block's boundary, at least `margin` from the query; when the
+// list's k-th distance is below margin^2 no such point can enter it, so the
+// list is the exact result, bit for bit (the same k smallest (distance,
+// index) keys).  The margin is taken short of the boundary by 1e-5 of the
+// larger of the box's extents and its coordinates' magnitudes: the rounding
+// of the quantisation (x - lo, the division), of the boundary and of the
+// distances adds up to about 5e-7 of that, and the squared distances keep
+// the strict order with the rest.  Queries that fail (or find the block too
+// full, or whose cloud the table kernel disabled) go to the accel traversal
+// with the block's k-th distance as the starting bound.  Measured on MI355X
+// (traversal, same inputs, cell-block path against the traversal alone):
+// cfg2 0.588 -> 0.569 ms (scan 0.40, fallback over 13% of the queries 0.14,
+// table and list 0.02), cfg4 0.923 -> 0.699 ms, cfg3 (clouds disabled:
+// long empty runs) 1.144 -> 1.168 ms.
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr int grid_axis_bits() { return D == 3 ? 10 : 16; }
+
+template <int D>
+__device__ __forceinline__ uint32_t grid_cell_id(const uint32_t (&c)[D]) {
+    if constexpr (D == 3) return morton::spread3(c[0]) | (morton::spread3(c[1]) << 1) | (morton::spread3(c[2]) << 2);
+    else return morton::spread2(c[0]) | (morton::spread2(c[1]) << 1);
+}
+
+// The level-l cell of a point (or query) against the cloud's box: the top l
+// bits of each axis of its Morton cell, so the cell id is its code >>
+// (D * (axis bits - l)).
+template <int D>
+__device__ __forceinline__ void grid_cell(const float* p, const float* lo, const float* hi, int shift,
+                                          uint32_t (&c)[D]) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        c[d] = morton::cell(morton::unit_coord(p[d], lo[d], hi[d]), 1u << grid_axis_bits<D>()) >> shift;
+    }
+}
+
+// Longest run of empty cells (in Morton order) a cloud may have: a longer
+// one means a large empty region, so the cloud is not near-uniform and the
+// block search is off for it (at the levels chosen, a uniform cloud has one
+// with probability below 1e-14).
+constexpr int kGridMaxGap = 64;
+
+__global__ void grid_init_kernel(uint32_t* flags, int64_t B, uint32_t* count) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < B) flags[i] = 0u;
+    if (i == 0) *count = 0u;
+}
+
+// One thread per point: writes the first-point entries of the cells from the
+// previous point's cell (exclusive) to its own, and after the last point
+// those up to the end.  flags[b] = 1 disables cloud b: a non-finite point or
+// box, an empty extent, a cell order that does not follow the points' (the
+// box is not the one their codes were taken against), or an empty run
+// longer than kGridMaxGap (its entries are then left unwritten, and unread).
+template <int D>
+__global__ __launch_bounds__(kBlock) void grid_table_kernel(const float4* __restrict__ pts,
+                                                            const float* __restrict__ node_aabbs, int64_t nr, int64_t B,
+                                                            int n, int level, int32_t* __restrict__ table,
+                                                            uint32_t* __restrict__ flags) {
+    // B * n fits in int32 (the entry points check it).
+    const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= B * n) return;
+    const int b = i / n;
+    const int j = i - b * n;
+    const float* root = node_aabbs + b * nr * 2 * D;
+    float lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        lo[d] = root[d];
+        hi[d] = root[D + d];
+    }
+    const int shift = grid_axis_bits<D>() - level;
+    const int64_t cells = int64_t(1) << (D * level);
+    int32_t* t = table + static_cast<int64_t>(b) * (cells + 1);
+    auto cell_of = [&](int64_t r, bool& ok) {
+        const float4 p4 = pts[r];
+        const float p[3] = {p4.x, p4.y, p4.z};
+        uint32_t c[D];
+        grid_cell<D>(p, lo, hi, shift, c);
+#pragma unroll
+        for (int d = 0; d < D; ++d) ok = ok && isfinite(p[d]);
+        return static_cast<int64_t>(grid_cell_id<D>(c));
+    };
+    bool ok = true;
+    const int64_t own = cell_of(i, ok);
+    // The previous point's cell is the previous lane's own (its cloud's, when
+    // j > 0), except in lane 0.
+    int64_t prev = __shfl_up(own, 1);
+    if (j == 0) {
+        prev = -1;
+    } else if (lane_id() == 0) {
+        bool prev_ok = true;
+        prev = cell_of(i - 1, prev_ok);
+    }
+    if (j == 0) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) ok = ok && isfinite(lo[d]) && isfinite(hi[d]) && hi[d] > lo[d];
+    }
+    const int64_t last = j == n - 1 ? cells : own;  // after the last point: every cell to the end
+    if (!ok || own < prev || own - prev > kGridMaxGap || last - own > kGridMaxGap) {
+        flags[b] = 1u;
+        return;
+    }
+    for (int64_t c = prev + 1; c <= own; ++c) t[c] = j;
+    for (int64_t c = own + 1; c <= last; ++c) t[c] = n;
+}
+
+// One query per lane, in launch order like the traversal (same tile map).
+// Failing queries are recorded per tile (a mask of its lanes, bounds[gid]
+// their block's k-th distance, FLT_MAX where none was taken), so that
+// grid_offsets_kernel and grid_list_kernel list them in launch order.
+template <int D, int K, bool kOrdered>
+__global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const float* __restrict__ node_aabbs, int64_t nr,
+                                                         int level, const int32_t* __restrict__ table,
+                                                         const uint32_t* __restrict__ flags, uint64_t* __restrict__ masks,
+                                                         float* __restrict__ bounds) {
+    constexpr int kCells = D == 3 ? 27 : 9;
+    // Points merged per pass, the bucket size.  12 per pass in 3-D (two
+    // sorted halves, merge_candidates12: one pass per cell where 6 take two,
+    // since some lane of 64 nearly always holds more than 6) measured the
+    // same at k = 16 (110 VGPRs, a wave per SIMD less) and slower at k = 4
+    // and 8, whose cells hold fewer points.
+    constexpr int kChunk = accel_bucket<D>();
+    const int64_t per_xcd = gridDim.x / kXcds;
+    const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (tile * kKnnBlock >= a.total_q) return;  // surplus tiles (whole waves)
+    const int64_t gid = tile * kKnnBlock + threadIdx.x;
+    // Lanes past the last query take no part; a lane whose cloud is
+    // disabled goes to the fallback at once (which also handles a corrupt
+    // order entry: no result).  A lane on a corrupt entry here takes no part.
+    bool valid = gid < a.total_q;
+    const int64_t b = valid ? gid / a.M : 0;
+    bool ok = valid && flags[b] == 0u;
+    if (__ballot(ok) == 0) {
+        const uint64_t left = __ballot(valid);
+        if (threadIdx.x == 0) masks[tile] = left;
+        if (valid) bounds[gid] = kFar;
+        return;
+    }
+    QueryLoc in{};
+    if (valid) {
+        in = locate<kOrdered, false, false, true>(a, gid);
+        valid = in.row >= 0;
+        ok = ok && valid;
+    }
+    const int n = a.num_leaves;
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        q[d] = valid ? a.queries[in.row * D + d] : 0.0f;
+        ok = ok && isfinite(q[d]);
+    }
+    const float* root = node_aabbs + b * nr * 2 * D;
+    float lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        lo[d] = root[d];
+        hi[d] = root[D + d];
+    }
+    const int shift = grid_axis_bits<D>() - level;
+    const int G = 1 << level;
+    uint32_t c[D];
+    grid_cell<D>(q, lo, hi, shift, c);
+    const int64_t cells = int64_t(1) << (D * level);
+    const int32_t* t = table + b * (cells + 1);
+    // A block is searched only while its point count stays near the cloud's
+    // mean (4x): a lane that passes the cap stops and goes to the traversal.
+    const int cap = 4 * kCells * static_cast<int>((n + cells - 1) / cells);
+    int total = 0;
+    uint64_t best[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
+    const float4* pts = static_cast<const float4*>(a.accel) + in.pstart;
+    // Cell by cell (reading a slab's runs together measured the same), in
+    // one loop body: unrolled, each copy kept the list in other registers
+    // (116 VGPRs at 3-D k = 16).  Offsets (dx, dy, dz) run over {-1, 0, 1}
+    // (dz only in 3-D).
+    int dx = -1, dy = -1, dz = D == 3 ? -1 : 0;
+#pragma unroll 1
+    for (int j = 0; j < kCells; ++j) {
+        {
+            const int x = static_cast<int>(c[0]) + dx, y = static_cast<int>(c[1]) + dy;
+            const int z = D == 3 ? static_cast<int>(c[D - 1]) + dz : 0;
+            const bool inside = ok && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
+            uint32_t cell[D];
+            cell[0] = static_cast<uint32_t>(x);
+            cell[1] = static_cast<uint32_t>(y);
+            if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
+            const uint32_t id = inside ? grid_cell_id<D>(cell) : 0u;
+            if (++dx == 2) {
+                dx = -1;
+                if (++dy == 2) {
+                    dy = -1;
+                    ++dz;
+                }
+            }
+            // Entries of an enabled cloud lie in [0, n]; clamped all the same.
+            int s = inside ? min(max(t[id], 0), n) : 0;
+            int e = inside ? min(max(t[id + 1], s), n) : 0;
+            total += e - s;
+            if (total > cap) {
+                ok = false;
+                e = s;
+            }
+            while (__ballot(s < e) != 0) {
+                const int cnt = e - s;
+                // Rows past the run read at most kChunk - 1 rows past the
+                // cloud's last point, inside the accel buffer (as the bucket
+                // scans do: the points area's padding and the record rows,
+                // >= 48 bytes per point, follow the last cloud).
+                const float4* r4 = pts + (s < e ? s : 0);
+                float4 p[kChunk];
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) p[u] = r4[u];
+                uint64_t cand[kChunk];
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) {
+                    const float dd = point_distance<D>(q, p[u]);
+                    cand[u] = u < cnt && dd < kFar ? candidate_key(dd, __float_as_uint(p[u].w)) : kEmptyKey;
+                }
+                merge_candidates<K, kChunk>(best, cand);
+                s += kChunk;
+            }
+        }
+    }
+    // Distance from the query to the block's boundary, where points lie
+    // beyond it (a block side at the grid's edge has none).
+    float margin = INFINITY;
+    float size = 0.0f;  // the larger of the extents and the coordinates' magnitudes
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        // The box again (not held through the scan).
+        lo[d] = root[d];
+        hi[d] = root[D + d];
+        const float ext = hi[d] - lo[d];
+        size = fmaxf(size, fmaxf(ext, fmaxf(fabsf(lo[d]), fabsf(hi[d]))));
+        const int b0 = static_cast<int>(c[d]) - 1, b1 = static_cast<int>(c[d]) + 2;
+        const float scale = ext / static_cast<float>(1u << grid_axis_bits<D>());
+        if (b0 > 0) margin = fminf(margin, q[d] - (lo[d] + static_cast<float>(b0 << shift) * scale));
+        if (b1 < G) margin = fminf(margin, (lo[d] + static_cast<float>(b1 << shift) * scale) - q[d]);
+    }
+    const float safe = margin - 1e-5f * size;
+    const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
+    const bool done = ok && safe > 0.0f && worst < safe * safe;
+    if (done) {
+        // Derived again rather than held through the scan.
+        const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
+        write_results<K, D>(a, out.out_row, best, 0, out.pstart);
+    }
+    const uint64_t left = __ballot(valid && !done);
+    if (threadIdx.x == 0) masks[tile] = left;
+    if (valid && !done) bounds[gid] = ok ? worst : kFar;
+}
+
+// The fallback list, every failing launch position in launch order, in two
+// launches: grid_offsets_kernel scans the tiles' mask counts within blocks
+// of kCompactTiles tiles (block totals to `sums`); grid_list_kernel (one
+// wave per tile) adds the earlier blocks' totals and writes the tile's
+// positions, and the last tile the list's length.
+constexpr int kCompactTiles = 1024;
+__global__ __launch_bounds__(kCompactTiles) void grid_offsets_kernel(const uint64_t* __restrict__ masks, int64_t tiles,
+                                                                    uint32_t* __restrict__ offsets,
+                                                                    uint32_t* __restrict__ sums) {
+    __shared__ uint32_t s_scan[kCompactTiles / kWave];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kCompactTiles + threadIdx.x;
+    const uint32_t c = t < tiles ? static_cast<uint32_t>(__popcll(masks[t])) : 0u;
+    uint32_t total = 0;
+    const uint32_t before = block_exclusive_sum<kCompactTiles>(c, s_scan, &total);
+    if (t < tiles) offsets[t] = before;
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+constexpr int kListWaves = 4;
+__global__ __launch_bounds__(kListWaves * kWave) void grid_list_kernel(const uint64_t* __restrict__ masks,
+                                                                      int64_t tiles,
+                                                                      const uint32_t* __restrict__ offsets,
+                                                                      const uint32_t* __restrict__ sums,
+                                                                      int32_t* __restrict__ list, uint32_t* count) {
+    // One wave per tile: the totals of the earlier blocks, then the tile's
+    // positions, a contiguous run of the list.
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kListWaves + threadIdx.x / kWave;
+    if (t >= tiles) return;
+    const int lane = lane_id();
+    const int block = static_cast<int>(t / kCompactTiles);
+    uint32_t before = 0;
+    for (int i = lane; i < block; i += kWave) before += sums[i];
+    before = wave_inclusive_sum(before);
+    const uint32_t base = __builtin_amdgcn_readlane(before, kWave - 1) + offsets[t];
+    const uint64_t m = masks[t];
+    if ((m >> lane) & 1ull) {
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+        list[base + rank] = static_cast<int32_t>(t * kKnnBlock + lane);
+    }
+    if (t == tiles - 1 && lane == 0) *count = base + static_cast<uint32_t>(__popcll(m));
 }
 
 template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel, bool kCompact = false>
@@ -991,6 +1322,122 @@ hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t s
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream) {
     if (a.total_q == 0) return hipSuccess;
     return D == 3 ? launch_d<3, true>(a, K, ragged, stream) : launch_d<2, true>(a, K, ragged, stream);
+}
+
+// Points per cell the level aims at: the k-th neighbour's distance then
+// stays about one cell (3-D: (3k / (4 pi rho))^(1/3) = 0.98 cells at rho =
+// k / 4; 2-D: (k / (pi rho))^(1/2) = 0.80 at rho = k / 2), inside the
+// block's one-cell margin for most queries (cfg2 87%, cfg4 97% in the CPU
+// model).  0 when the cloud is too small for a grid of at least 4 cells
+// per axis; at most 2^24 cells.
+int grid_level(int64_t n, int D, int K) {
+    // At k = 32 the block's 27 * 8 points cost more than the traversal
+    // (uniform 1M points, 3-D: +29%).
+    if (K > 16) return 0;
+    const double rho = D == 3 ? std::max(1, K / 4) : std::max(2, K / 2);
+    const double cells = static_cast<double>(n) / rho;
+    int l = static_cast<int>(std::lround(std::log2(std::max(cells, 1.0)) / D));
+    const int max_l = D == 3 ? 8 : 12;
+    if (l < 2) return 0;
+    return std::min(l, max_l);
+}
+
+namespace {
+struct GridLayout {
+    size_t table, flags, count, masks, offsets, sums, list, bounds, total;
+};
+GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
+    auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+    const size_t cells = size_t(1) << (D * level);
+    const size_t tiles = static_cast<size_t>((total_q + kKnnBlock - 1) / kKnnBlock);
+    GridLayout g;
+    g.table = 0;
+    g.flags = up(g.table + static_cast<size_t>(B) * (cells + 1) * 4);
+    g.count = up(g.flags + static_cast<size_t>(B) * 4);
+    g.masks = up(g.count + 4);
+    g.offsets = up(g.masks + tiles * 8);
+    g.sums = up(g.offsets + tiles * 4);
+    g.list = up(g.sums + (tiles + kCompactTiles - 1) / kCompactTiles * 4);
+    g.bounds = up(g.list + static_cast<size_t>(total_q) * 4);
+    g.total = up(g.bounds + static_cast<size_t>(total_q) * 4);
+    return g;
+}
+
+template <int D, int K>
+void launch_grid_dk(const KnnArgs& a, const float* node_aabbs, int64_t nr, int level, int32_t* table,
+                    uint32_t* flags, uint64_t* masks, float* bounds, hipStream_t stream) {
+    const int64_t tiles = (a.total_q + kKnnBlock - 1) / kKnnBlock;
+    const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
+    if (a.order != nullptr) {
+        grid_knn_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, masks,
+                                                                     bounds);
+    } else {
+        grid_knn_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, masks,
+                                                                      bounds);
+    }
+}
+}  // namespace
+
+size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D) {
+    return grid_layout(B, total_q, level, D).total;
+}
+
+hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t nr, int level, int D, int K,
+                           void* ws, hipStream_t stream) {
+    if (args.total_q == 0) return hipSuccess;
+    if (level < 2 || args.routes != nullptr || args.spatial_output || args.out_positions != nullptr ||
+        args.total_q >= (int64_t(1) << 31) || args.M <= 0) {
+        return hipErrorInvalidValue;
+    }
+    const GridLayout g = grid_layout(args.B, args.total_q, level, D);
+    char* base = static_cast<char*>(ws);
+    int32_t* table = reinterpret_cast<int32_t*>(base + g.table);
+    uint32_t* flags = reinterpret_cast<uint32_t*>(base + g.flags);
+    uint32_t* count = reinterpret_cast<uint32_t*>(base + g.count);
+    uint64_t* masks = reinterpret_cast<uint64_t*>(base + g.masks);
+    uint32_t* offsets = reinterpret_cast<uint32_t*>(base + g.offsets);
+    uint32_t* sums = reinterpret_cast<uint32_t*>(base + g.sums);
+    int32_t* list = reinterpret_cast<int32_t*>(base + g.list);
+    float* bounds = reinterpret_cast<float*>(base + g.bounds);
+    const int n = args.num_leaves;
+    grid_init_kernel<<<static_cast<unsigned>((args.B + kBlock - 1) / kBlock), kBlock, 0, stream>>>(flags, args.B,
+                                                                                                  count);
+    const int64_t pts = args.B * static_cast<int64_t>(n);
+    const unsigned tgrid = static_cast<unsigned>((pts + kBlock - 1) / kBlock);
+    const float4* p4 = static_cast<const float4*>(args.accel);
+    if (D == 3) grid_table_kernel<3><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
+    else grid_table_kernel<2><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
+    auto run = [&](auto dk) { dk(args, node_aabbs, nr, level, table, flags, masks, bounds, stream); };
+    // k <= 16 (grid_level).
+    if (D == 3) {
+        switch (K) {
+            case 4: run(launch_grid_dk<3, 4>); break;
+            case 8: run(launch_grid_dk<3, 8>); break;
+            case 16: run(launch_grid_dk<3, 16>); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (K) {
+            case 4: run(launch_grid_dk<2, 4>); break;
+            case 8: run(launch_grid_dk<2, 8>); break;
+            case 16: run(launch_grid_dk<2, 16>); break;
+            default: return hipErrorInvalidValue;
+        }
+    }
+    const int64_t tiles = (args.total_q + kKnnBlock - 1) / kKnnBlock;
+    const unsigned cgrid = static_cast<unsigned>((tiles + kCompactTiles - 1) / kCompactTiles);
+    grid_offsets_kernel<<<cgrid, kCompactTiles, 0, stream>>>(masks, tiles, offsets, sums);
+    grid_list_kernel<<<static_cast<unsigned>((tiles + kListWaves - 1) / kListWaves), kListWaves * kWave, 0, stream>>>(
+        masks, tiles, offsets, sums, list, count);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // The fallback: the accel traversal over the list (its grid sized for
+    // every query; work-groups past the list's tiles exit at once).
+    KnnArgs f = args;
+    f.fb_list = list;
+    f.fb_bound = bounds;
+    f.fb_count = count;
+    return launch_knn_accel(f, D, K, false, stream);
 }
 
 }  // namespace tbvh

@@ -429,9 +429,27 @@ struct KnnArgs {
     const void* accel2;            // accel of the false route
     int32_t num_leaves2;
     int32_t num_real_nodes2;
+    // Fallback pass of the cell-block search (batched accel only): launch
+    // position i < *fb_count runs the query at position fb_list[i], its list
+    // seeded with the k-th distance bound fb_bound[i] (FLT_MAX: none).
+    const int32_t* fb_list;
+    const float* fb_bound;
+    const uint32_t* fb_count;
 };
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
+
+// Cell-block k-NN (batched accel, `a` as for launch_knn_accel without
+// routes, spatial output or neighbour rows): every cloud's accel points are
+// cut into the level-`level` Morton cells against its root box (row 0 of
+// its node_aabbs, `nr` rows per cloud); each query scans the 3^D cells
+// around its own and keeps the result when its k-th distance is inside the
+// block's margin; the others run the accel traversal seeded with that
+// distance.  `ws` holds grid_workspace_bytes(B, total_q, level, D).
+int grid_level(int64_t n, int D, int K);
+size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D);
+hipError_t launch_grid_knn(const KnnArgs& a, const float* node_aabbs, int64_t nr, int level, int D, int K,
+                           void* ws, hipStream_t stream);
 
 // Tile-count bound for S segments holding `total` rows in kSortTile tiles.
 inline int64_t tiles_bound(int64_t total, int64_t S) {
