@@ -219,6 +219,18 @@ def test_fused_accel_matches_standalone_build(n, dim):
     assert_same_accel(fused, _standalone_accel(p, h), [n], dim)
 
 
+@pytest.mark.parametrize("dim", [2, 3])
+def test_fused_accel_matches_standalone_above_the_cooperative_span_limit(dim):
+    """Calls of more than 1.5M points finish the spanning radix-tree nodes
+    in two phases (one lane per node of short extent, a sub-group of eight
+    per longer one); calls up to it, a sub-group per node.  Both hold the
+    standalone build's bytes (one lane and binary searches per node)."""
+    rng = np.random.default_rng(90 + dim)
+    p = dev(rng.random((1_700_000, dim), dtype=np.float32))
+    h = tb.build_bvh(p)
+    assert_same_accel(h._aux["accel"], _standalone_accel(p, h), [p.shape[0]], dim)
+
+
 def test_fused_accel_matches_standalone_ragged():
     rng = np.random.default_rng(41)
     counts = [1, 3, 4096, 9000, 70_001, 2]

@@ -233,11 +233,149 @@ __global__ __launch_bounds__(kBlock) void accel_nodes_kernel(
 
 // Records of the radix-tree nodes the fused first tree pass could not
 // finish (their range spans two of its work-groups).  A work-group takes
-// kSpanGroups consecutive first-pass groups and runs their listed nodes
-// back to back, so its lanes stay busy; search and child boxes from global
-// memory (the finished implicit tree).
-constexpr int kSpanGroups = 8;
+// the listed nodes of kSpanGroups consecutive first-pass groups.  With one
+// lane per node, each node's searches are a chain of dependent code loads
+// (direction, exponential search, range search, split search: about
+// 3 log2(extent)), up to 63 for the nodes near the root at 1M points, and
+// the launch lasted as long as its longest chain (cfg2: 33 us for 34k
+// nodes, 8 per first-pass group, most of them short).  So a lane takes a
+// node only while its extent stays within kSpanLong positions (at most 8
+// steps per search); longer nodes (18% at cfg2) are queued and taken by
+// sub-groups of kSpanLanes lanes, where a search step probes 7 positions
+// at once and resolves 3 bits, and the child boxes' cover rows load in one
+// round trip.  Eight lanes for every node measured 18.5 us at cfg2 but
+// slower at 4M points and more (a wave per node in every 8 turned a launch
+// into several rounds of waves).
+constexpr int kSpanLanes = 8;
+constexpr int kSpanLong = 256;  // extents (positions from i) searched by one lane
+// Calls of at most this many points give every node a sub-group
+// (kSpanCoop): the waves still fit the chip in one round there, and the
+// first phase's chains (up to 27 loads) no longer come before the queue's.
+constexpr int64_t kSpanCoopPoints = int64_t(3) << 19;
+template <bool kCoop>
+constexpr int span_groups() { return kCoop ? 4 : 16; }
+
+// The 8 bits of `v` over this lane's sub-group (lanes [base, base + 8) of
+// the wave), lane base + j at bit j.
+__device__ __forceinline__ uint32_t span_ballot(bool v) {
+    const uint64_t m = __ballot(v);
+    return static_cast<uint32_t>(m >> (lane_id() & ~(kSpanLanes - 1))) & ((1u << kSpanLanes) - 1);
+}
+
+// Largest m in [0, 2^p) with pred(m), for a predicate that holds at 0 and
+// then fails from some point on: each step splits the interval into 8 (or
+// fewer, for the last bits) parts and lane j tests the start of part j + 1.
+template <class Pred>
+__device__ __forceinline__ int span_search(int p, int sl, Pred pred) {
+    int lo = 0;
+    while (p > 0) {
+        const int s3 = p < 3 ? p : 3;
+        p -= s3;
+        const int t = 1 << p;
+        const bool probe = sl < (1 << s3) - 1;
+        const uint32_t m = span_ballot(probe && pred(lo + (sl + 1) * t));
+        lo += __popc(m) * t;
+    }
+    return lo;
+}
+
+// karras_node by one sub-group: the same direction, extent and split
+// (every search below finds the boundary of a monotone predicate, which
+// the one-lane binary searches find too), from global codes.  The
+// exponential search starts at exponent p0 (prefix(i + 2^(p0 - 1) dir) >
+// dmin is known).
+__device__ __forceinline__ void span_karras_node(const CodeView& cv, int i, int sl, int p0, int& first, int& last,
+                                                 int& gamma) {
+    const uint32_t ci = cv.at(i);
+    int dir, dmin;
+    karras_dir(cv, i, ci, dir, dmin);
+    // Exponential search: the first p >= p0 with prefix(i + 2^p dir) <=
+    // dmin, 8 exponents per step (positions outside the cloud give -1).
+    int p = p0;
+    while (true) {
+        const int e = p + sl;
+        const uint32_t m = span_ballot(e < 30 && cv.prefix_len(i, ci, i + (1 << e) * dir) > dmin);
+        if (m != (1u << kSpanLanes) - 1) {
+            p += __builtin_ctz(~m);
+            break;
+        }
+        p += kSpanLanes;
+    }
+    const int l = span_search(p, sl, [&](int m) { return cv.prefix_len(i, ci, i + m * dir) > dmin; });
+    const int j = i + l * dir;
+    const int dnode = cv.prefix_len(i, ci, j);
+    const int split = span_search(p, sl, [&](int s) { return cv.prefix_len(i, ci, i + s * dir) > dnode; });
+    gamma = i + split * dir + (dir < 0 ? dir : 0);
+    first = min(i, j);
+    last = max(i, j);
+}
+
+// range_box of [a0, b0] and [a1, b1] by one sub-group.  The cover visits
+// at level u are those of range_box's loop in closed form: lo_u =
+// ceil(lo / 2^u), hi_u = floor(hi / 2^u), row lo_u - 1 when lo_u is odd
+// and row hi_u - 2 when hi_u is odd, while lo_u < hi_u.  Lane j loads the
+// rows of levels j, j + 8, ... together, merges them, and the sub-group
+// combines its lanes' boxes (min/max are exact and order-free on values).
 template <int D>
+__device__ __forceinline__ void span_range_boxes(const float* nodes, int vl, int L, int a0, int b0, int a1, int b1,
+                                                 int sl, float* box0, float* box1) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        box0[d] = FLT_MAX;
+        box0[D + d] = -FLT_MAX;
+        box1[d] = FLT_MAX;
+        box1[D + d] = -FLT_MAX;
+    }
+    const int64_t top = int64_t(1) << L;
+    const int64_t lo0 = a0 + top, hi0 = b0 + 1 + top, lo1 = a1 + top, hi1 = b1 + 1 + top;
+    // Levels sl + 8k, k < 4, in two halves (all 32 levels at once held
+    // 96 row floats in 3-D: 132 VGPRs); ranges below 2^16 points need only
+    // the first half's round trip.
+    constexpr int kRounds = 32 / kSpanLanes;
+#pragma unroll
+    for (int h = 0; h < kRounds; h += 2) {
+        float r[2][4][2 * D];
+        bool take[2][4];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int u = sl + (h + k) * kSpanLanes;
+            const int64_t up = (int64_t(1) << u) - 1;
+            const int64_t l0 = (lo0 + up) >> u, h0 = hi0 >> u, l1 = (lo1 + up) >> u, h1 = hi1 >> u;
+            const int64_t row[4] = {l0 - 1, h0 - 2, l1 - 1, h1 - 2};
+            take[k][0] = l0 < h0 && (l0 & 1);
+            take[k][1] = l0 < h0 && (h0 & 1);
+            take[k][2] = l1 < h1 && (l1 & 1);
+            take[k][3] = l1 < h1 && (h1 & 1);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (take[k][c]) {
+                    const float* src =
+                        nodes + static_cast<int64_t>(tree::memory_index(vl, L, static_cast<int>(row[c]))) * 2 * D;
+#pragma unroll
+                    for (int f = 0; f < 2 * D; ++f) r[k][c][f] = src[f];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            if (take[k][0]) merge_row<D>(box0, r[k][0]);
+            if (take[k][1]) merge_row<D>(box0, r[k][1]);
+            if (take[k][2]) merge_row<D>(box1, r[k][2]);
+            if (take[k][3]) merge_row<D>(box1, r[k][3]);
+        }
+    }
+#pragma unroll
+    for (int s = 1; s < kSpanLanes; s <<= 1) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            box0[d] = fminf(box0[d], __shfl_xor(box0[d], s, kWave));
+            box0[D + d] = fmaxf(box0[D + d], __shfl_xor(box0[D + d], s, kWave));
+            box1[d] = fminf(box1[d], __shfl_xor(box1[d], s, kWave));
+            box1[D + d] = fmaxf(box1[D + d], __shfl_xor(box1[D + d], s, kWave));
+        }
+    }
+}
+template <int D, bool kCoop>
 __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __restrict__ segs, int S,
                                                             int64_t groups_bound,
                                                             const uint32_t* __restrict__ sorted_codes,
@@ -246,9 +384,12 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
                                                             const float* __restrict__ node_aabbs,
                                                             float* __restrict__ records) {
     constexpr int R = 4 * D + 4;
+    constexpr int kSpanGroups = span_groups<kCoop>();
     __shared__ int s_seg[kSpanGroups];
     __shared__ uint32_t s_base[kSpanGroups + 1];
     __shared__ int64_t s_list0[kSpanGroups];
+    __shared__ uint32_t s_queue[kCoop ? 1 : kSpanGroups * kSubtreeLeaves];  // a group lists at most its own nodes
+    __shared__ uint32_t s_queued;
     const int tid = threadIdx.x;
     if (tid < kSpanGroups) {
         const int64_t G = static_cast<int64_t>(blockIdx.x) * kSpanGroups + tid;
@@ -275,31 +416,77 @@ __global__ __launch_bounds__(kBlock) void accel_span_kernel(const Segment* __res
         for (int k = 1; k <= kSpanGroups; ++k) s_base[k] += s_base[k - 1];
     }
     __syncthreads();
-    for (uint32_t e = tid; e < s_base[kSpanGroups]; e += kBlock) {
+    // Phase 1, one lane per node: direction and exponential search up to
+    // kSpanLong positions; a node whose range reaches that far is queued for
+    // phase 2, every other one finished here (searches of at most 8 steps).
+    const auto node_of = [&](uint32_t e, Segment& g, int& i) {
         int k = 0;
         while (e >= s_base[k + 1]) ++k;
-        const int sg = s_seg[k];
-        const Segment g = segs[sg];
-        const int i = static_cast<int>(span_list[s_list0[k] + (e - s_base[k])]);
-        if (i < 0 || i >= g.n - 1) continue;  // never for entries the tree pass wrote
+        g = segs[s_seg[k]];
+        i = static_cast<int>(span_list[s_list0[k] + (e - s_base[k])]);
+        return i >= 0 && i < g.n - 1;  // always, for entries the tree pass wrote
+    };
+    const auto view = [&](const Segment& g) {
         CodeView cv;
         cv.codes = sorted_codes + g.start;
         cv.win = nullptr;
         cv.w_lo = 0;
         cv.w_hi = 0;
         cv.n = g.n;
+        return cv;
+    };
+    if (tid == 0) s_queued = kCoop ? s_base[kSpanGroups] : 0u;
+    __syncthreads();
+    for (uint32_t e = tid; !kCoop && e < s_base[kSpanGroups]; e += kBlock) {
+        Segment g;
+        int i;
+        if (!node_of(e, g, i)) continue;
+        const CodeView cv = view(g);
+        const uint32_t ci = cv.at(i);
+        int dir, dmin;
+        karras_dir(cv, i, ci, dir, dmin);
+        int lmax = 2;
+        while (cv.prefix_len(i, ci, i + lmax * dir) > dmin) {
+            lmax <<= 1;
+            if (lmax > kSpanLong) break;
+        }
+        if (lmax > kSpanLong) {
+            if constexpr (!kCoop) s_queue[atomicAdd(&s_queued, 1u)] = e;
+            continue;
+        }
         int first, last, gamma;
-        karras_node(cv, i, first, last, gamma);
+        karras_range(cv, i, ci, dir, dmin, lmax, first, last, gamma);
         // A node inside a bucket is never referenced; it must not write,
         // since its child links would overwrite the bucket's own link.
         if (i != 0 && last - first + 1 <= accel_bucket<D>()) continue;
         const float* nodes = node_aabbs + g.node_start * 2 * D;
-        float* rec = records + (g.start + i) * R;
         float lbox[2 * D], rbox[2 * D];
         range_box<D>(nodes, g.vl, g.leaf_level, first, gamma, lbox);
         range_box<D>(nodes, g.vl, g.leaf_level, gamma + 1, last, rbox);
-        store_boxes<D>(rec, lbox, rbox);
+        store_boxes<D>(records + (g.start + i) * R, lbox, rbox);
         link_record<D>(records + g.start * R, i, first, gamma, last);
+    }
+    __syncthreads();
+    // Phase 2: sub-group `sub` (lanes sl = 0..7) takes queued nodes sub,
+    // sub + 32, ... (kCoop: every listed node, from exponent 1); every
+    // decision below is uniform over the sub-group.
+    const int sub = tid / kSpanLanes;
+    const int sl = tid % kSpanLanes;
+    constexpr int kLongExp = __builtin_ctz(kSpanLong);
+    for (uint32_t q = sub; q < s_queued; q += kBlock / kSpanLanes) {
+        Segment g;
+        int i;
+        if (!node_of(kCoop ? q : s_queue[q], g, i)) continue;
+        int first, last, gamma;
+        span_karras_node(view(g), i, sl, kCoop ? 1 : kLongExp + 1, first, last, gamma);
+        if (kCoop && i != 0 && last - first + 1 <= accel_bucket<D>()) continue;
+        const float* nodes = node_aabbs + g.node_start * 2 * D;
+        float lbox[2 * D], rbox[2 * D];
+        span_range_boxes<D>(nodes, g.vl, g.leaf_level, first, gamma, gamma + 1, last, sl, lbox, rbox);
+        if (sl == 0) {
+            store_boxes<D>(records + (g.start + i) * R, lbox, rbox);
+            link_record<D>(records + g.start * R, i, first, gamma, last);
+        }
     }
 }
 
@@ -377,13 +564,15 @@ hipError_t launch_accel_span(const float* node_aabbs, int D, const Segment* segs
     if (total - S <= 0) return hipSuccess;
     float* records = reinterpret_cast<float*>(static_cast<char*>(accel) + accel_points_bytes(total));
     const int Si = static_cast<int>(S);
-    const unsigned grid = static_cast<unsigned>((groups_bound + kSpanGroups - 1) / kSpanGroups);
+    auto run = [&](auto kernel, int groups) {
+        kernel<<<static_cast<unsigned>((groups_bound + groups - 1) / groups), kBlock, 0, stream>>>(
+            segs, Si, groups_bound, sorted_codes, span_list, span_count, node_aabbs, records);
+    };
+    const bool coop = total <= kSpanCoopPoints;
     if (D == 3) {
-        accel_span_kernel<3><<<grid, kBlock, 0, stream>>>(segs, Si, groups_bound, sorted_codes, span_list,
-                                                          span_count, node_aabbs, records);
+        coop ? run(accel_span_kernel<3, true>, span_groups<true>()) : run(accel_span_kernel<3, false>, span_groups<false>());
     } else {
-        accel_span_kernel<2><<<grid, kBlock, 0, stream>>>(segs, Si, groups_bound, sorted_codes, span_list,
-                                                          span_count, node_aabbs, records);
+        coop ? run(accel_span_kernel<2, true>, span_groups<true>()) : run(accel_span_kernel<2, false>, span_groups<false>());
     }
     return hipGetLastError();
 }
