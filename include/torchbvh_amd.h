@@ -369,9 +369,9 @@ int tbvh_knn_accel_spatial(const void* accel, const float* queries, const int64_
  * the others, and every query of a cloud that is not near-uniform (a long
  * empty run of cells, a non-finite point, cells out of the points' order),
  * run the accel traversal seeded with that k-th distance.  Workspace:
- * tbvh_knn_accel_grid_workspace_size (0 for clouds too small for a grid:
- * then this is tbvh_knn_accel); a null workspace also runs
- * tbvh_knn_accel. */
+ * tbvh_knn_accel_grid_workspace_size (0 for clouds too small for a grid
+ * or of 2^24 points or more: then this is tbvh_knn_accel); a null
+ * workspace also runs tbvh_knn_accel. */
 int tbvh_knn_accel_grid_workspace_size(int64_t B, int64_t M, int64_t num_leaves, int D, int k,
                                        size_t* bytes);
 int tbvh_knn_accel_grid(const void* accel, const float* node_aabbs, int64_t num_real_nodes,

@@ -165,8 +165,11 @@ def test_grid_knn_workspace_and_argument_errors():
     expect = up(up(up(up(up(up(up(table * 4) + 4) + 4) + tiles * 8) + tiles * 4) + (tiles + 1023) // 1024 * 4)
                 + M * 4)
     assert size.value == up(expect + M * 4)
-    # k = 32 keeps the traversal: no workspace.
-    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 32, ctypes.byref(size)) == 0 and size.value == 0
+    # k = 32 aims at 8 points per cell: 2^17 cells, rounded to the nearest level (2^18).
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 32, ctypes.byref(size)) == 0
+    assert size.value == up(expect + M * 4)
+    # Clouds of 2^24 points or more keep the traversal (run starts are packed into 24 bits).
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 24, 3, 16, ctypes.byref(size)) == 0 and size.value == 0
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 4, 16, ctypes.byref(size)) == 1
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 5, ctypes.byref(size)) == 1
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 16, None) == 1

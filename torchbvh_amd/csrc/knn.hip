@@ -969,10 +969,11 @@ knn_accel_kernel(KnnArgs a) {
 // the strict order with the rest.  Queries that fail (or find the block too
 // full, or whose cloud the table kernel disabled) go to the accel traversal
 // with the block's k-th distance as the starting bound.  Measured on MI355X
-// (traversal, same inputs, cell-block path against the traversal alone):
-// cfg2 0.588 -> 0.569 ms (scan 0.40, fallback over 13% of the queries 0.14,
-// table and list 0.02), cfg4 0.923 -> 0.699 ms, cfg3 (clouds disabled:
-// long empty runs) 1.144 -> 1.168 ms.
+// (k-NN call, same inputs, cell-block path against the traversal alone):
+// cfg2 0.58 -> 0.43 ms (scan 0.25, fallback over 13% of the queries 0.12,
+// table and list 0.02), 3-D k = 8 0.54 -> 0.34, cfg4 0.92 -> 0.68, 2-D
+// k = 32 2.00 -> 1.53, 3-D k = 32 0.97 -> 0.94, cfg3 (clouds disabled:
+// long empty runs) 1.16 -> 1.17 ms.
 // ---------------------------------------------------------------------------
 template <int D>
 constexpr int grid_axis_bits() { return D == 3 ? 10 : 16; }
@@ -1066,26 +1067,53 @@ __global__ __launch_bounds__(kBlock) void grid_table_kernel(const float4* __rest
     for (int64_t c = own + 1; c <= last; ++c) t[c] = n;
 }
 
+// The block's cells as offsets from the query's cell, its own first, then
+// those sharing a face with it, an edge, a corner: each (dx + 1) | (dy + 1)
+// << 2 | (dz + 1) << 4.  Near cells first make the list's k-th distance
+// small early, so later chunks more often hold nothing for any lane and
+// skip their merge.
+template <int D>
+struct NearOrder {
+    static constexpr int kCells = D == 3 ? 27 : 9;
+    uint8_t off[kCells];
+    constexpr NearOrder() : off{} {
+        int k = 0;
+        for (int m = 0; m <= D; ++m) {
+            for (int c = 0; c < kCells; ++c) {
+                const int dx = c % 3 - 1, dy = c / 3 % 3 - 1, dz = D == 3 ? c / 9 - 1 : 0;
+                if ((dx != 0) + (dy != 0) + (dz != 0) == m) off[k++] = static_cast<uint8_t>((dx + 1) | (dy + 1) << 2 | (dz + 1) << 4);
+            }
+        }
+    }
+};
+
 // One query per lane, in launch order like the traversal (same tile map).
 // Failing queries are recorded per tile (a mask of its lanes, bounds[gid]
 // their block's k-th distance, FLT_MAX where none was taken), so that
 // grid_offsets_kernel and grid_list_kernel list them in launch order.
+//
+// A lane first reads the runs of its block's cells (first point and count,
+// packed into one LDS word per cell: clouds of at most 2^24 points, runs of
+// at most 255, more sends the query to the traversal) and then streams
+// them as one sequence, kChunk points per merge, a chunk taking the rest of
+// one run and the start of the next.  Scanning cell by cell in lockstep,
+// a cell cost the wave as many chunks as its fullest lane needed (at 4
+// points per cell, nearly always two chunks of 6 somewhere among 64 lanes:
+// about 55 merges per wave at cfg2); the stream costs ceil(points / 8) per
+// lane.
 template <int D, int K, bool kOrdered>
 __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const float* __restrict__ node_aabbs, int64_t nr,
                                                          int level, const int32_t* __restrict__ table,
                                                          const uint32_t* __restrict__ flags, uint64_t* __restrict__ masks,
                                                          float* __restrict__ bounds) {
-    constexpr int kCells = D == 3 ? 27 : 9;
-    // Points merged per pass, the bucket size.  12 per pass in 3-D (two
-    // sorted halves, merge_candidates12: one pass per cell where 6 take two,
-    // since some lane of 64 nearly always holds more than 6) measured the
-    // same at k = 16 (110 VGPRs, a wave per SIMD less) and slower at k = 4
-    // and 8, whose cells hold fewer points.
-    constexpr int kChunk = accel_bucket<D>();
+    constexpr int kCells = NearOrder<D>::kCells;
+    constexpr int kChunk = 8;
+    __shared__ uint32_t s_runs[kCells * kKnnBlock];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     if (tile * kKnnBlock >= a.total_q) return;  // surplus tiles (whole waves)
-    const int64_t gid = tile * kKnnBlock + threadIdx.x;
+    const int lane = threadIdx.x;
+    const int64_t gid = tile * kKnnBlock + lane;
     // Lanes past the last query take no part; a lane whose cloud is
     // disabled goes to the fallback at once (which also handles a corrupt
     // order entry: no result).  A lane on a corrupt entry here takes no part.
@@ -1094,7 +1122,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     bool ok = valid && flags[b] == 0u;
     if (__ballot(ok) == 0) {
         const uint64_t left = __ballot(valid);
-        if (threadIdx.x == 0) masks[tile] = left;
+        if (lane == 0) masks[tile] = left;
         if (valid) bounds[gid] = kFar;
         return;
     }
@@ -1124,65 +1152,83 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     grid_cell<D>(q, lo, hi, shift, c);
     const int64_t cells = int64_t(1) << (D * level);
     const int32_t* t = table + b * (cells + 1);
-    // A block is searched only while its point count stays near the cloud's
-    // mean (4x): a lane that passes the cap stops and goes to the traversal.
+    // The block's runs, nearest cells first.  The search is kept only while
+    // the block's point count stays near the cloud's mean (4x); past that,
+    // or a run longer than a count field holds, the lane goes to the
+    // traversal.
+    constexpr NearOrder<D> kOrder{};
     const int cap = 4 * kCells * static_cast<int>((n + cells - 1) / cells);
     int total = 0;
+#pragma unroll
+    for (int j = 0; j < kCells; ++j) {
+        const int o = kOrder.off[j];
+        const int x = static_cast<int>(c[0]) + (o & 3) - 1, y = static_cast<int>(c[1]) + (o >> 2 & 3) - 1;
+        const int z = D == 3 ? static_cast<int>(c[D - 1]) + (o >> 4) - 1 : 0;
+        const bool inside = ok && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
+        uint32_t cell[D];
+        cell[0] = static_cast<uint32_t>(x);
+        cell[1] = static_cast<uint32_t>(y);
+        if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
+        const uint32_t id = inside ? grid_cell_id<D>(cell) : 0u;
+        // Entries of an enabled cloud lie in [0, n]; clamped all the same.
+        const int rs = inside ? min(max(t[id], 0), n) : 0;
+        const int re = inside ? min(max(t[id + 1], rs), n) : 0;
+        total += re - rs;
+        ok = ok && re - rs <= 255;
+        s_runs[j * kKnnBlock + lane] = static_cast<uint32_t>(rs) << 8 | static_cast<uint32_t>(min(re - rs, 255));
+    }
+    ok = ok && total <= cap;
     uint64_t best[K];
 #pragma unroll
     for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
     const float4* pts = static_cast<const float4*>(a.accel) + in.pstart;
-    // Cell by cell (reading a slab's runs together measured the same), in
-    // one loop body: unrolled, each copy kept the list in other registers
-    // (116 VGPRs at 3-D k = 16).  Offsets (dx, dy, dz) run over {-1, 0, 1}
-    // (dz only in 3-D).
-    int dx = -1, dy = -1, dz = D == 3 ? -1 : 0;
-#pragma unroll 1
-    for (int j = 0; j < kCells; ++j) {
-        {
-            const int x = static_cast<int>(c[0]) + dx, y = static_cast<int>(c[1]) + dy;
-            const int z = D == 3 ? static_cast<int>(c[D - 1]) + dz : 0;
-            const bool inside = ok && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
-            uint32_t cell[D];
-            cell[0] = static_cast<uint32_t>(x);
-            cell[1] = static_cast<uint32_t>(y);
-            if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
-            const uint32_t id = inside ? grid_cell_id<D>(cell) : 0u;
-            if (++dx == 2) {
-                dx = -1;
-                if (++dy == 2) {
-                    dy = -1;
-                    ++dz;
-                }
-            }
-            // Entries of an enabled cloud lie in [0, n]; clamped all the same.
-            int s = inside ? min(max(t[id], 0), n) : 0;
-            int e = inside ? min(max(t[id + 1], s), n) : 0;
-            total += e - s;
-            if (total > cap) {
-                ok = false;
-                e = s;
-            }
-            while (__ballot(s < e) != 0) {
-                const int cnt = e - s;
-                // Rows past the run read at most kChunk - 1 rows past the
-                // cloud's last point, inside the accel buffer (as the bucket
-                // scans do: the points area's padding and the record rows,
-                // >= 48 bytes per point, follow the last cloud).
-                const float4* r4 = pts + (s < e ? s : 0);
-                float4 p[kChunk];
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) p[u] = r4[u];
-                uint64_t cand[kChunk];
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) {
-                    const float dd = point_distance<D>(q, p[u]);
-                    cand[u] = u < cnt && dd < kFar ? candidate_key(dd, __float_as_uint(p[u].w)) : kEmptyKey;
-                }
-                merge_candidates<K, kChunk>(best, cand);
-                s += kChunk;
-            }
+    // Cursor: run j, its next point s and its end e (a lane that is not ok
+    // starts at the end).
+    int j = ok ? 0 : kCells - 1;
+    int s = 0, e = 0;
+    if (ok) {
+        const uint32_t r = s_runs[lane];
+        s = static_cast<int>(r >> 8);
+        e = s + static_cast<int>(r & 255u);
+    }
+    // Moves to the next run with points left, if any.
+    const auto advance = [&]() {
+        while (s == e && j < kCells - 1) {
+            ++j;
+            const uint32_t r = s_runs[j * kKnnBlock + lane];
+            s = static_cast<int>(r >> 8);
+            e = s + static_cast<int>(r & 255u);
         }
+    };
+    // A chunk takes the rest of the current run and the start of the next
+    // (one run per chunk measured +13% at cfg2, three the same as two; 12
+    // points per chunk slower).
+    while (true) {
+        advance();
+        const int s0 = s;
+        const int n0 = min(e - s, kChunk);
+        s += n0;
+        if (__ballot(n0 > 0) == 0) break;  // every lane's runs are exhausted
+        advance();
+        const int s1 = s - n0;  // slot u >= n0 takes point s1 + u
+        const int n1 = min(e - s, kChunk - n0);
+        s += n1;
+        float4 p[kChunk];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            const int row = u < n0 ? s0 + u : u < n0 + n1 ? s1 + u : 0;
+            p[u] = pts[row];
+        }
+        uint64_t cand[kChunk];
+        uint64_t least = kEmptyKey;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            const float dd = point_distance<D>(q, p[u]);
+            cand[u] = u < n0 + n1 && dd < kFar ? candidate_key(dd, __float_as_uint(p[u].w)) : kEmptyKey;
+            least = key_min(least, cand[u]);
+        }
+        // A chunk that improves no lane's list needs no merge.
+        if (__ballot(least < best[K - 1]) != 0) merge_candidates<K, kChunk>(best, cand);
     }
     // Distance from the query to the block's boundary, where points lie
     // beyond it (a block side at the grid's edge has none).
@@ -1209,7 +1255,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
         write_results<K, D>(a, out.out_row, best, 0, out.pstart);
     }
     const uint64_t left = __ballot(valid && !done);
-    if (threadIdx.x == 0) masks[tile] = left;
+    if (lane == 0) masks[tile] = left;
     if (valid && !done) bounds[gid] = ok ? worst : kFar;
 }
 
@@ -1331,9 +1377,8 @@ hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStre
 // model).  0 when the cloud is too small for a grid of at least 4 cells
 // per axis; at most 2^24 cells.
 int grid_level(int64_t n, int D, int K) {
-    // At k = 32 the block's 27 * 8 points cost more than the traversal
-    // (uniform 1M points, 3-D: +29%).
-    if (K > 16) return 0;
+    // Run starts (at most n) are packed into 24 bits.
+    if (n >= (int64_t(1) << 24)) return 0;
     const double rho = D == 3 ? std::max(1, K / 4) : std::max(2, K / 2);
     const double cells = static_cast<double>(n) / rho;
     int l = static_cast<int>(std::lround(std::log2(std::max(cells, 1.0)) / D));
@@ -1408,12 +1453,13 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
     if (D == 3) grid_table_kernel<3><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
     else grid_table_kernel<2><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
     auto run = [&](auto dk) { dk(args, node_aabbs, nr, level, table, flags, masks, bounds, stream); };
-    // k <= 16 (grid_level).
+    // k in {4, 8, 16, 32} (supported_k).
     if (D == 3) {
         switch (K) {
             case 4: run(launch_grid_dk<3, 4>); break;
             case 8: run(launch_grid_dk<3, 8>); break;
             case 16: run(launch_grid_dk<3, 16>); break;
+            case 32: run(launch_grid_dk<3, 32>); break;
             default: return hipErrorInvalidValue;
         }
     } else {
@@ -1421,6 +1467,7 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
             case 4: run(launch_grid_dk<2, 4>); break;
             case 8: run(launch_grid_dk<2, 8>); break;
             case 16: run(launch_grid_dk<2, 16>); break;
+            case 32: run(launch_grid_dk<2, 32>); break;
             default: return hipErrorInvalidValue;
         }
     }
