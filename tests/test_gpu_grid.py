@@ -99,6 +99,25 @@ def test_nonfinite_queries():
     check_single(p, q, 16, "non-finite queries")
 
 
+@pytest.mark.parametrize("k", [8, 16])
+def test_void_sends_queries_through_every_stage(k):
+    """A uniform cloud with a spherical hole of about two cells' radius:
+    queries near its rim miss the first 3^3 block's margin and are decided by
+    the second (5^3, cells beyond the first k-th distance dropped); queries
+    deep inside keep too many cells or miss that margin too and take the
+    traversal.  Every row against the oracle."""
+    rng = np.random.default_rng(15 + k)
+    p = rng.random((300_000, 3), dtype=np.float32)
+    centre = np.float32(0.5)
+    p = p[np.linalg.norm(p - centre, axis=1) > 0.07]
+    q = rng.random((Q, 3), dtype=np.float32)
+    inside = q.shape[0] // 4
+    d = rng.normal(size=(inside, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    q[:inside] = (centre + d * rng.random((inside, 1)) * 0.09).astype(np.float32)
+    check_single(p, q, k, f"void k={k}")
+
+
 def test_clustered_cloud_falls_back():
     rng = np.random.default_rng(10)
     centres = rng.random((8, 3), dtype=np.float32)

@@ -1067,25 +1067,109 @@ __global__ __launch_bounds__(kBlock) void grid_table_kernel(const float4* __rest
     for (int64_t c = own + 1; c <= last; ++c) t[c] = n;
 }
 
-// The block's cells as offsets from the query's cell, its own first, then
-// those sharing a face with it, an edge, a corner: each (dx + 1) | (dy + 1)
-// << 2 | (dz + 1) << 4.  Near cells first make the list's k-th distance
-// small early, so later chunks more often hold nothing for any lane and
-// skip their merge.
-template <int D>
+// The cells of a block of (2W + 1)^D cells as offsets from the query's
+// cell, nearest first (by squared offset, then in storage order): its own,
+// then (W = 1) those sharing a face with it, an edge, a corner.  Each is
+// (dx + W) | (dy + W) << 3 | (dz + W) << 6.  Near cells first make the
+// list's k-th distance small early, so later chunks more often hold
+// nothing for any lane and skip their merge.
+template <int D, int W>
 struct NearOrder {
-    static constexpr int kCells = D == 3 ? 27 : 9;
-    uint8_t off[kCells];
+    static constexpr int kSide = 2 * W + 1;
+    static constexpr int kCells = D == 3 ? kSide * kSide * kSide : kSide * kSide;
+    uint16_t off[kCells];
     constexpr NearOrder() : off{} {
         int k = 0;
-        for (int m = 0; m <= D; ++m) {
+        for (int m = 0; m <= D * W * W; ++m) {
             for (int c = 0; c < kCells; ++c) {
-                const int dx = c % 3 - 1, dy = c / 3 % 3 - 1, dz = D == 3 ? c / 9 - 1 : 0;
-                if ((dx != 0) + (dy != 0) + (dz != 0) == m) off[k++] = static_cast<uint8_t>((dx + 1) | (dy + 1) << 2 | (dz + 1) << 4);
+                const int dx = c % kSide - W, dy = c / kSide % kSide - W, dz = D == 3 ? c / (kSide * kSide) - W : 0;
+                if (dx * dx + dy * dy + dz * dz == m) {
+                    off[k++] = static_cast<uint16_t>((dx + W) | (dy + W) << 3 | (dz + W) << 6);
+                }
             }
         }
     }
+    static constexpr int dx(int o) { return (o & 7) - W; }
+    static constexpr int dy(int o) { return (o >> 3 & 7) - W; }
+    static constexpr int dz(int o) { return D == 3 ? (o >> 6) - W : 0; }
 };
+
+// Streams one lane's runs into its list: `runs` is the lane's column of
+// packed runs ((first point << 8) | count, kKnnBlock words apart), `nruns`
+// of them, `pts` the cloud's accel points.  A chunk takes the rest of the
+// current run and the start of the next (one run per chunk measured +13% at
+// cfg2, three the same as two; 12 points per chunk slower).
+template <int D, int K>
+__device__ __forceinline__ void grid_stream(const uint32_t* runs, int nruns, const float4* pts, const float* q,
+                                            uint64_t (&best)[K]) {
+    constexpr int kChunk = 8;
+    // Cursor: run j, its next point s and its end e.
+    int j = 0, s = 0, e = 0;
+    if (nruns > 0) {
+        const uint32_t r = runs[0];
+        s = static_cast<int>(r >> 8);
+        e = s + static_cast<int>(r & 255u);
+    }
+    // Moves to the next run with points left, if any.
+    const auto advance = [&]() {
+        while (s == e && j < nruns - 1) {
+            ++j;
+            const uint32_t r = runs[j * kKnnBlock];
+            s = static_cast<int>(r >> 8);
+            e = s + static_cast<int>(r & 255u);
+        }
+    };
+    while (true) {
+        advance();
+        const int s0 = s;
+        const int n0 = min(e - s, kChunk);
+        s += n0;
+        if (__ballot(n0 > 0) == 0) break;  // every lane's runs are exhausted
+        advance();
+        const int s1 = s - n0;  // slot u >= n0 takes point s1 + u
+        const int n1 = min(e - s, kChunk - n0);
+        s += n1;
+        float4 p[kChunk];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            const int row = u < n0 ? s0 + u : u < n0 + n1 ? s1 + u : 0;
+            p[u] = pts[row];
+        }
+        uint64_t cand[kChunk];
+        uint64_t least = kEmptyKey;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            const float dd = point_distance<D>(q, p[u]);
+            cand[u] = u < n0 + n1 && dd < kFar ? candidate_key(dd, __float_as_uint(p[u].w)) : kEmptyKey;
+            least = key_min(least, cand[u]);
+        }
+        // A chunk that improves no lane's list needs no merge.
+        if (__ballot(least < best[K - 1]) != 0) merge_candidates<K, kChunk>(best, cand);
+    }
+}
+
+// Distance from the query to the boundary of the block of cells c - w ..
+// c + w per axis, where points lie beyond it (a block side at the grid's
+// edge has none), less the slack (1e-5 of the larger of the box's extents
+// and its coordinates' magnitudes) that covers the rounding of the
+// quantisation, of the boundary and of the distances.
+template <int D>
+__device__ __forceinline__ float grid_safe_margin(const float* q, const float* root, const uint32_t (&c)[D], int shift,
+                                                  int G, int w) {
+    float margin = INFINITY;
+    float size = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const float lo = root[d], hi = root[D + d];
+        const float ext = hi - lo;
+        size = fmaxf(size, fmaxf(ext, fmaxf(fabsf(lo), fabsf(hi))));
+        const int b0 = static_cast<int>(c[d]) - w, b1 = static_cast<int>(c[d]) + w + 1;
+        const float scale = ext / static_cast<float>(1u << grid_axis_bits<D>());
+        if (b0 > 0) margin = fminf(margin, q[d] - (lo + static_cast<float>(b0 << shift) * scale));
+        if (b1 < G) margin = fminf(margin, (lo + static_cast<float>(b1 << shift) * scale) - q[d]);
+    }
+    return margin - 1e-5f * size;
+}
 
 // One query per lane, in launch order like the traversal (same tile map).
 // Failing queries are recorded per tile (a mask of its lanes, bounds[gid]
@@ -1106,8 +1190,8 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
                                                          int level, const int32_t* __restrict__ table,
                                                          const uint32_t* __restrict__ flags, uint64_t* __restrict__ masks,
                                                          float* __restrict__ bounds) {
-    constexpr int kCells = NearOrder<D>::kCells;
-    constexpr int kChunk = 8;
+    using Order = NearOrder<D, 1>;
+    constexpr int kCells = Order::kCells;
     __shared__ uint32_t s_runs[kCells * kKnnBlock];
     const int64_t per_xcd = gridDim.x / kXcds;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
@@ -1156,14 +1240,14 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     // the block's point count stays near the cloud's mean (4x); past that,
     // or a run longer than a count field holds, the lane goes to the
     // traversal.
-    constexpr NearOrder<D> kOrder{};
+    constexpr Order kOrder{};
     const int cap = 4 * kCells * static_cast<int>((n + cells - 1) / cells);
     int total = 0;
 #pragma unroll
     for (int j = 0; j < kCells; ++j) {
         const int o = kOrder.off[j];
-        const int x = static_cast<int>(c[0]) + (o & 3) - 1, y = static_cast<int>(c[1]) + (o >> 2 & 3) - 1;
-        const int z = D == 3 ? static_cast<int>(c[D - 1]) + (o >> 4) - 1 : 0;
+        const int x = static_cast<int>(c[0]) + Order::dx(o), y = static_cast<int>(c[1]) + Order::dy(o);
+        const int z = D == 3 ? static_cast<int>(c[D - 1]) + Order::dz(o) : 0;
         const bool inside = ok && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
         uint32_t cell[D];
         cell[0] = static_cast<uint32_t>(x);
@@ -1181,6 +1265,9 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     uint64_t best[K];
 #pragma unroll
     for (int i = 0; i < K; ++i) best[i] = candidate_key(kFar, 0xffffffffu);
+    // The stream of grid_stream, written out here: as a call it came out at
+    // 136 VGPRs instead of 89 at 3-D k = 16 (3 waves per SIMD instead of 5).
+    constexpr int kChunk = 8;
     const float4* pts = static_cast<const float4*>(a.accel) + in.pstart;
     // Cursor: run j, its next point s and its end e (a lane that is not ok
     // starts at the end).
@@ -1230,23 +1317,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
         // A chunk that improves no lane's list needs no merge.
         if (__ballot(least < best[K - 1]) != 0) merge_candidates<K, kChunk>(best, cand);
     }
-    // Distance from the query to the block's boundary, where points lie
-    // beyond it (a block side at the grid's edge has none).
-    float margin = INFINITY;
-    float size = 0.0f;  // the larger of the extents and the coordinates' magnitudes
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        // The box again (not held through the scan).
-        lo[d] = root[d];
-        hi[d] = root[D + d];
-        const float ext = hi[d] - lo[d];
-        size = fmaxf(size, fmaxf(ext, fmaxf(fabsf(lo[d]), fabsf(hi[d]))));
-        const int b0 = static_cast<int>(c[d]) - 1, b1 = static_cast<int>(c[d]) + 2;
-        const float scale = ext / static_cast<float>(1u << grid_axis_bits<D>());
-        if (b0 > 0) margin = fminf(margin, q[d] - (lo[d] + static_cast<float>(b0 << shift) * scale));
-        if (b1 < G) margin = fminf(margin, (lo[d] + static_cast<float>(b1 << shift) * scale) - q[d]);
-    }
-    const float safe = margin - 1e-5f * size;
+    const float safe = grid_safe_margin<D>(q, root, c, shift, G, 1);
     const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
     const bool done = ok && safe > 0.0f && worst < safe * safe;
     if (done) {
@@ -1259,18 +1330,158 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     if (valid && !done) bounds[gid] = ok ? worst : kFar;
 }
 
+// Second pass over the first pass's failures (list[0 .. *count), launch
+// positions; bounds[gid] the k-th distance of the first block's list,
+// FLT_MAX where it had none): the block of 5^D cells around the query, less
+// the cells that lie wholly beyond that distance (lower bound of their
+// points' distances, short by the slack, greater than it: no such point can
+// enter the final list, whose k-th distance is at most the bound).  Its
+// margin is at least two cells, so nearly every query the first block
+// missed by a little is decided here; the list starts seeded with (bound,
+// 0xffffffff) entries (displaced by the k points within the bound, which
+// all lie in the kept cells).  Failures go to the traversal with this
+// list's k-th distance, per tile of list positions as in the first pass.
+// Run for 3-D k = 8 and 16 only (grid_second_pass).  At cfg2 the first pass
+// leaves 13% of the queries, which the traversal answered in 117 us; with
+// this pass the whole call measured 0.425 -> 0.386 ms (3-D k = 8: 0.344 ->
+// 0.310), but +50% at 3-D k = 4 (0.5 points per cell: 125 cells to cull
+// and more first-pass failures), +5% in 2-D (first-pass failures rare: its
+// three launches cost more than they save), +4% at k = 32.
+constexpr int kGridRuns2 = 64;  // kept cells per lane (more: the traversal)
+template <int D, int K, bool kOrdered>
+__global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const float* __restrict__ node_aabbs,
+                                                          int64_t nr, int level, const int32_t* __restrict__ table,
+                                                          const int32_t* __restrict__ list,
+                                                          const uint32_t* __restrict__ count,
+                                                          uint64_t* __restrict__ masks, float* __restrict__ bounds) {
+    using Order = NearOrder<D, 2>;
+    constexpr int kCells = Order::kCells;
+    __shared__ uint32_t s_runs[kGridRuns2 * kKnnBlock];
+    const int64_t listed = *count;
+    const int64_t per_xcd = ((listed + kKnnBlock - 1) / kKnnBlock + kXcds - 1) / kXcds;
+    if (blockIdx.x / kXcds >= per_xcd) return;
+    const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (tile * kKnnBlock >= listed) return;  // surplus tiles (whole waves)
+    const int lane = threadIdx.x;
+    const int64_t pos = tile * kKnnBlock + lane;
+    const bool valid = pos < listed;
+    const int64_t gid = valid ? list[pos] : 0;
+    const float seed = valid ? bounds[gid] : kFar;
+    // Lanes without a bound (disabled cloud, full block, non-finite query,
+    // corrupt order entry) go on to the traversal.
+    bool ok = valid && seed < kFar;
+    if (__ballot(ok) == 0) {
+        const uint64_t left = __ballot(valid);
+        if (lane == 0) masks[tile] = left;
+        return;
+    }
+    QueryLoc in{};
+    if (ok) {
+        in = locate<kOrdered, false, false, true>(a, gid);
+        ok = in.row >= 0;
+    }
+    const int n = a.num_leaves;
+    const int64_t b = ok ? gid / a.M : 0;
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) q[d] = ok ? a.queries[in.row * D + d] : 0.0f;
+    const float* root = node_aabbs + b * nr * 2 * D;
+    float lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        lo[d] = root[d];
+        hi[d] = root[D + d];
+    }
+    const int shift = grid_axis_bits<D>() - level;
+    const int G = 1 << level;
+    uint32_t c[D];
+    grid_cell<D>(q, lo, hi, shift, c);
+    // Squared lower bounds of |p_d - q_d| for points in the cells at offset
+    // -2 .. 2 on each axis: the distance to the nearer face of the column,
+    // short by the slack (as in grid_safe_margin), 0 for the query's own.
+    float lb[D][5];
+    {
+        float size = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) size = fmaxf(size, fmaxf(hi[d] - lo[d], fmaxf(fabsf(lo[d]), fabsf(hi[d]))));
+        const float slack = 1e-5f * size;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const float scale = (hi[d] - lo[d]) / static_cast<float>(1u << grid_axis_bits<D>());
+            const auto face = [&](int k) { return lo[d] + static_cast<float>((static_cast<int>(c[d]) + k) << shift) * scale; };
+            const float f[5] = {q[d] - face(-1), q[d] - face(0), 0.0f, face(1) - q[d], face(2) - q[d]};
+#pragma unroll
+            for (int k = 0; k < 5; ++k) {
+                const float v = fmaxf(f[k] - slack, 0.0f);
+                lb[d][k] = k == 2 ? 0.0f : v * v;
+            }
+        }
+    }
+    const int64_t cells = int64_t(1) << (D * level);
+    const int32_t* t = table + b * (cells + 1);
+    constexpr Order kOrder{};
+    int nruns = 0;
+#pragma unroll
+    for (int j = 0; j < kCells; ++j) {
+        const int o = kOrder.off[j];
+        const int ox = Order::dx(o), oy = Order::dy(o), oz = Order::dz(o);
+        const int x = static_cast<int>(c[0]) + ox, y = static_cast<int>(c[1]) + oy;
+        const int z = D == 3 ? static_cast<int>(c[D - 1]) + oz : 0;
+        float bound = lb[0][ox + 2] + lb[1][oy + 2];
+        if constexpr (D == 3) bound += lb[D - 1][oz + 2];
+        const bool keep = ok && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G && !(bound > seed);
+        if (keep) {
+            uint32_t cell[D];
+            cell[0] = static_cast<uint32_t>(x);
+            cell[1] = static_cast<uint32_t>(y);
+            if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
+            const uint32_t id = grid_cell_id<D>(cell);
+            // Entries of an enabled cloud lie in [0, n]; clamped all the same.
+            const int rs = min(max(t[id], 0), n);
+            const int re = min(max(t[id + 1], rs), n);
+            ok = ok && re - rs <= 255 && (re == rs || nruns < kGridRuns2);
+            if (ok && re > rs) {
+                s_runs[nruns * kKnnBlock + lane] = static_cast<uint32_t>(rs) << 8 | static_cast<uint32_t>(re - rs);
+                ++nruns;
+            }
+        }
+    }
+    uint64_t best[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) best[i] = candidate_key(seed, 0xffffffffu);
+    grid_stream<D, K>(s_runs + lane, ok ? nruns : 0, static_cast<const float4*>(a.accel) + in.pstart, q, best);
+    const float safe = grid_safe_margin<D>(q, root, c, shift, G, 2);
+    const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
+    const bool done = ok && static_cast<uint32_t>(best[K - 1]) != 0xffffffffu && safe > 0.0f && worst < safe * safe;
+    if (done) {
+        const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
+        write_results<K, D>(a, out.out_row, best, 0, out.pstart);
+    }
+    const uint64_t left = __ballot(valid && !done);
+    if (lane == 0) masks[tile] = left;
+    // A seeded slot left in the list keeps the bound at the seed.
+    if (ok && !done) bounds[gid] = worst;
+}
+
 // The fallback list, every failing launch position in launch order, in two
 // launches: grid_offsets_kernel scans the tiles' mask counts within blocks
 // of kCompactTiles tiles (block totals to `sums`); grid_list_kernel (one
 // wave per tile) adds the earlier blocks' totals and writes the tile's
 // positions, and the last tile the list's length.
 constexpr int kCompactTiles = 1024;
+// With `limit`, only tiles holding positions below *limit are read (the
+// second pass writes no others) and the rest count as empty.
+__device__ __forceinline__ uint64_t grid_mask(const uint64_t* masks, int64_t tiles, const uint32_t* limit, int64_t t) {
+    return t < tiles && (limit == nullptr || t * kKnnBlock < static_cast<int64_t>(*limit)) ? masks[t] : 0ull;
+}
+
 __global__ __launch_bounds__(kCompactTiles) void grid_offsets_kernel(const uint64_t* __restrict__ masks, int64_t tiles,
+                                                                    const uint32_t* limit,
                                                                     uint32_t* __restrict__ offsets,
                                                                     uint32_t* __restrict__ sums) {
     __shared__ uint32_t s_scan[kCompactTiles / kWave];
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kCompactTiles + threadIdx.x;
-    const uint32_t c = t < tiles ? static_cast<uint32_t>(__popcll(masks[t])) : 0u;
+    const uint32_t c = static_cast<uint32_t>(__popcll(grid_mask(masks, tiles, limit, t)));
     uint32_t total = 0;
     const uint32_t before = block_exclusive_sum<kCompactTiles>(c, s_scan, &total);
     if (t < tiles) offsets[t] = before;
@@ -1278,10 +1489,12 @@ __global__ __launch_bounds__(kCompactTiles) void grid_offsets_kernel(const uint6
 }
 
 constexpr int kListWaves = 4;
+// Entries are launch positions, or with `map`, map[position].
 __global__ __launch_bounds__(kListWaves * kWave) void grid_list_kernel(const uint64_t* __restrict__ masks,
-                                                                      int64_t tiles,
+                                                                      int64_t tiles, const uint32_t* limit,
                                                                       const uint32_t* __restrict__ offsets,
                                                                       const uint32_t* __restrict__ sums,
+                                                                      const int32_t* map,
                                                                       int32_t* __restrict__ list, uint32_t* count) {
     // One wave per tile: the totals of the earlier blocks, then the tile's
     // positions, a contiguous run of the list.
@@ -1293,11 +1506,12 @@ __global__ __launch_bounds__(kListWaves * kWave) void grid_list_kernel(const uin
     for (int i = lane; i < block; i += kWave) before += sums[i];
     before = wave_inclusive_sum(before);
     const uint32_t base = __builtin_amdgcn_readlane(before, kWave - 1) + offsets[t];
-    const uint64_t m = masks[t];
+    const uint64_t m = grid_mask(masks, tiles, limit, t);
     if ((m >> lane) & 1ull) {
         const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-        list[base + rank] = static_cast<int32_t>(t * kKnnBlock + lane);
+        const int64_t at = t * kKnnBlock + lane;
+        list[base + rank] = map != nullptr ? map[at] : static_cast<int32_t>(at);
     }
     if (t == tiles - 1 && lane == 0) *count = base + static_cast<uint32_t>(__popcll(m));
 }
@@ -1389,7 +1603,7 @@ int grid_level(int64_t n, int D, int K) {
 
 namespace {
 struct GridLayout {
-    size_t table, flags, count, masks, offsets, sums, list, bounds, total;
+    size_t table, flags, count, count2, masks, offsets, sums, list, list2, bounds, total;
 };
 GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
     auto up = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -1399,26 +1613,42 @@ GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
     g.table = 0;
     g.flags = up(g.table + static_cast<size_t>(B) * (cells + 1) * 4);
     g.count = up(g.flags + static_cast<size_t>(B) * 4);
-    g.masks = up(g.count + 4);
+    g.count2 = up(g.count + 4);
+    g.masks = up(g.count2 + 4);
     g.offsets = up(g.masks + tiles * 8);
     g.sums = up(g.offsets + tiles * 4);
     g.list = up(g.sums + (tiles + kCompactTiles - 1) / kCompactTiles * 4);
-    g.bounds = up(g.list + static_cast<size_t>(total_q) * 4);
+    g.list2 = up(g.list + static_cast<size_t>(total_q) * 4);
+    g.bounds = up(g.list2 + static_cast<size_t>(total_q) * 4);
     g.total = up(g.bounds + static_cast<size_t>(total_q) * 4);
     return g;
 }
 
+// Whether the second pass runs (see grid_knn2_kernel).
+constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K == 16); }
+
+// Pass 1 (pass == 1) or pass 2 over `list` (*count entries).
 template <int D, int K>
-void launch_grid_dk(const KnnArgs& a, const float* node_aabbs, int64_t nr, int level, int32_t* table,
-                    uint32_t* flags, uint64_t* masks, float* bounds, hipStream_t stream) {
+void launch_grid_dk(const KnnArgs& a, int pass, const float* node_aabbs, int64_t nr, int level, int32_t* table,
+                    uint32_t* flags, const int32_t* list, const uint32_t* count, uint64_t* masks, float* bounds,
+                    hipStream_t stream) {
     const int64_t tiles = (a.total_q + kKnnBlock - 1) / kKnnBlock;
     const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
-    if (a.order != nullptr) {
-        grid_knn_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, masks,
-                                                                     bounds);
+    const bool ordered = a.order != nullptr;
+    if (pass == 1) {
+        if (ordered) {
+            grid_knn_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, masks,
+                                                                         bounds);
+        } else {
+            grid_knn_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags,
+                                                                          masks, bounds);
+        }
+    } else if (ordered) {
+        grid_knn2_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, count,
+                                                                      masks, bounds);
     } else {
-        grid_knn_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, masks,
-                                                                      bounds);
+        grid_knn2_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, count,
+                                                                       masks, bounds);
     }
 }
 }  // namespace
@@ -1452,38 +1682,51 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
     const float4* p4 = static_cast<const float4*>(args.accel);
     if (D == 3) grid_table_kernel<3><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
     else grid_table_kernel<2><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
-    auto run = [&](auto dk) { dk(args, node_aabbs, nr, level, table, flags, masks, bounds, stream); };
-    // k in {4, 8, 16, 32} (supported_k).
-    if (D == 3) {
-        switch (K) {
-            case 4: run(launch_grid_dk<3, 4>); break;
-            case 8: run(launch_grid_dk<3, 8>); break;
-            case 16: run(launch_grid_dk<3, 16>); break;
-            case 32: run(launch_grid_dk<3, 32>); break;
-            default: return hipErrorInvalidValue;
-        }
-    } else {
-        switch (K) {
-            case 4: run(launch_grid_dk<2, 4>); break;
-            case 8: run(launch_grid_dk<2, 8>); break;
-            case 16: run(launch_grid_dk<2, 16>); break;
-            case 32: run(launch_grid_dk<2, 32>); break;
-            default: return hipErrorInvalidValue;
-        }
-    }
+    uint32_t* count2 = reinterpret_cast<uint32_t*>(base + g.count2);
+    int32_t* list2 = reinterpret_cast<int32_t*>(base + g.list2);
     const int64_t tiles = (args.total_q + kKnnBlock - 1) / kKnnBlock;
     const unsigned cgrid = static_cast<unsigned>((tiles + kCompactTiles - 1) / kCompactTiles);
-    grid_offsets_kernel<<<cgrid, kCompactTiles, 0, stream>>>(masks, tiles, offsets, sums);
-    grid_list_kernel<<<static_cast<unsigned>((tiles + kListWaves - 1) / kListWaves), kListWaves * kWave, 0, stream>>>(
-        masks, tiles, offsets, sums, list, count);
+    const unsigned lgrid = static_cast<unsigned>((tiles + kListWaves - 1) / kListWaves);
+    const int passes = grid_second_pass(D, K) ? 2 : 1;
+    for (int pass = 1; pass <= passes; ++pass) {
+        auto run = [&](auto dk) {
+            dk(args, pass, node_aabbs, nr, level, table, flags, list, count, masks, bounds, stream);
+        };
+        // k in {4, 8, 16, 32} (supported_k).
+        if (D == 3) {
+            switch (K) {
+                case 4: run(launch_grid_dk<3, 4>); break;
+                case 8: run(launch_grid_dk<3, 8>); break;
+                case 16: run(launch_grid_dk<3, 16>); break;
+                case 32: run(launch_grid_dk<3, 32>); break;
+                default: return hipErrorInvalidValue;
+            }
+        } else {
+            switch (K) {
+                case 4: run(launch_grid_dk<2, 4>); break;
+                case 8: run(launch_grid_dk<2, 8>); break;
+                case 16: run(launch_grid_dk<2, 16>); break;
+                case 32: run(launch_grid_dk<2, 32>); break;
+                default: return hipErrorInvalidValue;
+            }
+        }
+        // Pass 1 lists launch positions; pass 2, positions of that list
+        // (tiles past its length unwritten), mapped back through it.
+        const uint32_t* limit = pass == 1 ? nullptr : count;
+        grid_offsets_kernel<<<cgrid, kCompactTiles, 0, stream>>>(masks, tiles, limit, offsets, sums);
+        grid_list_kernel<<<lgrid, kListWaves * kWave, 0, stream>>>(masks, tiles, limit, offsets, sums,
+                                                                   pass == 1 ? nullptr : list,
+                                                                   pass == 1 ? list : list2,
+                                                                   pass == 1 ? count : count2);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // The fallback: the accel traversal over the list (its grid sized for
     // every query; work-groups past the list's tiles exit at once).
     KnnArgs f = args;
-    f.fb_list = list;
+    f.fb_list = passes == 2 ? list2 : list;
     f.fb_bound = bounds;
-    f.fb_count = count;
+    f.fb_count = passes == 2 ? count2 : count;
     return launch_knn_accel(f, D, K, false, stream);
 }
 
