@@ -18,6 +18,7 @@ The synthetic workloads of every BASELINE config are defined here
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -137,14 +138,15 @@ PROFILES = Path(__file__).resolve().parent / "profiles"
 
 
 def measured_traffic(config: str):
-    """HBM bytes per traversal launch measured by rocprofv3 (FETCH_SIZE and
-    WRITE_SIZE, each scaled by the same counter's reading for a copy of
-    known size), as recorded in profiles/knn_accel_<config>_counters.md on
-    the line ``traffic_bytes_per_launch: <bytes>``; None when absent."""
-    path = PROFILES / f"knn_accel_{config}_counters.md"
+    """HBM bytes per k-NN call measured by rocprofv3 (FETCH_SIZE and
+    WRITE_SIZE of the call's kernels, each scaled by the same counter's
+    reading for a copy of known size), as recorded in
+    profiles/knn_call_<config>_counters.md on the line
+    ``traffic_bytes_per_call: <bytes>``; None when absent."""
+    path = PROFILES / f"knn_call_{config}_counters.md"
     try:
         for line in path.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith("traffic_bytes_per_call:"):
                 return int(line.split(":", 1)[1].strip())
     except (OSError, ValueError):
         pass
@@ -672,6 +674,18 @@ def main() -> int:
 
     value = total_q / (ms_per_step * 1e-3)
     trav_gbs = n_bytes / (trav_ms * 1e-3) / 1e9 if trav_ms > 0 else None
+    # Which kernels the timed k-NN call runs: batched calls above
+    # GRID_MIN_QUERIES take the cell-block search where the clouds allow a
+    # grid (a nonzero workspace), the rest the accel traversal alone.
+    from torchbvh_amd import _native as native
+    ws = ctypes.c_size_t(0)
+    clouds, per_cloud = (1, pts.shape[0]) if kind == "single" else (pts.shape[0], pts.shape[1])
+    grid = (kind != "ragged" and total_q > native.GRID_MIN_QUERIES
+            and native.load().tbvh_knn_accel_grid_workspace_size(
+                clouds, total_q // clouds, per_cloud, D, k, ctypes.byref(ws)) == 0
+            and ws.value > 0)
+    call_what = ("k-NN call: cell-block passes (grid_knn_kernel; grid_knn2_kernel for 3-D k = 8, 16) and the "
+                 "traversal of what they leave (knn_accel_kernel)" if grid else "knn_accel_kernel (traversal)")
     traffic = measured_traffic(args.config)
     line = {
         "metric": "k-NN queries/sec + BVH build ms, 1M pts/1M queries k=16 3D fp32, 1 GPU",
@@ -713,7 +727,7 @@ def main() -> int:
         "query_sort_full_bytes_formula": "Q(4D+72)",
         "roofline": {
             "bound": "hbm",
-            "kernel": "knn_accel_kernel (traversal)",
+            "kernel": call_what,
             "achieved": trav_gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
