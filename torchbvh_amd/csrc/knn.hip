@@ -1171,6 +1171,9 @@ __device__ __forceinline__ float grid_safe_margin(const float* q, const float* r
     return margin - 1e-5f * size;
 }
 
+// Whether the second pass runs (see grid_knn2_kernel).
+constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K == 16); }
+
 // One query per lane, in launch order like the traversal (same tile map).
 // Failing queries are recorded per tile (a mask of its lanes, bounds[gid]
 // their block's k-th distance, FLT_MAX where none was taken), so that
@@ -1320,7 +1323,9 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     const float safe = grid_safe_margin<D>(q, root, c, shift, G, 1);
     const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
     const bool done = ok && safe > 0.0f && worst < safe * safe;
-    if (done) {
+    // Failures with a full list leave it in their result row for the
+    // second pass, which goes on from it.
+    if (done || (grid_second_pass(D, K) && ok && worst < kFar)) {
         // Derived again rather than held through the scan.
         const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
         write_results<K, D>(a, out.out_row, best, 0, out.pstart);
@@ -1332,22 +1337,26 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
 
 // Second pass over the first pass's failures (list[0 .. *count), launch
 // positions; bounds[gid] the k-th distance of the first block's list,
-// FLT_MAX where it had none): the block of 5^D cells around the query, less
-// the cells that lie wholly beyond that distance (lower bound of their
-// points' distances, short by the slack, greater than it: no such point can
-// enter the final list, whose k-th distance is at most the bound).  Its
-// margin is at least two cells, so nearly every query the first block
-// missed by a little is decided here; the list starts seeded with (bound,
-// 0xffffffff) entries (displaced by the k points within the bound, which
-// all lie in the kept cells).  Failures go to the traversal with this
-// list's k-th distance, per tile of list positions as in the first pass.
+// FLT_MAX where it had none): the block of 5^D cells around the query.  The
+// first block's 3^D cells are done: their k nearest points are the list
+// the first pass left in the query's result row, which this pass reads
+// back.  Of the shell around them it keeps the cells not wholly beyond
+// that list's k-th distance (lower bound of their points' distances, short
+// by the slack, greater than it: no such point can enter the final list,
+// whose k-th distance is at most the bound), streams their points into the
+// list, and keeps the result when its k-th distance is inside the block's
+// margin, at least two cells.  Failures go to the traversal with the new
+// k-th distance, per tile of list positions as in the first pass.
 // Run for 3-D k = 8 and 16 only (grid_second_pass).  At cfg2 the first pass
 // leaves 13% of the queries, which the traversal answered in 117 us; with
 // this pass the whole call measured 0.425 -> 0.386 ms (3-D k = 8: 0.344 ->
 // 0.310), but +50% at 3-D k = 4 (0.5 points per cell: 125 cells to cull
 // and more first-pass failures), +5% in 2-D (first-pass failures rare: its
-// three launches cost more than they save), +4% at k = 32.
-constexpr int kGridRuns2 = 64;  // kept cells per lane (more: the traversal)
+// three launches cost more than they save), +4% at k = 32.  Reading the
+// first list back instead of scanning the inner block again: this pass
+// 81 -> 63 us at cfg2 (the call 0.379 -> 0.378 ms; 3-D k = 8 0.306 ->
+// 0.294 ms); it waits on memory more than it computes.
+constexpr int kGridRuns2 = 32;  // kept shell cells per lane (more: the traversal)
 template <int D, int K, bool kOrdered>
 __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const float* __restrict__ node_aabbs,
                                                           int64_t nr, int level, const int32_t* __restrict__ table,
@@ -1425,6 +1434,8 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
     for (int j = 0; j < kCells; ++j) {
         const int o = kOrder.off[j];
         const int ox = Order::dx(o), oy = Order::dy(o), oz = Order::dz(o);
+        // The first block's cells are in the list already.
+        if (ox >= -1 && ox <= 1 && oy >= -1 && oy <= 1 && oz >= -1 && oz <= 1) continue;
         const int x = static_cast<int>(c[0]) + ox, y = static_cast<int>(c[1]) + oy;
         const int z = D == 3 ? static_cast<int>(c[D - 1]) + oz : 0;
         float bound = lb[0][ox + 2] + lb[1][oy + 2];
@@ -1446,20 +1457,26 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
             }
         }
     }
+    // The first block's list, ascending (its k-th distance is the bound).
     uint64_t best[K];
+    {
+        const int64_t* oi = a.out_indices + (ok ? in.out_row : 0) * K;
+        const float* od = a.out_distances + (ok ? in.out_row : 0) * K;
 #pragma unroll
-    for (int i = 0; i < K; ++i) best[i] = candidate_key(seed, 0xffffffffu);
+        for (int i = 0; i < K; ++i) {
+            best[i] = ok ? candidate_key(od[i], static_cast<uint32_t>(oi[i])) : kEmptyKey;
+        }
+    }
     grid_stream<D, K>(s_runs + lane, ok ? nruns : 0, static_cast<const float4*>(a.accel) + in.pstart, q, best);
     const float safe = grid_safe_margin<D>(q, root, c, shift, G, 2);
     const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
-    const bool done = ok && static_cast<uint32_t>(best[K - 1]) != 0xffffffffu && safe > 0.0f && worst < safe * safe;
+    const bool done = ok && safe > 0.0f && worst < safe * safe;
     if (done) {
         const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
         write_results<K, D>(a, out.out_row, best, 0, out.pstart);
     }
     const uint64_t left = __ballot(valid && !done);
     if (lane == 0) masks[tile] = left;
-    // A seeded slot left in the list keeps the bound at the seed.
     if (ok && !done) bounds[gid] = worst;
 }
 
@@ -1623,9 +1640,6 @@ GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
     g.total = up(g.bounds + static_cast<size_t>(total_q) * 4);
     return g;
 }
-
-// Whether the second pass runs (see grid_knn2_kernel).
-constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K == 16); }
 
 // Pass 1 (pass == 1) or pass 2 over `list` (*count entries).
 template <int D, int K>
