@@ -1246,23 +1246,42 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     constexpr Order kOrder{};
     const int cap = 4 * kCells * static_cast<int>((n + cells - 1) / cells);
     int total = 0;
+    // Nine cells at a time, every lane loading both table entries of each
+    // (a cell outside the grid, or any cell of a lane that is not searching,
+    // reads entry 0 and is masked after): the 18 loads then issue together.
+    // With each cell's loads under its own branch, every load waited for
+    // the one before (54 round trips per wave at 3-D).
+    constexpr int kGroup = 9;
+    static_assert(kCells % kGroup == 0, "whole groups of cells");
+    const bool searching = ok;
 #pragma unroll
-    for (int j = 0; j < kCells; ++j) {
-        const int o = kOrder.off[j];
-        const int x = static_cast<int>(c[0]) + Order::dx(o), y = static_cast<int>(c[1]) + Order::dy(o);
-        const int z = D == 3 ? static_cast<int>(c[D - 1]) + Order::dz(o) : 0;
-        const bool inside = ok && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
-        uint32_t cell[D];
-        cell[0] = static_cast<uint32_t>(x);
-        cell[1] = static_cast<uint32_t>(y);
-        if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
-        const uint32_t id = inside ? grid_cell_id<D>(cell) : 0u;
-        // Entries of an enabled cloud lie in [0, n]; clamped all the same.
-        const int rs = inside ? min(max(t[id], 0), n) : 0;
-        const int re = inside ? min(max(t[id + 1], rs), n) : 0;
-        total += re - rs;
-        ok = ok && re - rs <= 255;
-        s_runs[j * kKnnBlock + lane] = static_cast<uint32_t>(rs) << 8 | static_cast<uint32_t>(min(re - rs, 255));
+    for (int g0 = 0; g0 < kCells; g0 += kGroup) {
+        int32_t raw_s[kGroup], raw_e[kGroup];
+        bool in[kGroup];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            const int o = kOrder.off[g0 + u];
+            const int x = static_cast<int>(c[0]) + Order::dx(o), y = static_cast<int>(c[1]) + Order::dy(o);
+            const int z = D == 3 ? static_cast<int>(c[D - 1]) + Order::dz(o) : 0;
+            in[u] = searching && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
+            uint32_t cell[D];
+            cell[0] = static_cast<uint32_t>(x);
+            cell[1] = static_cast<uint32_t>(y);
+            if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
+            const uint32_t id = in[u] ? grid_cell_id<D>(cell) : 0u;
+            raw_s[u] = t[id];
+            raw_e[u] = t[id + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+            // Entries of an enabled cloud lie in [0, n]; clamped all the same.
+            const int rs = in[u] ? min(max(raw_s[u], 0), n) : 0;
+            const int re = in[u] ? min(max(raw_e[u], rs), n) : 0;
+            total += re - rs;
+            ok = ok && re - rs <= 255;
+            s_runs[(g0 + u) * kKnnBlock + lane] =
+                static_cast<uint32_t>(rs) << 8 | static_cast<uint32_t>(min(re - rs, 255));
+        }
     }
     ok = ok && total <= cap;
     uint64_t best[K];
@@ -1429,6 +1448,9 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
     const int64_t cells = int64_t(1) << (D * level);
     const int32_t* t = table + b * (cells + 1);
     constexpr Order kOrder{};
+    // The kept cells' ids first (no loads), then their table entries in
+    // batches of 8 whose loads issue together (loading under each cell's
+    // own branch, every load waited for the one before).
     int nruns = 0;
 #pragma unroll
     for (int j = 0; j < kCells; ++j) {
@@ -1446,14 +1468,31 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
             cell[0] = static_cast<uint32_t>(x);
             cell[1] = static_cast<uint32_t>(y);
             if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
-            const uint32_t id = grid_cell_id<D>(cell);
-            // Entries of an enabled cloud lie in [0, n]; clamped all the same.
-            const int rs = min(max(t[id], 0), n);
-            const int re = min(max(t[id + 1], rs), n);
-            ok = ok && re - rs <= 255 && (re == rs || nruns < kGridRuns2);
-            if (ok && re > rs) {
-                s_runs[nruns * kKnnBlock + lane] = static_cast<uint32_t>(rs) << 8 | static_cast<uint32_t>(re - rs);
-                ++nruns;
+            ok = ok && nruns < kGridRuns2;
+            if (ok) s_runs[nruns * kKnnBlock + lane] = grid_cell_id<D>(cell);
+            ++nruns;
+        }
+    }
+    if (!ok) nruns = 0;
+    constexpr int kBatch = 8;
+#pragma unroll
+    for (int r0 = 0; r0 < kGridRuns2; r0 += kBatch) {
+        if (__ballot(r0 < nruns) == 0) break;
+        int32_t raw_s[kBatch], raw_e[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const uint32_t id = r0 + u < nruns ? s_runs[(r0 + u) * kKnnBlock + lane] : 0u;
+            raw_s[u] = t[id];
+            raw_e[u] = t[id + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (r0 + u < nruns) {
+                // Entries of an enabled cloud lie in [0, n]; clamped all the same.
+                const int rs = min(max(raw_s[u], 0), n);
+                const int re = min(max(raw_e[u], rs), n);
+                ok = ok && re - rs <= 255;
+                s_runs[(r0 + u) * kKnnBlock + lane] = static_cast<uint32_t>(rs) << 8 | static_cast<uint32_t>(re - rs);
             }
         }
     }
