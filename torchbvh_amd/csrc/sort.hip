@@ -54,10 +54,18 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(const Segment* __r
     if (lt < g.tiles) {
         const int64_t row0 = g.start + static_cast<int64_t>(lt) * kSortTile;
         const int count = min(kSortTile, g.n - lt * kSortTile);
+        // All of this thread's keys are loaded before any is counted (rows
+        // past the tile read its first row), so the loads issue together;
+        // a load under each item's own branch waited for the one before.
+        uint32_t k[kItems];
 #pragma unroll
         for (int i = 0; i < kItems; ++i) {
             const int pos = i * kThreads + threadIdx.x;
-            if (pos < count) atomicAdd(&s_cnt[(keys[row0 + pos] >> shift) & (kRadix - 1)], 1u);
+            k[i] = keys[row0 + (pos < count ? pos : 0)];
+        }
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            if (i * kThreads + threadIdx.x < count) atomicAdd(&s_cnt[(k[i] >> shift) & (kRadix - 1)], 1u);
         }
     }
     __syncthreads();
