@@ -166,7 +166,7 @@ def test_grid_knn_workspace_and_argument_errors():
                 + M * 4)
     expect = up(expect + M * 4)
     assert size.value == up(expect + M * 4)
-    # k = 32 aims at 8 points per cell: 2^17 cells, rounded to the nearest level (2^18).
+    # k = 32 keeps at least 4 points per cell: 2^18 cells.
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 32, ctypes.byref(size)) == 0
     assert size.value == up(expect + M * 4)
     # Clouds of 2^24 points or more keep the traversal (run starts are packed into 24 bits).

@@ -1640,18 +1640,25 @@ hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStre
     return D == 3 ? launch_d<3, true>(a, K, ragged, stream) : launch_d<2, true>(a, K, ragged, stream);
 }
 
-// Points per cell the level aims at: the k-th neighbour's distance then
-// stays about one cell (3-D: (3k / (4 pi rho))^(1/3) = 0.98 cells at rho =
-// k / 4; 2-D: (k / (pi rho))^(1/2) = 0.80 at rho = k / 2), inside the
-// block's one-cell margin for most queries (cfg2 87%, cfg4 97% in the CPU
-// model).  0 when the cloud is too small for a grid of at least 4 cells
-// per axis; at most 2^24 cells.
+// The finest level with at least rho points per cell on average, so that
+// the k-th neighbour's distance stays within about one cell (3-D:
+// (3k / (4 pi rho))^(1/3) = 0.98 cells at rho = k / 4; 2-D: (k / (pi
+// rho))^(1/2) = 0.80 at rho = k / 2), inside the block's one-cell margin
+// for most queries (cfg2 87%, cfg4 97% in the CPU model); a level holds
+// rho to 2^D rho points per cell.  Measured on uniform 3-D clouds (k-NN
+// call, schedule order), the nearest level instead: 2^19 points at k = 16
+// gave 2 points per cell and 0.411 ms where 16 per cell take 0.315 (plain
+// traversal 0.359); 2^18 at k = 8, 1 per cell and 0.248 ms against 8 per
+// cell 0.131 (plain 0.199); 2^20 at k = 4, 0.5 per cell and 0.391 ms
+// against 4 per cell 0.271.  k = 32 keeps 4 per cell (0.922 ms at 2^20,
+// 32 per cell 1.051, plain 0.954).  0 when the cloud is too small for a
+// grid of at least 4 cells per axis; at most 2^24 cells.
 int grid_level(int64_t n, int D, int K) {
     // Run starts (at most n) are packed into 24 bits.
     if (n >= (int64_t(1) << 24)) return 0;
-    const double rho = D == 3 ? std::max(1, K / 4) : std::max(2, K / 2);
+    const double rho = D == 3 ? (K >= 32 ? 4 : std::max(1, K / 4)) : std::max(2, K / 2);
     const double cells = static_cast<double>(n) / rho;
-    int l = static_cast<int>(std::lround(std::log2(std::max(cells, 1.0)) / D));
+    const int l = static_cast<int>(std::floor(std::log2(std::max(cells, 1.0)) / D));
     const int max_l = D == 3 ? 8 : 12;
     if (l < 2) return 0;
     return std::min(l, max_l);
