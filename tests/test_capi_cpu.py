@@ -174,20 +174,26 @@ def test_grid_knn_workspace_and_argument_errors():
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 4, 16, ctypes.byref(size)) == 1
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 5, ctypes.byref(size)) == 1
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 16, None) == 1
+    # k = 4 keeps the traversal below 2^17 points per cloud, and 2-D clouds below 2^15 points.
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 16, 3, 4, ctypes.byref(size)) == 0 and size.value == 0
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 2, 4, ctypes.byref(size)) == 0 and size.value == 0
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 10_000, 2, 8, ctypes.byref(size)) == 0 and size.value == 0
+    # 10,000 points at k = 16 in 3-D: level 3 leaves 19.5 points per cell (4.9 x rho): no grid.
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, 10_000, 3, 16, ctypes.byref(size)) == 0 and size.value == 0
     N = 1 << 16
-    assert L.tbvh_knn_accel_grid_workspace_size(1, M, N, 3, 4, ctypes.byref(size)) == 0 and size.value > 0
+    assert L.tbvh_knn_accel_grid_workspace_size(1, M, N, 3, 8, ctypes.byref(size)) == 0 and size.value > 0
     need = size.value
     nr = _native.real_node_count(N)
-    args = lambda nr_, ws, ws_bytes: (FAKE, FAKE, nr_, FAKE, None, 1, M, N, 3, 4, FAKE, FAKE, ws, ws_bytes, None)
+    args = lambda nr_, ws, ws_bytes: (FAKE, FAKE, nr_, FAKE, None, 1, M, N, 3, 8, FAKE, FAKE, ws, ws_bytes, None)
     assert L.tbvh_knn_accel_grid(*args(nr + 1, FAKE, need)) == 1
     assert "num_real_nodes" in _err(L)
     assert L.tbvh_knn_accel_grid(*args(nr, FAKE, need - 1)) == 2
     assert "workspace" in _err(L)
     assert L.tbvh_knn_accel_grid(*args(nr, ctypes.c_void_p(0x100008), need)) == 1
     assert "aligned" in _err(L)
-    assert L.tbvh_knn_accel_grid(FAKE, None, nr, FAKE, None, 1, M, N, 3, 4, FAKE, FAKE, FAKE, need, None) == 1
+    assert L.tbvh_knn_accel_grid(FAKE, None, nr, FAKE, None, 1, M, N, 3, 8, FAKE, FAKE, FAKE, need, None) == 1
     assert "node_aabbs" in _err(L)
-    assert L.tbvh_knn_accel_grid(None, None, 0, None, None, 1, 0, N, 3, 4, None, None, None, 0, None) == 0
+    assert L.tbvh_knn_accel_grid(None, None, 0, None, None, 1, 0, N, 3, 8, None, None, None, 0, None) == 0
 
 
 def test_accel_from_tree_and_accel_alignment_errors():

@@ -17,6 +17,7 @@ fallback: without it every call raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 import weakref
 from pathlib import Path
@@ -226,6 +227,15 @@ MAX_ACCEL_CLOUD = 1 << 28
 # search (tbvh_knn_accel_grid); below it its three extra launches cost more
 # than it saves.
 GRID_MIN_QUERIES = 1 << 17
+
+
+@functools.lru_cache(maxsize=256)
+def _grid_workspace_size(B: int, M: int, n: int, D: int, k: int) -> int:
+    """Workspace bytes of the cell-block search for this call shape, 0
+    where it does not run (tbvh_knn_accel_grid_workspace_size)."""
+    need = ctypes.c_size_t(0)
+    _check(load().tbvh_knn_accel_grid_workspace_size(B, M, n, D, k, ctypes.byref(need)))
+    return int(need.value)
 
 
 # ---------------------------------------------------------------------------
@@ -778,17 +788,16 @@ class _NativeOps:
                     _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
                     int(dim), int(k), _ptr(source_points), C, _ptr(indices), _ptr(distances),
                     _ptr(positions), _stream(dev)))
-            elif accel is not None and not spatial and B * M > GRID_MIN_QUERIES:
+            elif (accel is not None and not spatial and B * M > GRID_MIN_QUERIES
+                  and (need := _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k))) > 0):
                 # The cell-block search first (same results; see
-                # tbvh_knn_accel_grid); its workspace is 0 for small clouds.
-                need = ctypes.c_size_t(0)
-                _check(L.tbvh_knn_accel_grid_workspace_size(B, M, int(num_leaves), int(dim), int(k),
-                                                            ctypes.byref(need)))
-                ws = torch.empty(max(int(need.value), 1), dtype=torch.uint8, device=dev)
+                # tbvh_knn_accel_grid), where the clouds allow a grid and
+                # it measured faster (a nonzero workspace).
+                ws = torch.empty(need, dtype=torch.uint8, device=dev)
                 _check(L.tbvh_knn_accel_grid(
                     _ptr(accel), _ptr(node_aabbs), int(num_real_nodes), _ptr(query_points), _ptr(query_order),
                     B, M, int(num_leaves), int(dim), int(k), _ptr(indices), _ptr(distances),
-                    _ptr(ws) if need.value else None, int(need.value), _stream(dev)))
+                    _ptr(ws), need, _stream(dev)))
             elif accel is not None:
                 fn = L.tbvh_knn_accel_spatial if spatial else L.tbvh_knn_accel
                 _check(fn(

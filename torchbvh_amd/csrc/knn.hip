@@ -1651,17 +1651,33 @@ hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStre
 // traversal 0.359); 2^18 at k = 8, 1 per cell and 0.248 ms against 8 per
 // cell 0.131 (plain 0.199); 2^20 at k = 4, 0.5 per cell and 0.391 ms
 // against 4 per cell 0.271.  k = 32 keeps 4 per cell (0.922 ms at 2^20,
-// 32 per cell 1.051, plain 0.954).  0 when the cloud is too small for a
-// grid of at least 4 cells per axis; at most 2^24 cells.
+// 32 per cell 1.051, plain 0.954), and so does k = 4 at 2 (1 per cell
+// lost at every size measured).  0 when the cloud is too small for a grid
+// of at least 4 cells per axis, or where the traversal alone measured
+// faster (below); at most 2^24 cells.
 int grid_level(int64_t n, int D, int K) {
     // Run starts (at most n) are packed into 24 bits.
     if (n >= (int64_t(1) << 24)) return 0;
-    const double rho = D == 3 ? (K >= 32 ? 4 : std::max(1, K / 4)) : std::max(2, K / 2);
+    // Where the traversal alone is cheap enough that the block passes'
+    // launches and scans do not pay (k-NN call against the traversal,
+    // uniform clouds, 2^15 to 2^17 points): k = 4 below 2^17 points per
+    // cloud (3-D, +12% to +30%) and in 2-D at every size measured (+9% to
+    // +30%; -7% at 2^20); 2-D clouds of 10,000 points (16 of them, k = 8:
+    // +24%).
+    if (K <= 4 && (D == 2 || n < (int64_t(1) << 17))) return 0;
+    if (D == 2 && n < (int64_t(1) << 15)) return 0;
+    const double rho = D == 3 ? (K >= 32 ? 4 : std::max(2, K / 4)) : std::max(2, K / 2);
     const double cells = static_cast<double>(n) / rho;
-    const int l = static_cast<int>(std::floor(std::log2(std::max(cells, 1.0)) / D));
+    int l = static_cast<int>(std::floor(std::log2(std::max(cells, 1.0)) / D));
     const int max_l = D == 3 ? 8 : 12;
     if (l < 2) return 0;
-    return std::min(l, max_l);
+    l = std::min(l, max_l);
+    // A level that leaves many more points per cell than rho scans too
+    // much (16 clouds of 10,000 points at k = 16, 4.9 rho: +17%; of 50,000
+    // at k = 8, 6.1 rho: +5%; 4 rho at 2^16 and 2^19 points, k = 16: -17%
+    // and -9%).
+    if (static_cast<double>(n) / std::ldexp(1.0, D * l) > 4.5 * rho) return 0;
+    return l;
 }
 
 namespace {
