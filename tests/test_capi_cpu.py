@@ -155,16 +155,17 @@ def test_grid_knn_workspace_and_argument_errors():
     size = ctypes.c_size_t()
     # Too small for a grid of 4 cells per axis: no workspace (then the call is tbvh_knn_accel).
     assert L.tbvh_knn_accel_grid_workspace_size(1, 10, 20, 3, 4, ctypes.byref(size)) == 0 and size.value == 0
-    # 2^20 points, k = 16 in 3-D: 4 points per cell, 2^18 cells; then flags, two counts, one
-    # 64-bit mask and one offset per 64 queries, a total per 1024 masks, two lists, the bounds.
+    # 2^20 points, k = 16 in 3-D: 4 points per cell, 2^18 cells; then flags, the two lists'
+    # 8 x 64 counts each (32 words apart), the two lists (8 x 64 sub-lists, each for the
+    # 64-query tiles of one eighth of the tiles with one residue mod 64), the bounds.
     M = 1000
     up = lambda x: (x + 255) // 256 * 256
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 16, ctypes.byref(size)) == 0
     table = (1 << 18) + 1
     tiles = (M + 63) // 64
-    expect = up(up(up(up(up(up(up(up(table * 4) + 4) + 4) + 4) + tiles * 8) + tiles * 4) + (tiles + 1023) // 1024 * 4)
-                + M * 4)
-    expect = up(expect + M * 4)
+    seg = ((tiles + 7) // 8 + 63) // 64 * 64
+    expect = up(up(up(up(table * 4) + 4) + 2 * 512 * 32 * 4) + 512 * seg * 4)
+    expect = up(expect + 512 * seg * 4)
     assert size.value == up(expect + M * 4)
     # k = 32 keeps at least 4 points per cell: 2^18 cells.
     assert L.tbvh_knn_accel_grid_workspace_size(1, M, 1 << 20, 3, 32, ctypes.byref(size)) == 0

@@ -279,6 +279,26 @@ __device__ __forceinline__ void merge_candidates12(uint64_t (&best)[K], uint64_t
 constexpr int kKnnBlock = 64;
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 
+// The cell-block search's failure lists (launch positions left for the next
+// stage) are cut into kXcds * kGridSubLists sub-lists, each with its own
+// count, filled by one atomic add per wave.  Work-group b's sub-list is that
+// of its XCD share (b % kXcds, as in the tile map) and of the residue of its
+// local tile index (b / kXcds) mod kGridSubLists; the next stage's
+// work-group b reads chunk (b / kXcds) / kGridSubLists of the same
+// sub-list, so that it takes failures of tiles near its own.  One count per
+// XCD share measured 375 us for the first pass at cfg3, where every wave
+// fails at once: same-address atomics serialise (about 90 ns each).  The
+// counts lie kCountStride words apart, each on a 128-byte line of its own.
+constexpr int kGridSubLists = 64;
+constexpr int kCountStride = 32;
+constexpr int kGridCounts = kXcds * kGridSubLists;  // per list
+__device__ __forceinline__ int grid_sublist() {
+    return static_cast<int>(blockIdx.x % kXcds) * kGridSubLists + static_cast<int>(blockIdx.x / kXcds) % kGridSubLists;
+}
+__device__ __forceinline__ int64_t grid_chunk_start() {
+    return static_cast<int64_t>(blockIdx.x / kXcds / kGridSubLists) * kKnnBlock;
+}
+
 // Entries of a lane's deferred-node stack, all in LDS (6 bytes each: a
 // 32-bit child ref and a 16-bit distance, in columns of stride kKnnBlock):
 // as many as the LDS budget of each (D, k) holds.  7.5 KB per work-group for
@@ -867,27 +887,22 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     __shared__ uint32_t lds_refs[kLds * kKnnBlock];
     __shared__ uint16_t lds_dists[kCompact ? 1 : kLds * kKnnBlock];
     __shared__ uint8_t lds_hi[kCompact ? kLds * kKnnBlock : 1];
-    int64_t per_xcd = gridDim.x / kXcds;
+    const int64_t per_xcd = gridDim.x / kXcds;
     // The cell-block search's fallback pass: its list names the launch
-    // positions left to search, in launch order, and bounds the k-th
-    // distance of each (at least k points lie within it, so slots seeded
-    // (bound, 0xffffffff) are all displaced by points, the bound's own
-    // included: the result is exact).  The grid is sized for every query;
-    // the tile map spreads the list's tiles over the XCDs like a launch of
-    // its own length.
+    // positions left to search, and bounds the k-th distance of each (at
+    // least k points lie within it, so slots seeded (bound, 0xffffffff) are
+    // all displaced by points, the bound's own included: the result is
+    // exact).  Work-group b takes a chunk of sub-list grid_sublist(), fb_seg
+    // entries apart (the grid is sized for every query).
     const bool fallback = kAccel && !kRouted && a.fb_list != nullptr;
-    int64_t listed = 0;
-    if (fallback) {
-        listed = *a.fb_count;
-        per_xcd = ((listed + kKnnBlock - 1) / kKnnBlock + kXcds - 1) / kXcds;
-        if (blockIdx.x / kXcds >= per_xcd) return;
-    }
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     int64_t gid = tile * kKnnBlock + threadIdx.x;
     float seed = kFar;
     if (fallback) {
-        if (gid >= listed) return;
-        gid = a.fb_list[gid];
+        const int64_t listed = a.fb_count[grid_sublist() * kCountStride];
+        const int64_t at = grid_chunk_start() + threadIdx.x;
+        if (at >= listed) return;
+        gid = a.fb_list[grid_sublist() * a.fb_seg + at];
         seed = a.fb_bound[gid];
     }
     if (gid >= a.total_q) return;
@@ -931,7 +946,7 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     // held in registers through the traversal: the compiler cannot tell the
     // two apart, so nothing of the first derivation stays live.
     int64_t gid_out = tile * kKnnBlock + __lane_id();
-    if (fallback) gid_out = a.fb_list[gid_out];
+    if (fallback) gid_out = a.fb_list[grid_sublist() * a.fb_seg + grid_chunk_start() + __lane_id()];
     const QueryLoc out = locate<kOrdered, kRagged, kRouted, kAccel>(a, gid_out);
     write_results<K, D>(a, out.out_row, best, out.index_offset, out.pstart);
 }
@@ -1002,10 +1017,33 @@ __device__ __forceinline__ void grid_cell(const float* p, const float* lo, const
 // with probability below 1e-14).
 constexpr int kGridMaxGap = 64;
 
-__global__ void grid_init_kernel(uint32_t* flags, int64_t B, uint32_t* count) {
+// Clears the clouds' flags and the failure lists' counts (`ncounts` of
+// them, kCountStride words apart).
+__global__ void grid_init_kernel(uint32_t* flags, int64_t B, uint32_t* counts, int ncounts) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < B) flags[i] = 0u;
-    if (i == 0) *count = 0u;
+    if (i < ncounts) counts[i * kCountStride] = 0u;
+}
+
+// Appends the lanes set in `left` (wave-uniform) to this work-group's
+// sub-list of a failure list (`seg` entries each).  A sub-list holds the
+// launch positions of one residue class of one XCD share's tiles (or, for
+// the second list, of one sub-list of the first), at most `seg` of them,
+// so it cannot overflow.  One atomic per wave reserves the entries; their
+// order within a sub-list follows the waves' completion and changes no
+// result (each query's search depends only on the query and its bound).
+__device__ __forceinline__ void grid_append(int32_t* list, uint32_t* counts, int64_t seg, uint64_t left,
+                                            int64_t gid) {
+    if (left == 0) return;
+    const int sub = grid_sublist();
+    uint32_t base = 0;
+    if (lane_id() == 0) base = atomicAdd(&counts[sub * kCountStride], static_cast<uint32_t>(__popcll(left)));
+    base = __builtin_amdgcn_readlane(base, 0);
+    if ((left >> lane_id()) & 1ull) {
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(left >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(left), 0u));
+        list[sub * seg + base + rank] = static_cast<int32_t>(gid);
+    }
 }
 
 // One thread per point: writes the first-point entries of the cells from the
@@ -1191,7 +1229,8 @@ constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K ==
 template <int D, int K, bool kOrdered>
 __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const float* __restrict__ node_aabbs, int64_t nr,
                                                          int level, const int32_t* __restrict__ table,
-                                                         const uint32_t* __restrict__ flags, uint64_t* __restrict__ masks,
+                                                         const uint32_t* __restrict__ flags, int32_t* __restrict__ list,
+                                                         uint32_t* __restrict__ counts, int64_t seg,
                                                          float* __restrict__ bounds) {
     using Order = NearOrder<D, 1>;
     constexpr int kCells = Order::kCells;
@@ -1208,8 +1247,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     const int64_t b = valid ? gid / a.M : 0;
     bool ok = valid && flags[b] == 0u;
     if (__ballot(ok) == 0) {
-        const uint64_t left = __ballot(valid);
-        if (lane == 0) masks[tile] = left;
+        grid_append(list, counts, seg, __ballot(valid), gid);
         if (valid) bounds[gid] = kFar;
         return;
     }
@@ -1349,8 +1387,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
         const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
         write_results<K, D>(a, out.out_row, best, 0, out.pstart);
     }
-    const uint64_t left = __ballot(valid && !done);
-    if (lane == 0) masks[tile] = left;
+    grid_append(list, counts, seg, __ballot(valid && !done), gid);
     if (valid && !done) bounds[gid] = ok ? worst : kFar;
 }
 
@@ -1380,27 +1417,26 @@ template <int D, int K, bool kOrdered>
 __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const float* __restrict__ node_aabbs,
                                                           int64_t nr, int level, const int32_t* __restrict__ table,
                                                           const int32_t* __restrict__ list,
-                                                          const uint32_t* __restrict__ count,
-                                                          uint64_t* __restrict__ masks, float* __restrict__ bounds) {
+                                                          const uint32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ list2, uint32_t* __restrict__ counts2,
+                                                          int64_t seg, float* __restrict__ bounds) {
     using Order = NearOrder<D, 2>;
     constexpr int kCells = Order::kCells;
     __shared__ uint32_t s_runs[kGridRuns2 * kKnnBlock];
-    const int64_t listed = *count;
-    const int64_t per_xcd = ((listed + kKnnBlock - 1) / kKnnBlock + kXcds - 1) / kXcds;
-    if (blockIdx.x / kXcds >= per_xcd) return;
-    const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    if (tile * kKnnBlock >= listed) return;  // surplus tiles (whole waves)
+    // A chunk of this work-group's sub-list of the first list (the grid is
+    // sized for every query; work-groups past the sub-list's length exit).
+    const int64_t listed = counts[grid_sublist() * kCountStride];
+    const int64_t at0 = grid_chunk_start();
+    if (at0 >= listed) return;  // surplus work-groups (whole waves)
     const int lane = threadIdx.x;
-    const int64_t pos = tile * kKnnBlock + lane;
-    const bool valid = pos < listed;
-    const int64_t gid = valid ? list[pos] : 0;
+    const bool valid = at0 + lane < listed;
+    const int64_t gid = valid ? list[grid_sublist() * seg + at0 + lane] : 0;
     const float seed = valid ? bounds[gid] : kFar;
     // Lanes without a bound (disabled cloud, full block, non-finite query,
     // corrupt order entry) go on to the traversal.
     bool ok = valid && seed < kFar;
     if (__ballot(ok) == 0) {
-        const uint64_t left = __ballot(valid);
-        if (lane == 0) masks[tile] = left;
+        grid_append(list2, counts2, seg, __ballot(valid), gid);
         return;
     }
     QueryLoc in{};
@@ -1514,62 +1550,8 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
         const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
         write_results<K, D>(a, out.out_row, best, 0, out.pstart);
     }
-    const uint64_t left = __ballot(valid && !done);
-    if (lane == 0) masks[tile] = left;
+    grid_append(list2, counts2, seg, __ballot(valid && !done), gid);
     if (ok && !done) bounds[gid] = worst;
-}
-
-// The fallback list, every failing launch position in launch order, in two
-// launches: grid_offsets_kernel scans the tiles' mask counts within blocks
-// of kCompactTiles tiles (block totals to `sums`); grid_list_kernel (one
-// wave per tile) adds the earlier blocks' totals and writes the tile's
-// positions, and the last tile the list's length.
-constexpr int kCompactTiles = 1024;
-// With `limit`, only tiles holding positions below *limit are read (the
-// second pass writes no others) and the rest count as empty.
-__device__ __forceinline__ uint64_t grid_mask(const uint64_t* masks, int64_t tiles, const uint32_t* limit, int64_t t) {
-    return t < tiles && (limit == nullptr || t * kKnnBlock < static_cast<int64_t>(*limit)) ? masks[t] : 0ull;
-}
-
-__global__ __launch_bounds__(kCompactTiles) void grid_offsets_kernel(const uint64_t* __restrict__ masks, int64_t tiles,
-                                                                    const uint32_t* limit,
-                                                                    uint32_t* __restrict__ offsets,
-                                                                    uint32_t* __restrict__ sums) {
-    __shared__ uint32_t s_scan[kCompactTiles / kWave];
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kCompactTiles + threadIdx.x;
-    const uint32_t c = static_cast<uint32_t>(__popcll(grid_mask(masks, tiles, limit, t)));
-    uint32_t total = 0;
-    const uint32_t before = block_exclusive_sum<kCompactTiles>(c, s_scan, &total);
-    if (t < tiles) offsets[t] = before;
-    if (threadIdx.x == 0) sums[blockIdx.x] = total;
-}
-
-constexpr int kListWaves = 4;
-// Entries are launch positions, or with `map`, map[position].
-__global__ __launch_bounds__(kListWaves * kWave) void grid_list_kernel(const uint64_t* __restrict__ masks,
-                                                                      int64_t tiles, const uint32_t* limit,
-                                                                      const uint32_t* __restrict__ offsets,
-                                                                      const uint32_t* __restrict__ sums,
-                                                                      const int32_t* map,
-                                                                      int32_t* __restrict__ list, uint32_t* count) {
-    // One wave per tile: the totals of the earlier blocks, then the tile's
-    // positions, a contiguous run of the list.
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kListWaves + threadIdx.x / kWave;
-    if (t >= tiles) return;
-    const int lane = lane_id();
-    const int block = static_cast<int>(t / kCompactTiles);
-    uint32_t before = 0;
-    for (int i = lane; i < block; i += kWave) before += sums[i];
-    before = wave_inclusive_sum(before);
-    const uint32_t base = __builtin_amdgcn_readlane(before, kWave - 1) + offsets[t];
-    const uint64_t m = grid_mask(masks, tiles, limit, t);
-    if ((m >> lane) & 1ull) {
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-        const int64_t at = t * kKnnBlock + lane;
-        list[base + rank] = map != nullptr ? map[at] : static_cast<int32_t>(at);
-    }
-    if (t == tiles - 1 && lane == 0) *count = base + static_cast<uint32_t>(__popcll(m));
 }
 
 template <int D, int K, bool kOrdered, bool kRagged, bool kRouted, bool kAccel, bool kCompact = false>
@@ -1681,50 +1663,56 @@ int grid_level(int64_t n, int D, int K) {
 }
 
 namespace {
+// Workspace: the cells' first-point tables, the clouds' flags, the two
+// failure lists' counts (kGridCounts each, kCountStride words apart), the
+// two lists (kGridCounts sub-lists of `seg` entries: the launch positions
+// of one XCD share's tiles of one residue mod kGridSubLists), the k-th
+// distance bounds.
 struct GridLayout {
-    size_t table, flags, count, count2, masks, offsets, sums, list, list2, bounds, total;
+    size_t table, flags, counts, list, list2, bounds, total;
+    int64_t seg;
 };
 GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
     auto up = [](size_t x) { return (x + 255) / 256 * 256; };
     const size_t cells = size_t(1) << (D * level);
-    const size_t tiles = static_cast<size_t>((total_q + kKnnBlock - 1) / kKnnBlock);
+    const int64_t tiles = (total_q + kKnnBlock - 1) / kKnnBlock;
+    const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
     GridLayout g;
+    g.seg = (per_xcd + kGridSubLists - 1) / kGridSubLists * kKnnBlock;
+    const size_t list_bytes = static_cast<size_t>(kGridCounts * g.seg) * 4;
     g.table = 0;
     g.flags = up(g.table + static_cast<size_t>(B) * (cells + 1) * 4);
-    g.count = up(g.flags + static_cast<size_t>(B) * 4);
-    g.count2 = up(g.count + 4);
-    g.masks = up(g.count2 + 4);
-    g.offsets = up(g.masks + tiles * 8);
-    g.sums = up(g.offsets + tiles * 4);
-    g.list = up(g.sums + (tiles + kCompactTiles - 1) / kCompactTiles * 4);
-    g.list2 = up(g.list + static_cast<size_t>(total_q) * 4);
-    g.bounds = up(g.list2 + static_cast<size_t>(total_q) * 4);
+    g.counts = up(g.flags + static_cast<size_t>(B) * 4);
+    g.list = up(g.counts + static_cast<size_t>(2 * kGridCounts * kCountStride) * 4);
+    g.list2 = up(g.list + list_bytes);
+    g.bounds = up(g.list2 + list_bytes);
     g.total = up(g.bounds + static_cast<size_t>(total_q) * 4);
     return g;
 }
 
-// Pass 1 (pass == 1) or pass 2 over `list` (*count entries).
+// Pass 1 (pass == 1: failures to `list`) or pass 2 (over `list`, failures
+// to `list2`).
 template <int D, int K>
 void launch_grid_dk(const KnnArgs& a, int pass, const float* node_aabbs, int64_t nr, int level, int32_t* table,
-                    uint32_t* flags, const int32_t* list, const uint32_t* count, uint64_t* masks, float* bounds,
-                    hipStream_t stream) {
+                    uint32_t* flags, int32_t* list, uint32_t* counts, int32_t* list2, uint32_t* counts2, int64_t seg,
+                    float* bounds, hipStream_t stream) {
     const int64_t tiles = (a.total_q + kKnnBlock - 1) / kKnnBlock;
     const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
     const bool ordered = a.order != nullptr;
     if (pass == 1) {
         if (ordered) {
-            grid_knn_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, masks,
-                                                                         bounds);
+            grid_knn_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, list,
+                                                                         counts, seg, bounds);
         } else {
-            grid_knn_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags,
-                                                                          masks, bounds);
+            grid_knn_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, list,
+                                                                          counts, seg, bounds);
         }
     } else if (ordered) {
-        grid_knn2_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, count,
-                                                                      masks, bounds);
+        grid_knn2_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, counts,
+                                                                      list2, counts2, seg, bounds);
     } else {
-        grid_knn2_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, count,
-                                                                       masks, bounds);
+        grid_knn2_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, counts,
+                                                                       list2, counts2, seg, bounds);
     }
 }
 }  // namespace
@@ -1744,29 +1732,24 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
     char* base = static_cast<char*>(ws);
     int32_t* table = reinterpret_cast<int32_t*>(base + g.table);
     uint32_t* flags = reinterpret_cast<uint32_t*>(base + g.flags);
-    uint32_t* count = reinterpret_cast<uint32_t*>(base + g.count);
-    uint64_t* masks = reinterpret_cast<uint64_t*>(base + g.masks);
-    uint32_t* offsets = reinterpret_cast<uint32_t*>(base + g.offsets);
-    uint32_t* sums = reinterpret_cast<uint32_t*>(base + g.sums);
+    uint32_t* counts = reinterpret_cast<uint32_t*>(base + g.counts);
+    uint32_t* counts2 = counts + kGridCounts * kCountStride;
     int32_t* list = reinterpret_cast<int32_t*>(base + g.list);
+    int32_t* list2 = reinterpret_cast<int32_t*>(base + g.list2);
     float* bounds = reinterpret_cast<float*>(base + g.bounds);
     const int n = args.num_leaves;
-    grid_init_kernel<<<static_cast<unsigned>((args.B + kBlock - 1) / kBlock), kBlock, 0, stream>>>(flags, args.B,
-                                                                                                  count);
+    const int64_t init = std::max<int64_t>(args.B, 2 * kGridCounts);
+    grid_init_kernel<<<static_cast<unsigned>((init + kBlock - 1) / kBlock), kBlock, 0, stream>>>(flags, args.B, counts,
+                                                                                                2 * kGridCounts);
     const int64_t pts = args.B * static_cast<int64_t>(n);
     const unsigned tgrid = static_cast<unsigned>((pts + kBlock - 1) / kBlock);
     const float4* p4 = static_cast<const float4*>(args.accel);
     if (D == 3) grid_table_kernel<3><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
     else grid_table_kernel<2><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
-    uint32_t* count2 = reinterpret_cast<uint32_t*>(base + g.count2);
-    int32_t* list2 = reinterpret_cast<int32_t*>(base + g.list2);
-    const int64_t tiles = (args.total_q + kKnnBlock - 1) / kKnnBlock;
-    const unsigned cgrid = static_cast<unsigned>((tiles + kCompactTiles - 1) / kCompactTiles);
-    const unsigned lgrid = static_cast<unsigned>((tiles + kListWaves - 1) / kListWaves);
     const int passes = grid_second_pass(D, K) ? 2 : 1;
     for (int pass = 1; pass <= passes; ++pass) {
         auto run = [&](auto dk) {
-            dk(args, pass, node_aabbs, nr, level, table, flags, list, count, masks, bounds, stream);
+            dk(args, pass, node_aabbs, nr, level, table, flags, list, counts, list2, counts2, g.seg, bounds, stream);
         };
         // k in {4, 8, 16, 32} (supported_k).
         if (D == 3) {
@@ -1786,23 +1769,17 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
                 default: return hipErrorInvalidValue;
             }
         }
-        // Pass 1 lists launch positions; pass 2, positions of that list
-        // (tiles past its length unwritten), mapped back through it.
-        const uint32_t* limit = pass == 1 ? nullptr : count;
-        grid_offsets_kernel<<<cgrid, kCompactTiles, 0, stream>>>(masks, tiles, limit, offsets, sums);
-        grid_list_kernel<<<lgrid, kListWaves * kWave, 0, stream>>>(masks, tiles, limit, offsets, sums,
-                                                                   pass == 1 ? nullptr : list,
-                                                                   pass == 1 ? list : list2,
-                                                                   pass == 1 ? count : count2);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // The fallback: the accel traversal over the list (its grid sized for
-    // every query; work-groups past the list's tiles exit at once).
+    // The fallback: the accel traversal over the last list (its grid sized
+    // for every query; work-groups past their segment's length exit at
+    // once).
     KnnArgs f = args;
     f.fb_list = passes == 2 ? list2 : list;
     f.fb_bound = bounds;
-    f.fb_count = passes == 2 ? count2 : count;
+    f.fb_count = passes == 2 ? counts2 : counts;
+    f.fb_seg = g.seg;
     return launch_knn_accel(f, D, K, false, stream);
 }
 

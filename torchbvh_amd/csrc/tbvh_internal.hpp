@@ -429,12 +429,15 @@ struct KnnArgs {
     const void* accel2;            // accel of the false route
     int32_t num_leaves2;
     int32_t num_real_nodes2;
-    // Fallback pass of the cell-block search (batched accel only): launch
-    // position i < *fb_count runs the query at position fb_list[i], its list
-    // seeded with the k-th distance bound fb_bound[i] (FLT_MAX: none).
+    // Fallback pass of the cell-block search (batched accel only): the list
+    // is sub-lists of fb_seg entries, each with a count in fb_count (knn.hip
+    // grid_sublist); an entry names a launch position, whose query runs with
+    // its list seeded with the k-th distance bound fb_bound[position]
+    // (FLT_MAX: none).
     const int32_t* fb_list;
     const float* fb_bound;
     const uint32_t* fb_count;
+    int64_t fb_seg;
 };
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
