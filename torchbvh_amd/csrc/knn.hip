@@ -176,16 +176,37 @@ struct SourceRow {
     float v[C];
 };
 
-template <int K, int D = 0>
+template <int K, int D = 0, bool kWideDist = false>
 __device__ __forceinline__ void write_results(const KnnArgs& a, int64_t out_row, const uint64_t (&best)[K],
                                               int64_t index_offset, int64_t pstart) {
     int64_t* oi = a.out_indices + out_row * K;
     float* od = a.out_distances + out_row * K;
+    // With kWideDist, the distance row as 16-byte stores where the output
+    // allows (a wave-uniform test): each store of a wave writes 64 rows, so
+    // four instead of sixteen at K = 16.  Measured at cfg2: the cell-block
+    // second pass -2 us with them, the first pass +10 us (its registers
+    // 87 -> 96, the same occupancy), so only the second pass asks.
+    if (kWideDist && (reinterpret_cast<uintptr_t>(a.out_distances) & 15u) == 0) {
 #pragma unroll
-    for (int i = 0; i < K; ++i) {
-        const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
-        oi[i] = idx >= 0 ? idx + index_offset : idx;
-        od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
+        for (int i = 0; i < K; ++i) {
+            const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+            oi[i] = idx >= 0 ? idx + index_offset : idx;
+        }
+        float4* od4 = reinterpret_cast<float4*>(od);
+#pragma unroll
+        for (int v = 0; v < K / 4; ++v) {
+            od4[v] = make_float4(__uint_as_float(static_cast<uint32_t>(best[4 * v] >> 32)),
+                                 __uint_as_float(static_cast<uint32_t>(best[4 * v + 1] >> 32)),
+                                 __uint_as_float(static_cast<uint32_t>(best[4 * v + 2] >> 32)),
+                                 __uint_as_float(static_cast<uint32_t>(best[4 * v + 3] >> 32)));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            const int64_t idx = static_cast<int32_t>(static_cast<uint32_t>(best[i]));
+            oi[i] = idx >= 0 ? idx + index_offset : idx;
+            od[i] = __uint_as_float(static_cast<uint32_t>(best[i] >> 32));
+        }
     }
     if constexpr (D > 0 && (K * D) % 4 == 0) {
         if (a.out_positions != nullptr && a.source_cols == D) {
@@ -1532,15 +1553,40 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
             }
         }
     }
-    // The first block's list, ascending (its k-th distance is the bound).
+    // The first block's list, ascending (its k-th distance is the bound),
+    // read as 16-byte loads where the outputs allow (wave-uniform tests).
     uint64_t best[K];
     {
         const int64_t* oi = a.out_indices + (ok ? in.out_row : 0) * K;
         const float* od = a.out_distances + (ok ? in.out_row : 0) * K;
+        uint32_t ri[K];
+        float rd[K];
+        if ((reinterpret_cast<uintptr_t>(a.out_indices) & 15u) == 0) {
 #pragma unroll
-        for (int i = 0; i < K; ++i) {
-            best[i] = ok ? candidate_key(od[i], static_cast<uint32_t>(oi[i])) : kEmptyKey;
+            for (int v = 0; v < K / 2; ++v) {
+                const int4 w = reinterpret_cast<const int4*>(oi)[v];
+                ri[2 * v] = static_cast<uint32_t>(w.x);
+                ri[2 * v + 1] = static_cast<uint32_t>(w.z);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < K; ++i) ri[i] = static_cast<uint32_t>(oi[i]);
         }
+        if ((reinterpret_cast<uintptr_t>(a.out_distances) & 15u) == 0) {
+#pragma unroll
+            for (int v = 0; v < K / 4; ++v) {
+                const float4 w = reinterpret_cast<const float4*>(od)[v];
+                rd[4 * v] = w.x;
+                rd[4 * v + 1] = w.y;
+                rd[4 * v + 2] = w.z;
+                rd[4 * v + 3] = w.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < K; ++i) rd[i] = od[i];
+        }
+#pragma unroll
+        for (int i = 0; i < K; ++i) best[i] = ok ? candidate_key(rd[i], ri[i]) : kEmptyKey;
     }
     grid_stream<D, K>(s_runs + lane, ok ? nruns : 0, static_cast<const float4*>(a.accel) + in.pstart, q, best);
     const float safe = grid_safe_margin<D>(q, root, c, shift, G, 2);
@@ -1548,7 +1594,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
     const bool done = ok && safe > 0.0f && worst < safe * safe;
     if (done) {
         const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
-        write_results<K, D>(a, out.out_row, best, 0, out.pstart);
+        write_results<K, D, true>(a, out.out_row, best, 0, out.pstart);
     }
     grid_append(list2, counts2, seg, __ballot(valid && !done), gid);
     if (ok && !done) bounds[gid] = worst;
