@@ -207,6 +207,17 @@ int tbvh_knn_accel_positions(const void* accel, const float* queries, const int6
                              const float* source_points, int source_cols,
                              int64_t* out_indices, float* out_distances, float* out_positions,
                              void* stream);
+/* tbvh_knn_accel_grid with the neighbour rows of tbvh_knn_accel_positions
+ * (the same workspace; results and rows the same as
+ * tbvh_knn_accel_positions'). */
+int tbvh_knn_accel_grid_positions(const void* accel, const float* node_aabbs,
+                                  int64_t num_real_nodes, const float* queries,
+                                  const int64_t* order, int64_t B, int64_t M,
+                                  int64_t num_leaves, int D, int k,
+                                  const float* source_points, int source_cols,
+                                  int64_t* out_indices, float* out_distances,
+                                  float* out_positions, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 int tbvh_knn_accel_ragged_positions(const void* accel, const int64_t* point_offsets,
                                     int64_t total_points, const float* queries,
                                     const int64_t* query_offsets, const int64_t* order,

@@ -111,3 +111,55 @@ def test_binding_rows_without_accel_match_fused():
         assert pos.shape == (2, 800, 16, cols)
         for b in range(2):
             assert torch.equal(pos[b], wide[b][idx[b]])
+
+
+@pytest.mark.parametrize("dim,k,cols", [(3, 16, 3), (3, 8, 5), (2, 8, 2), (3, 4, 3)])
+def test_cell_block_search_rows(dim, k, cols):
+    """Above GRID_MIN_QUERIES the rows come from the cell-block search
+    (tbvh_knn_accel_grid_positions); they, the indices and the distances
+    must equal the traversal's (tbvh_knn_accel_positions) bit for bit, and
+    source_points indexed by the returned indices."""
+    import ctypes
+
+    from torchbvh_amd import _native
+
+    n, m = 200_000, _native.GRID_MIN_QUERIES + 777
+    p = rand(n, dim, seed=11)
+    q = rand(m, dim, seed=12)
+    src = rand(n, cols, seed=13) * 10
+    h = tb.build_bvh(p)
+    idx, d = tb.query_knn(h, q, k)
+    if cols == dim:  # query_knn takes rows of the points' width (reference _query.py:169-174)
+        idx_r, d_r, pos = tb.query_knn(h, q, k, source_points=src)
+        assert torch.equal(idx_r, idx) and torch.equal(d_r, d)
+        assert torch.equal(pos, src[idx])
+    # the C ABI, any row width: grid form against the plain traversal
+    L = _native.load()
+    acc = h._aux["accel"]
+    nodes = h["node_aabbs"].unsqueeze(0)
+    nr = int(h["num_real_nodes"])
+    qb = q.unsqueeze(0)
+    need = ctypes.c_size_t(0)
+    assert L.tbvh_knn_accel_grid_workspace_size(1, m, n, dim, k, ctypes.byref(need)) == 0 and need.value > 0
+    outs = []
+    for grid in (True, False):
+        oi = torch.empty((1, m, k), dtype=torch.int64, device=DEV)
+        od = torch.empty((1, m, k), dtype=torch.float32, device=DEV)
+        op = torch.empty((1, m, k, cols), dtype=torch.float32, device=DEV)
+        if grid:
+            ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+            rc = L.tbvh_knn_accel_grid_positions(
+                _native._ptr(acc), _native._ptr(nodes), nr, _native._ptr(qb), None, 1, m, n, dim, k,
+                _native._ptr(src), cols, _native._ptr(oi), _native._ptr(od), _native._ptr(op),
+                _native._ptr(ws), need.value, _native._stream(DEV))
+        else:
+            rc = L.tbvh_knn_accel_positions(
+                _native._ptr(acc), _native._ptr(qb), None, 1, m, n, dim, k, _native._ptr(src), cols,
+                _native._ptr(oi), _native._ptr(od), _native._ptr(op), _native._stream(DEV))
+        assert rc == 0, L.tbvh_last_error()
+        outs.append((oi, od, op))
+    torch.cuda.synchronize()
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+    assert torch.equal(outs[0][0][0], idx) and torch.equal(outs[0][1][0], d)
+    assert torch.equal(outs[0][2][0], src[idx])

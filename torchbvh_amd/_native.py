@@ -110,6 +110,9 @@ def _declare(L) -> None:
     L.tbvh_knn_accel_positions.argtypes = (
         [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp]
     )
+    L.tbvh_knn_accel_grid_positions.argtypes = (
+        [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    )
     L.tbvh_knn_accel_ragged_positions.argtypes = (
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp]
     )
@@ -124,7 +127,7 @@ def _declare(L) -> None:
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
         "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
         "tbvh_knn_accel_grid_workspace_size", "tbvh_knn_accel_grid",
-        "tbvh_knn_accel_positions", "tbvh_knn_accel_ragged_positions",
+        "tbvh_knn_accel_positions", "tbvh_knn_accel_grid_positions", "tbvh_knn_accel_ragged_positions",
         "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
         "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
@@ -783,13 +786,24 @@ class _NativeOps:
             return _with_positions(indices, distances, positions, source_points)
         L = load()
         with torch.cuda.device(dev):
-            if fused:
+            grid = (accel is not None and not spatial and B * M > GRID_MIN_QUERIES
+                    and _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k)) > 0)
+            if fused and grid:
+                # The cell-block search with the neighbour rows (the same
+                # rows as tbvh_knn_accel_positions).
+                need = _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k))
+                ws = torch.empty(need, dtype=torch.uint8, device=dev)
+                _check(L.tbvh_knn_accel_grid_positions(
+                    _ptr(accel), _ptr(node_aabbs), int(num_real_nodes), _ptr(query_points), _ptr(query_order),
+                    B, M, int(num_leaves), int(dim), int(k), _ptr(source_points), C, _ptr(indices),
+                    _ptr(distances), _ptr(positions), _ptr(ws), need, _stream(dev)))
+            elif fused:
                 _check(L.tbvh_knn_accel_positions(
                     _ptr(accel), _ptr(query_points), _ptr(query_order), B, M, int(num_leaves),
                     int(dim), int(k), _ptr(source_points), C, _ptr(indices), _ptr(distances),
                     _ptr(positions), _stream(dev)))
-            elif (accel is not None and not spatial and B * M > GRID_MIN_QUERIES
-                  and (need := _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k))) > 0):
+            elif grid:
+                need = _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k))
                 # The cell-block search first (same results; see
                 # tbvh_knn_accel_grid), where the clouds allow a grid and
                 # it measured faster (a nonzero workspace).

@@ -1101,6 +1101,18 @@ int tbvh_knn_accel_positions(const void* accel, const float* queries, const int6
                              out_distances, stream_ptr, source_points, source_cols, out_positions);
 }
 
+int tbvh_knn_accel_grid_positions(const void* accel, const float* node_aabbs, int64_t num_real_nodes,
+                                  const float* queries, const int64_t* order, int64_t B, int64_t M,
+                                  int64_t num_leaves, int D, int k, const float* source_points, int source_cols,
+                                  int64_t* out_indices, float* out_distances, float* out_positions, void* ws,
+                                  size_t ws_bytes, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_grid_positions";
+    if (int r = check_positions(op, source_points, source_cols, out_positions)) return r;
+    return knn_accel_batched(op, accel, queries, order, B, M, num_leaves, D, k, false, out_indices, out_distances,
+                             stream_ptr, source_points, source_cols, out_positions, node_aabbs, num_real_nodes,
+                             ws, ws_bytes);
+}
+
 int tbvh_knn_accel_ragged_positions(const void* accel, const int64_t* point_offsets, int64_t total_points,
                                     const float* queries, const int64_t* query_offsets, const int64_t* order,
                                     int64_t B, int64_t total_q, int D, int k, const float* source_points,
