@@ -390,6 +390,16 @@ int tbvh_knn_accel_grid(const void* accel, const float* node_aabbs, int64_t num_
                         int64_t B, int64_t M, int64_t num_leaves, int D, int k,
                         int64_t* out_indices, float* out_distances,
                         void* workspace, size_t workspace_bytes, void* stream);
+/* Spatial-output form of tbvh_knn_accel_grid, for the binding
+ * `query_knn_batched_cached_bounds_spatial` (torchbvh/csrc/bindings.cpp:
+ * 199, knn_query.cu:448-461): results in launch (order) position, the same
+ * as tbvh_knn_accel_spatial's; the same workspace; `order` required. */
+int tbvh_knn_accel_grid_spatial(const void* accel, const float* node_aabbs,
+                                int64_t num_real_nodes, const float* queries,
+                                const int64_t* order, int64_t B, int64_t M,
+                                int64_t num_leaves, int D, int k,
+                                int64_t* out_indices, float* out_distances,
+                                void* workspace, size_t workspace_bytes, void* stream);
 int tbvh_knn_accel_ragged(const void* accel, const int64_t* point_offsets,
                           int64_t total_points, const float* queries,
                           const int64_t* query_offsets, const int64_t* order,

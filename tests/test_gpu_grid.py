@@ -200,3 +200,48 @@ def test_c_abi_grid_equals_accel_traversal(ordered):
     assert rc == 0 and torch.equal(ni, ti) and torch.equal(nd, td)
     rc, _, _ = _call(L, "grid", acc, h["node_aabbs"], nr + 1, qb, order, B, M, N, D, k, ws, need.value)
     assert rc != 0 and b"num_real_nodes" in L.tbvh_last_error()
+
+
+@pytest.mark.parametrize("schedule", [False, True])
+@pytest.mark.parametrize("D,k", [(3, 16), (2, 8)])
+def test_c_abi_grid_spatial_equals_accel_spatial(schedule, D, k):
+    """Spatial output (results in launch position, the MLS binding): the
+    cell-block search through tbvh_knn_accel_grid_spatial against
+    tbvh_knn_accel_spatial, bit for bit, with the full Morton order the
+    reference binding produces and with the traversal schedule; and the
+    _C binding (which takes it above GRID_MIN_QUERIES) against both."""
+    rng = np.random.default_rng(17 + k)
+    B, N, M = 2, 200_000, GRID_MIN_QUERIES // 2 + 901
+    p = rng.random((B, N, D), dtype=np.float32)
+    q = rng.random((B, M, D), dtype=np.float32)
+    h = tb.build_bvh(dev(p))
+    acc = h._aux["accel"]
+    qb = dev(q)
+    order = _C.morton_sort_queries_narrow(qb, h["scene_min"], h["scene_max"], schedule=schedule)
+    L = _native.load()
+    need = ctypes.c_size_t(0)
+    assert L.tbvh_knn_accel_grid_workspace_size(B, M, N, D, k, ctypes.byref(need)) == 0 and need.value > 0
+    ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+    nr = int(h["num_real_nodes"])
+    P, st = _native._ptr, _native._stream(DEV)
+    outs = []
+    for grid in (True, False):
+        idx = torch.full((B, M, k), -7, dtype=torch.int64, device=DEV)
+        dist = torch.full((B, M, k), -7.0, device=DEV)
+        if grid:
+            rc = L.tbvh_knn_accel_grid_spatial(P(acc), P(h["node_aabbs"]), nr, P(qb), P(order), B, M, N, D, k,
+                                               P(idx), P(dist), P(ws), need.value, st)
+        else:
+            rc = L.tbvh_knn_accel_spatial(P(acc), P(qb), P(order), B, M, N, D, k, P(idx), P(dist), st)
+        assert rc == 0, L.tbvh_last_error()
+        outs.append((idx, dist))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    bi, bd = _C.query_knn_batched_cached_bounds_spatial(h["node_aabbs"], h["sorted_indices"], qb, order,
+                                                        h["num_leaves"], h["num_real_nodes"], D, k)
+    assert torch.equal(bi, outs[1][0]) and torch.equal(bd, outs[1][1])
+    # cloud 0 against the oracle, rows mapped back from launch position to input row
+    o = order[0].cpu().numpy()
+    ei, ed = oracle.knn_bvh(oracle.build(p[0]), q[0][o], k)
+    assert_same_int(bi[0].cpu().numpy(), ei, "cloud 0 indices (launch order)")
+    assert_same_f32(bd[0].cpu().numpy(), ed, "cloud 0 distances (launch order)")

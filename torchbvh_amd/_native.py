@@ -110,6 +110,7 @@ def _declare(L) -> None:
     L.tbvh_knn_accel_positions.argtypes = (
         [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp]
     )
+    L.tbvh_knn_accel_grid_spatial.argtypes = L.tbvh_knn_accel_grid.argtypes
     L.tbvh_knn_accel_grid_positions.argtypes = (
         [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     )
@@ -126,7 +127,7 @@ def _declare(L) -> None:
         "tbvh_morton_codes", "tbvh_knn", "tbvh_knn_ragged", "tbvh_accel_size",
         "tbvh_accel_workspace_size", "tbvh_accel_build", "tbvh_accel_build_ragged",
         "tbvh_knn_accel", "tbvh_knn_accel_ragged", "tbvh_knn_spatial", "tbvh_knn_accel_spatial",
-        "tbvh_knn_accel_grid_workspace_size", "tbvh_knn_accel_grid",
+        "tbvh_knn_accel_grid_workspace_size", "tbvh_knn_accel_grid", "tbvh_knn_accel_grid_spatial",
         "tbvh_knn_accel_positions", "tbvh_knn_accel_grid_positions", "tbvh_knn_accel_ragged_positions",
         "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
@@ -786,9 +787,9 @@ class _NativeOps:
             return _with_positions(indices, distances, positions, source_points)
         L = load()
         with torch.cuda.device(dev):
-            grid = (accel is not None and not spatial and B * M > GRID_MIN_QUERIES
+            grid = (accel is not None and B * M > GRID_MIN_QUERIES
                     and _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k)) > 0)
-            if fused and grid:
+            if fused and grid and not spatial:
                 # The cell-block search with the neighbour rows (the same
                 # rows as tbvh_knn_accel_positions).
                 need = _grid_workspace_size(B, M, int(num_leaves), int(dim), int(k))
@@ -808,7 +809,8 @@ class _NativeOps:
                 # tbvh_knn_accel_grid), where the clouds allow a grid and
                 # it measured faster (a nonzero workspace).
                 ws = torch.empty(need, dtype=torch.uint8, device=dev)
-                _check(L.tbvh_knn_accel_grid(
+                fn = L.tbvh_knn_accel_grid_spatial if spatial else L.tbvh_knn_accel_grid
+                _check(fn(
                     _ptr(accel), _ptr(node_aabbs), int(num_real_nodes), _ptr(query_points), _ptr(query_order),
                     B, M, int(num_leaves), int(dim), int(k), _ptr(indices), _ptr(distances),
                     _ptr(ws), need, _stream(dev)))

@@ -1033,6 +1033,15 @@ int tbvh_knn_accel(const void* accel, const float* queries, const int64_t* order
                              out_indices, out_distances, stream_ptr);
 }
 
+int tbvh_knn_accel_grid_spatial(const void* accel, const float* node_aabbs, int64_t num_real_nodes,
+                                const float* queries, const int64_t* order, int64_t B, int64_t M, int64_t num_leaves,
+                                int D, int k, int64_t* out_indices, float* out_distances, void* ws, size_t ws_bytes,
+                                void* stream_ptr) {
+    return knn_accel_batched("tbvh_knn_accel_grid_spatial", accel, queries, order, B, M, num_leaves, D, k, true,
+                             out_indices, out_distances, stream_ptr, nullptr, 0, nullptr, node_aabbs, num_real_nodes,
+                             ws, ws_bytes);
+}
+
 int tbvh_knn_accel_spatial(const void* accel, const float* queries, const int64_t* order, int64_t B,
                            int64_t M, int64_t num_leaves, int D, int k, int64_t* out_indices,
                            float* out_distances, void* stream_ptr) {

@@ -1770,8 +1770,7 @@ size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D) {
 hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t nr, int level, int D, int K,
                            void* ws, hipStream_t stream) {
     if (args.total_q == 0) return hipSuccess;
-    if (level < 2 || args.routes != nullptr || args.spatial_output || args.total_q >= (int64_t(1) << 31) ||
-        args.M <= 0) {
+    if (level < 2 || args.routes != nullptr || args.total_q >= (int64_t(1) << 31) || args.M <= 0) {
         return hipErrorInvalidValue;
     }
     const GridLayout g = grid_layout(args.B, args.total_q, level, D);
