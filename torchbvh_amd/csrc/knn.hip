@@ -1153,6 +1153,24 @@ struct NearOrder {
     static constexpr int dz(int o) { return D == 3 ? (o >> 6) - W : 0; }
 };
 
+// The cell-block passes' point distance.  Every point and query they take is
+// finite (grid_table_kernel disables a cloud holding a non-finite point or
+// box; a lane with a non-finite query takes no part), so e = p - q is never
+// NaN and point_distance's max(|e|, 0) is |e|; |e|^2 and e^2 are the same
+// bits (IEEE products are sign-symmetric, fused or not; an overflowed
+// difference squares to inf either way).
+template <int D>
+__device__ __forceinline__ float point_distance_finite(const float* q, const float4 p) {
+    const float pc[3] = {p.x, p.y, p.z};
+    float s = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const float e = pc[d] - q[d];
+        s = d == 0 ? e * e : __builtin_fmaf(e, e, s);
+    }
+    return s;
+}
+
 // Streams one lane's runs into its list: `runs` is the lane's column of
 // packed runs ((first point << 8) | count, kKnnBlock words apart), `nruns`
 // of them, `pts` the cloud's accel points.  A chunk takes the rest of the
@@ -1381,17 +1399,29 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
         const int s1 = s - n0;  // slot u >= n0 takes point s1 + u
         const int n1 = min(e - s, kChunk - n0);
         s += n1;
+        // Slot u >= n0 reads row s1 + u >= the next run's start (s1 is it
+        // less n0), so every row is non-negative; a slot past n0 + n1 reads
+        // at most kChunk - 1 rows past a row the lane was given (rows 0 ..
+        // kChunk - 1 for a lane given none), inside the accel buffer, whose
+        // record rows follow its point rows, and its key is dropped.
+        // Measured against the select form below (padding slots reading row
+        // 0), pass 1 at cfg2: 241.7 -> 236.9 us at 3-D k = 16, 261.7 ->
+        // 254.6 us at k = 32; but 2-D k = 8 550.7 -> 598.7 us, where padding
+        // slots are more common, and 3-D k = 8 takes 82 VGPRs instead of 76
+        // (6 -> 5 waves per SIMD).
         float4 p[kChunk];
+        if constexpr (D == 3 && K >= 16) {
 #pragma unroll
-        for (int u = 0; u < kChunk; ++u) {
-            const int row = u < n0 ? s0 + u : u < n0 + n1 ? s1 + u : 0;
-            p[u] = pts[row];
+            for (int u = 0; u < kChunk; ++u) p[u] = pts[static_cast<uint32_t>(u < n0 ? s0 + u : s1 + u)];
+        } else {
+#pragma unroll
+            for (int u = 0; u < kChunk; ++u) p[u] = pts[u < n0 ? s0 + u : u < n0 + n1 ? s1 + u : 0];
         }
         uint64_t cand[kChunk];
         uint64_t least = kEmptyKey;
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
-            const float dd = point_distance<D>(q, p[u]);
+            const float dd = point_distance_finite<D>(q, p[u]);
             cand[u] = u < n0 + n1 && dd < kFar ? candidate_key(dd, __float_as_uint(p[u].w)) : kEmptyKey;
             least = key_min(least, cand[u]);
         }
