@@ -1252,9 +1252,8 @@ __device__ __forceinline__ float grid_safe_margin(const float* q, const float* r
 constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K == 16); }
 
 // One query per lane, in launch order like the traversal (same tile map).
-// Failing queries are recorded per tile (a mask of its lanes, bounds[gid]
-// their block's k-th distance, FLT_MAX where none was taken), so that
-// grid_offsets_kernel and grid_list_kernel list them in launch order.
+// Failing queries are appended to the failure list (grid_append; bounds[gid]
+// their block's k-th distance, FLT_MAX where none was taken).
 //
 // A lane first reads the runs of its block's cells (first point and count,
 // packed into one LDS word per cell: clouds of at most 2^24 points, runs of

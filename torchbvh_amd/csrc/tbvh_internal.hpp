@@ -443,7 +443,7 @@ hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t s
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 
 // Cell-block k-NN (batched accel, `a` as for launch_knn_accel without
-// routes, spatial output or neighbour rows): every cloud's accel points are
+// routes; spatial output and neighbour rows as there): every cloud's accel points are
 // cut into the level-`level` Morton cells against its root box (row 0 of
 // its node_aabbs, `nr` rows per cloud); each query scans the 3^D cells
 // around its own and keeps the result when its k-th distance is inside the
