@@ -195,6 +195,24 @@ def test_grid_knn_workspace_and_argument_errors():
     assert L.tbvh_knn_accel_grid(FAKE, None, nr, FAKE, None, 1, M, N, 3, 8, FAKE, FAKE, FAKE, need, None) == 1
     assert "node_aabbs" in _err(L)
     assert L.tbvh_knn_accel_grid(None, None, 0, None, None, 1, 0, N, 3, 8, None, None, None, 0, None) == 0
+    # The spatial form needs the launch order; the neighbour-row form its source and rows, then
+    # the same checks as the plain form.
+    sp = lambda order, nr_, ws_bytes: (FAKE, FAKE, nr_, FAKE, order, 1, M, N, 3, 8, FAKE, FAKE, FAKE, ws_bytes, None)
+    assert L.tbvh_knn_accel_grid_spatial(*sp(None, nr, need)) == 1
+    assert "null" in _err(L)
+    assert L.tbvh_knn_accel_grid_spatial(*sp(FAKE, nr + 1, need)) == 1
+    assert "num_real_nodes" in _err(L)
+    assert L.tbvh_knn_accel_grid_spatial(*sp(FAKE, nr, need - 1)) == 2
+    pos = lambda src, cols, nr_, ws_bytes: (FAKE, FAKE, nr_, FAKE, None, 1, M, N, 3, 8, src, cols, FAKE, FAKE, FAKE,
+                                            FAKE, ws_bytes, None)
+    assert L.tbvh_knn_accel_grid_positions(*pos(None, 3, nr, need)) == 1
+    assert "source" in _err(L)
+    assert L.tbvh_knn_accel_grid_positions(*pos(FAKE, 0, nr, need)) == 1
+    assert "source_cols" in _err(L)
+    assert L.tbvh_knn_accel_grid_positions(*pos(FAKE, 3, nr + 1, need)) == 1
+    assert "num_real_nodes" in _err(L)
+    assert L.tbvh_knn_accel_grid_positions(*pos(FAKE, 3, nr, need - 1)) == 2
+    assert "workspace" in _err(L)
 
 
 def test_accel_from_tree_and_accel_alignment_errors():
