@@ -1057,9 +1057,11 @@ __device__ __forceinline__ void grid_append(int32_t* list, uint32_t* counts, int
                                             int64_t gid) {
     if (left == 0) return;
     const int sub = grid_sublist();
+    // The first active lane reserves the entries and hands out the base.
+    const int leader = __ffsll(static_cast<long long>(__ballot(1))) - 1;
     uint32_t base = 0;
-    if (lane_id() == 0) base = atomicAdd(&counts[sub * kCountStride], static_cast<uint32_t>(__popcll(left)));
-    base = __builtin_amdgcn_readlane(base, 0);
+    if (lane_id() == leader) base = atomicAdd(&counts[sub * kCountStride], static_cast<uint32_t>(__popcll(left)));
+    base = __builtin_amdgcn_readlane(base, leader);
     if ((left >> lane_id()) & 1ull) {
         const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(left >> 32),
                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(left), 0u));
