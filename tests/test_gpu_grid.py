@@ -245,3 +245,49 @@ def test_c_abi_grid_spatial_equals_accel_spatial(schedule, D, k):
     ei, ed = oracle.knn_bvh(oracle.build(p[0]), q[0][o], k)
     assert_same_int(bi[0].cpu().numpy(), ei, "cloud 0 indices (launch order)")
     assert_same_f32(bd[0].cpu().numpy(), ed, "cloud 0 distances (launch order)")
+
+
+def test_grid_spatial_and_rows_with_disabled_cloud_and_nonfinite_queries():
+    """A batched call mixing a near-uniform cloud with a disabled one (NaN
+    points), with NaN and infinite queries in both: the spatial-output and
+    neighbour-row forms of the cell-block search equal the plain traversal's
+    spatial and neighbour-row forms bit for bit (the disabled cloud and the
+    non-finite queries go to the traversal)."""
+    rng = np.random.default_rng(29)
+    B, N, M, D, k, C = 2, 150_000, GRID_MIN_QUERIES // 2 + 333, 3, 16, 3
+    p = rng.random((B, N, D), dtype=np.float32)
+    p[1, ::997] = np.nan
+    q = rng.random((B, M, D), dtype=np.float32)
+    q[0, 5] = np.nan
+    q[0, 77, 1] = np.inf
+    q[1, 11, 2] = -np.inf
+    src = rng.random((B, N, C), dtype=np.float32)
+    h = tb.build_bvh(dev(p))
+    acc = h._aux["accel"]
+    qb, sb = dev(q), dev(src)
+    order = _C.morton_sort_queries_narrow(qb, h["scene_min"], h["scene_max"])
+    L = _native.load()
+    need = ctypes.c_size_t(0)
+    assert L.tbvh_knn_accel_grid_workspace_size(B, M, N, D, k, ctypes.byref(need)) == 0 and need.value > 0
+    ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+    nr = int(h["num_real_nodes"])
+    P, st = _native._ptr, _native._stream(DEV)
+
+    def outs():
+        return (torch.full((B, M, k), -7, dtype=torch.int64, device=DEV), torch.full((B, M, k), -7.0, device=DEV),
+                torch.full((B, M, k, C), -7.0, device=DEV))
+
+    gi, gd, _ = outs()
+    ti, td, _ = outs()
+    assert L.tbvh_knn_accel_grid_spatial(P(acc), P(h["node_aabbs"]), nr, P(qb), P(order), B, M, N, D, k, P(gi),
+                                         P(gd), P(ws), need.value, st) == 0
+    assert L.tbvh_knn_accel_spatial(P(acc), P(qb), P(order), B, M, N, D, k, P(ti), P(td), st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(gi, ti) and torch.equal(gd, td)
+    gi, gd, gp = outs()
+    ti, td, tp = outs()
+    assert L.tbvh_knn_accel_grid_positions(P(acc), P(h["node_aabbs"]), nr, P(qb), P(order), B, M, N, D, k, P(sb), C,
+                                           P(gi), P(gd), P(gp), P(ws), need.value, st) == 0
+    assert L.tbvh_knn_accel_positions(P(acc), P(qb), P(order), B, M, N, D, k, P(sb), C, P(ti), P(td), P(tp), st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(gi, ti) and torch.equal(gd, td) and torch.equal(gp, tp)
