@@ -429,6 +429,25 @@ int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_acce
                                   int64_t true_num_leaves, int64_t false_num_leaves,
                                   int D, int k,
                                   int64_t* out_indices, float* out_distances, void* stream);
+/* Cell-block form of tbvh_knn_accel_routed_spatial, for the same binding
+ * (no counterpart in the reference; identical results): each query first
+ * searches the block of grid cells around it in its route's structure (as
+ * tbvh_knn_accel_grid does, against that structure's root box, row 0 of
+ * its node_aabbs per cloud), and the queries the block cannot decide run
+ * the routed accel traversal.  Workspace:
+ * tbvh_knn_accel_routed_grid_workspace_size (0 where either cloud is too
+ * small for a grid, or of 2^24 points or more: then this is
+ * tbvh_knn_accel_routed_spatial); a null workspace also runs that. */
+int tbvh_knn_accel_routed_grid_workspace_size(int64_t B, int64_t M, int64_t true_num_leaves,
+                                              int64_t false_num_leaves, int D, int k, size_t* bytes);
+int tbvh_knn_accel_routed_grid_spatial(const void* true_accel, const float* true_node_aabbs,
+                                       int64_t true_num_real_nodes, const void* false_accel,
+                                       const float* false_node_aabbs, int64_t false_num_real_nodes,
+                                       const float* queries, const uint8_t* routes,
+                                       const int64_t* order, int64_t B, int64_t M,
+                                       int64_t true_num_leaves, int64_t false_num_leaves,
+                                       int D, int k, int64_t* out_indices, float* out_distances,
+                                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- displaced-query interpolation --------------------------------------------------
  * Replaces the neighbour gather and rank loop of `interpolate_displaced`

@@ -215,6 +215,65 @@ def test_grid_knn_workspace_and_argument_errors():
     assert "workspace" in _err(L)
 
 
+def test_routed_grid_workspace_and_argument_errors():
+    """The routed cell-block search's workspace: the true route's tables,
+    then the false route's (each at its own cloud's level), flags for both
+    structures' clouds, then the counts, lists and bounds as in the plain
+    search; none where either cloud takes no grid.  Argument errors before
+    any launch."""
+    L = _native.load()
+    size = ctypes.c_size_t()
+    up = lambda x: (x + 255) // 256 * 256
+    B, M = 2, 1000
+    # True clouds of 2^20 points (k = 16, 3-D: level 6, 2^18 cells), false clouds of 2^17 (level 5).
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 20, 1 << 17, 3, 16, ctypes.byref(size)) == 0
+    tiles = (B * M + 63) // 64
+    seg = ((tiles + 7) // 8 + 63) // 64 * 64
+    end = up(up(B * ((1 << 18) + 1) * 4) + B * ((1 << 15) + 1) * 4)
+    end = up(end + 2 * B * 4)
+    end = up(end + 2 * 512 * 32 * 4)
+    end = up(up(end + 512 * seg * 4) + 512 * seg * 4)
+    assert size.value == up(end + B * M * 4)
+    # Swapped clouds: the true route's table is the smaller one, the total the same.
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 17, 1 << 20, 3, 16, ctypes.byref(size)) == 0
+    assert size.value == up(end + B * M * 4)
+    # Either cloud without a grid: none (the call is then tbvh_knn_accel_routed_spatial).
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 20, 1000, 3, 4, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 24, 1 << 20, 3, 16, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 20, 1 << 20, 3, 5, ctypes.byref(size)) == 1
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 20, 1 << 20, 4, 16, ctypes.byref(size)) == 1
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 20, 8, 3, 16, ctypes.byref(size)) == 1
+    assert "source counts" in _err(L)
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, 1 << 20, 1 << 20, 3, 16, None) == 1
+    N = 1 << 17
+    assert L.tbvh_knn_accel_routed_grid_workspace_size(B, M, N, N, 3, 8, ctypes.byref(size)) == 0
+    need = size.value
+    assert need > 0
+    nr = _native.real_node_count(N)
+
+    def call(nr_t=nr, nr_f=nr, ws=FAKE, ws_bytes=need, nodes_f=FAKE, routes=FAKE, accel_f=FAKE, Mq=M):
+        return L.tbvh_knn_accel_routed_grid_spatial(FAKE, FAKE, nr_t, accel_f, nodes_f, nr_f, FAKE, routes, FAKE,
+                                                    B, Mq, N, N, 3, 8, FAKE, FAKE, ws, ws_bytes, None)
+    assert call(nr_f=nr + 1) == 1
+    assert "num_real_nodes" in _err(L)
+    assert call(nr_t=nr - 1) == 1
+    assert "num_real_nodes" in _err(L)
+    assert call(ws_bytes=need - 1) == 2
+    assert "workspace" in _err(L)
+    assert call(ws=ctypes.c_void_p(0x100008)) == 1
+    assert "aligned" in _err(L)
+    assert call(nodes_f=None) == 1
+    assert "node_aabbs" in _err(L)
+    assert call(routes=None) == 1
+    assert "null" in _err(L)
+    assert call(accel_f=ctypes.c_void_p(0x100010)) == 1
+    assert "aligned" in _err(L)
+    assert L.tbvh_knn_accel_routed_grid_spatial(None, None, 0, None, None, 0, None, None, None, B, 0, N, N, 3, 8,
+                                                None, None, None, 0, None) == 0
+
+
 def test_accel_from_tree_and_accel_alignment_errors():
     """tbvh_accel_build_from_tree checks the node count against the tree
     over N points and needs its defects word; every k-NN accel entry point

@@ -85,6 +85,11 @@ def _declare(L) -> None:
     L.tbvh_knn_accel_routed_spatial.argtypes = (
         [_vp] * 5 + [_i64] * 4 + [_int, _int, _vp, _vp, _vp]
     )
+    L.tbvh_knn_accel_routed_grid_workspace_size.argtypes = [_i64, _i64, _i64, _i64, _int, _int, _vp]
+    L.tbvh_knn_accel_routed_grid_spatial.argtypes = (
+        [_vp, _vp, _i64, _vp, _vp, _i64] + [_vp] * 3 + [_i64] * 4
+        + [_int, _int, _vp, _vp, _vp, ctypes.c_size_t, _vp]
+    )
     L.tbvh_morton_codes.argtypes = [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]
     L.tbvh_knn.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]
     L.tbvh_knn_spatial.argtypes = L.tbvh_knn.argtypes
@@ -131,6 +136,7 @@ def _declare(L) -> None:
         "tbvh_knn_accel_positions", "tbvh_knn_accel_grid_positions", "tbvh_knn_accel_ragged_positions",
         "tbvh_sort_routed_queries_workspace_size", "tbvh_sort_routed_queries",
         "tbvh_knn_routed_spatial", "tbvh_knn_accel_routed_spatial",
+        "tbvh_knn_accel_routed_grid_workspace_size", "tbvh_knn_accel_routed_grid_spatial",
         "tbvh_build_primitives_workspace_size", "tbvh_build_primitives",
         "tbvh_morton_sort_points_workspace_size", "tbvh_morton_sort_points",
         "tbvh_interpolate_neighbors", "tbvh_build_with_accel_noalloc", "tbvh_accel_build_from_tree",
@@ -239,6 +245,15 @@ def _grid_workspace_size(B: int, M: int, n: int, D: int, k: int) -> int:
     where it does not run (tbvh_knn_accel_grid_workspace_size)."""
     need = ctypes.c_size_t(0)
     _check(load().tbvh_knn_accel_grid_workspace_size(B, M, n, D, k, ctypes.byref(need)))
+    return int(need.value)
+
+
+@functools.lru_cache(maxsize=256)
+def _routed_grid_workspace_size(B: int, M: int, n_true: int, n_false: int, D: int, k: int) -> int:
+    """Workspace bytes of the routed cell-block search, 0 where it does not
+    run (tbvh_knn_accel_routed_grid_workspace_size)."""
+    need = ctypes.c_size_t(0)
+    _check(load().tbvh_knn_accel_routed_grid_workspace_size(B, M, n_true, n_false, D, k, ctypes.byref(need)))
     return int(need.value)
 
 
@@ -939,7 +954,20 @@ class _NativeOps:
         false_accel = _pick_accel(op, false_accel, false_node_aabbs, false_sorted_indices, int(dim))
         L = load()
         with torch.cuda.device(dev):
-            if true_accel is not None and false_accel is not None:
+            need = 0
+            if true_accel is not None and false_accel is not None and B * M > GRID_MIN_QUERIES:
+                need = _routed_grid_workspace_size(B, M, int(true_num_leaves), int(false_num_leaves),
+                                                   int(dim), int(k))
+            if need > 0:
+                # The cell-block search in each query's route's structure
+                # first (the same results; see tbvh_knn_accel_grid).
+                ws = torch.empty(need, dtype=torch.uint8, device=dev)
+                _check(L.tbvh_knn_accel_routed_grid_spatial(
+                    _ptr(true_accel), _ptr(true_node_aabbs), int(true_num_real_nodes), _ptr(false_accel),
+                    _ptr(false_node_aabbs), int(false_num_real_nodes), _ptr(query_points), _ptr(routes),
+                    _ptr(query_order), B, M, int(true_num_leaves), int(false_num_leaves), int(dim), int(k),
+                    _ptr(indices), _ptr(distances), _ptr(ws), need, _stream(dev)))
+            elif true_accel is not None and false_accel is not None:
                 _check(L.tbvh_knn_accel_routed_spatial(
                     _ptr(true_accel), _ptr(false_accel), _ptr(query_points), _ptr(routes),
                     _ptr(query_order), B, M, int(true_num_leaves), int(false_num_leaves), int(dim),

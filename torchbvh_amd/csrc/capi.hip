@@ -1192,11 +1192,12 @@ int tbvh_knn_routed_spatial(const float* true_node_aabbs, const int64_t* true_so
     return ok();
 }
 
-int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_accel, const float* queries,
-                                  const uint8_t* routes, const int64_t* order, int64_t B, int64_t M,
-                                  int64_t true_num_leaves, int64_t false_num_leaves, int D, int k,
-                                  int64_t* out_indices, float* out_distances, void* stream_ptr) {
-    const char* op = "tbvh_knn_accel_routed_spatial";
+// The routed accel traversal's arguments, checked (shared by the plain and
+// the cell-block entry points).
+static int routed_accel_args(const char* op, const void* true_accel, const void* false_accel,
+                             const float* queries, const uint8_t* routes, const int64_t* order, int64_t B,
+                             int64_t M, int64_t true_num_leaves, int64_t false_num_leaves, int D, int k,
+                             int64_t* out_indices, float* out_distances, KnnArgs& a) {
     if (int r = check_routed(op, B, M, true_num_leaves, false_num_leaves, kMaxAccelCloud, D, k)) return r;
     if (M == 0) return ok();
     if (!true_accel || !false_accel || !queries || !routes || !order || !out_indices || !out_distances) {
@@ -1205,7 +1206,7 @@ int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_acce
     if (!aligned(true_accel) || !aligned(false_accel)) {
         return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: accels must be %zu-byte aligned", op, kAlign);
     }
-    KnnArgs a{};
+    a = KnnArgs{};
     a.queries = queries;
     a.order = order;
     a.routes = routes;
@@ -1220,7 +1221,69 @@ int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_acce
     a.out_indices = out_indices;
     a.out_distances = out_distances;
     a.spatial_output = true;
+    return TBVH_OK;
+}
+
+int tbvh_knn_accel_routed_spatial(const void* true_accel, const void* false_accel, const float* queries,
+                                  const uint8_t* routes, const int64_t* order, int64_t B, int64_t M,
+                                  int64_t true_num_leaves, int64_t false_num_leaves, int D, int k,
+                                  int64_t* out_indices, float* out_distances, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_routed_spatial";
+    KnnArgs a{};
+    if (int r = routed_accel_args(op, true_accel, false_accel, queries, routes, order, B, M, true_num_leaves,
+                                  false_num_leaves, D, k, out_indices, out_distances, a)) {
+        return r;
+    }
+    if (M == 0) return ok();
     TBVH_TRY(op, launch_knn_accel(a, D, k, false, static_cast<hipStream_t>(stream_ptr)));
+    return ok();
+}
+
+int tbvh_knn_accel_routed_grid_workspace_size(int64_t B, int64_t M, int64_t true_num_leaves,
+                                              int64_t false_num_leaves, int D, int k, size_t* bytes) {
+    const char* op = "tbvh_knn_accel_routed_grid_workspace_size";
+    if (!bytes) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null output pointer", op);
+    if (int r = check_routed(op, B, M, true_num_leaves, false_num_leaves, kMaxAccelCloud, D, k)) return r;
+    const int level = grid_level(true_num_leaves, D, k);
+    const int level2 = grid_level(false_num_leaves, D, k);
+    *bytes = level > 0 && level2 > 0 ? grid_workspace_bytes(B, B * M, level, D, level2) : 0;
+    return ok();
+}
+
+int tbvh_knn_accel_routed_grid_spatial(const void* true_accel, const float* true_node_aabbs,
+                                       int64_t true_num_real_nodes, const void* false_accel,
+                                       const float* false_node_aabbs, int64_t false_num_real_nodes,
+                                       const float* queries, const uint8_t* routes, const int64_t* order,
+                                       int64_t B, int64_t M, int64_t true_num_leaves, int64_t false_num_leaves,
+                                       int D, int k, int64_t* out_indices, float* out_distances, void* ws,
+                                       size_t ws_bytes, void* stream_ptr) {
+    const char* op = "tbvh_knn_accel_routed_grid_spatial";
+    KnnArgs a{};
+    if (int r = routed_accel_args(op, true_accel, false_accel, queries, routes, order, B, M, true_num_leaves,
+                                  false_num_leaves, D, k, out_indices, out_distances, a)) {
+        return r;
+    }
+    if (M == 0) return ok();
+    const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const int level = ws ? grid_level(true_num_leaves, D, k) : 0;
+    const int level2 = ws ? grid_level(false_num_leaves, D, k) : 0;
+    if (level > 0 && level2 > 0) {
+        if (!true_node_aabbs || !false_node_aabbs) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: null node_aabbs", op);
+        if (true_num_real_nodes != tree::real_node_count(static_cast<int>(true_num_leaves)) ||
+            false_num_real_nodes != tree::real_node_count(static_cast<int>(false_num_leaves))) {
+            return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: num_real_nodes does not match num_leaves", op);
+        }
+        if (!aligned(ws)) return fail(TBVH_ERR_INVALID_ARGUMENT, "%s: workspace must be %zu-byte aligned", op, kAlign);
+        const size_t need = grid_workspace_bytes(B, B * M, level, D, level2);
+        if (ws_bytes < need) {
+            return fail(TBVH_ERR_WORKSPACE_TOO_SMALL, "%s: workspace of %zu bytes is smaller than the %zu needed", op,
+                        ws_bytes, need);
+        }
+        TBVH_TRY(op, launch_grid_knn(a, true_node_aabbs, true_num_real_nodes, level, D, k, ws, stream,
+                                     false_node_aabbs, false_num_real_nodes, level2));
+        return ok();
+    }
+    TBVH_TRY(op, launch_knn_accel(a, D, k, false, stream));
     return ok();
 }
 

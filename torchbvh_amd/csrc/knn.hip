@@ -915,7 +915,7 @@ __device__ __forceinline__ void knn_query(const KnnArgs& a) {
     // all displaced by points, the bound's own included: the result is
     // exact).  Work-group b takes a chunk of sub-list grid_sublist(), fb_seg
     // entries apart (the grid is sized for every query).
-    const bool fallback = kAccel && !kRouted && a.fb_list != nullptr;
+    const bool fallback = kAccel && a.fb_list != nullptr;
     const int64_t tile = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     int64_t gid = tile * kKnnBlock + threadIdx.x;
     float seed = kFar;
@@ -1253,6 +1253,16 @@ __device__ __forceinline__ float grid_safe_margin(const float* q, const float* r
 // Whether the second pass runs (see grid_knn2_kernel).
 constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K == 16); }
 
+// A routed search's second structure (the false route's): its node boxes
+// (`nr` rows per cloud, row 0 the root box), its level and its clouds'
+// first-point tables.  Its clouds' flags follow the first's (flags[B + b]).
+struct GridSecond {
+    const float* nodes;
+    int64_t nr;
+    int level;
+    const int32_t* table;
+};
+
 // One query per lane, in launch order like the traversal (same tile map).
 // Failing queries are appended to the failure list (grid_append; bounds[gid]
 // their block's k-th distance, FLT_MAX where none was taken).
@@ -1266,12 +1276,16 @@ constexpr bool grid_second_pass(int D, int K) { return D == 3 && (K == 8 || K ==
 // points per cell, nearly always two chunks of 6 somewhere among 64 lanes:
 // about 55 merges per wave at cfg2); the stream costs ceil(points / 8) per
 // lane.
-template <int D, int K, bool kOrdered>
+//
+// Routed (kRouted: batched, ordered, spatial output): each lane searches
+// the structure its query's route names (locate), with that structure's
+// box, level, table and points, its indices offset as in the traversal.
+template <int D, int K, bool kOrdered, bool kRouted>
 __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const float* __restrict__ node_aabbs, int64_t nr,
                                                          int level, const int32_t* __restrict__ table,
                                                          const uint32_t* __restrict__ flags, int32_t* __restrict__ list,
                                                          uint32_t* __restrict__ counts, int64_t seg,
-                                                         float* __restrict__ bounds) {
+                                                         float* __restrict__ bounds, GridSecond g2) {
     using Order = NearOrder<D, 1>;
     constexpr int kCells = Order::kCells;
     __shared__ uint32_t s_runs[kCells * kKnnBlock];
@@ -1285,38 +1299,57 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     // order entry: no result).  A lane on a corrupt entry here takes no part.
     bool valid = gid < a.total_q;
     const int64_t b = valid ? gid / a.M : 0;
-    bool ok = valid && flags[b] == 0u;
-    if (__ballot(ok) == 0) {
-        grid_append(list, counts, seg, __ballot(valid), gid);
-        if (valid) bounds[gid] = kFar;
-        return;
-    }
+    bool ok;
     QueryLoc in{};
-    if (valid) {
-        in = locate<kOrdered, false, false, true>(a, gid);
-        valid = in.row >= 0;
-        ok = ok && valid;
+    if constexpr (kRouted) {
+        // The route names the structure, so the query is located first; the
+        // false route's clouds have flags B .. 2B - 1.
+        const bool launched = valid;
+        if (valid) {
+            in = locate<true, false, true, true>(a, gid);
+            valid = in.row >= 0;
+        }
+        ok = valid && flags[(in.second ? a.B : 0) + b] == 0u;
+        if (__ballot(ok) == 0) {
+            grid_append(list, counts, seg, __ballot(launched), gid);
+            if (launched) bounds[gid] = kFar;
+            return;
+        }
+    } else {
+        ok = valid && flags[b] == 0u;
+        if (__ballot(ok) == 0) {
+            grid_append(list, counts, seg, __ballot(valid), gid);
+            if (valid) bounds[gid] = kFar;
+            return;
+        }
+        if (valid) {
+            in = locate<kOrdered, false, false, true>(a, gid);
+            valid = in.row >= 0;
+            ok = ok && valid;
+        }
     }
-    const int n = a.num_leaves;
+    const bool second = kRouted && in.second;
+    const int n = kRouted ? in.n : a.num_leaves;
     float q[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         q[d] = valid ? a.queries[in.row * D + d] : 0.0f;
         ok = ok && isfinite(q[d]);
     }
-    const float* root = node_aabbs + b * nr * 2 * D;
+    const float* root = second ? g2.nodes + b * g2.nr * 2 * D : node_aabbs + b * nr * 2 * D;
     float lo[D], hi[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         lo[d] = root[d];
         hi[d] = root[D + d];
     }
-    const int shift = grid_axis_bits<D>() - level;
-    const int G = 1 << level;
+    const int lv = second ? g2.level : level;
+    const int shift = grid_axis_bits<D>() - lv;
+    const int G = 1 << lv;
     uint32_t c[D];
     grid_cell<D>(q, lo, hi, shift, c);
-    const int64_t cells = int64_t(1) << (D * level);
-    const int32_t* t = table + b * (cells + 1);
+    const int64_t cells = int64_t(1) << (D * lv);
+    const int32_t* t = (second ? g2.table : table) + b * (cells + 1);
     // The block's runs, nearest cells first.  The search is kept only while
     // the block's point count stays near the cloud's mean (4x); past that,
     // or a run longer than a count field holds, the lane goes to the
@@ -1368,7 +1401,7 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     // The stream of grid_stream, written out here: as a call it came out at
     // 136 VGPRs instead of 89 at 3-D k = 16 (3 waves per SIMD instead of 5).
     constexpr int kChunk = 8;
-    const float4* pts = static_cast<const float4*>(a.accel) + in.pstart;
+    const float4* pts = static_cast<const float4*>(second ? a.accel2 : a.accel) + in.pstart;
     // Cursor: run j, its next point s and its end e (a lane that is not ok
     // starts at the end).
     int j = ok ? 0 : kCells - 1;
@@ -1436,8 +1469,8 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     // second pass, which goes on from it.
     if (done || (grid_second_pass(D, K) && ok && worst < kFar)) {
         // Derived again rather than held through the scan.
-        const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
-        write_results<K, D>(a, out.out_row, best, 0, out.pstart);
+        const QueryLoc out = locate<kOrdered, false, kRouted, true>(a, gid);
+        write_results<K, D>(a, out.out_row, best, out.index_offset, out.pstart);
     }
     grid_append(list, counts, seg, __ballot(valid && !done), gid);
     if (valid && !done) bounds[gid] = ok ? worst : kFar;
@@ -1464,14 +1497,16 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
 // first list back instead of scanning the inner block again: this pass
 // 81 -> 63 us at cfg2 (the call 0.379 -> 0.378 ms; 3-D k = 8 0.306 ->
 // 0.294 ms); it waits on memory more than it computes.
+// Routed (kRouted) as in the first pass: each lane takes its route's
+// structure, and the list read back has its indices offset.
 constexpr int kGridRuns2 = 32;  // kept shell cells per lane (more: the traversal)
-template <int D, int K, bool kOrdered>
+template <int D, int K, bool kOrdered, bool kRouted>
 __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const float* __restrict__ node_aabbs,
                                                           int64_t nr, int level, const int32_t* __restrict__ table,
                                                           const int32_t* __restrict__ list,
                                                           const uint32_t* __restrict__ counts,
                                                           int32_t* __restrict__ list2, uint32_t* __restrict__ counts2,
-                                                          int64_t seg, float* __restrict__ bounds) {
+                                                          int64_t seg, float* __restrict__ bounds, GridSecond g2) {
     using Order = NearOrder<D, 2>;
     constexpr int kCells = Order::kCells;
     __shared__ uint32_t s_runs[kGridRuns2 * kKnnBlock];
@@ -1493,23 +1528,25 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
     }
     QueryLoc in{};
     if (ok) {
-        in = locate<kOrdered, false, false, true>(a, gid);
+        in = locate<kOrdered, false, kRouted, true>(a, gid);
         ok = in.row >= 0;
     }
-    const int n = a.num_leaves;
+    const bool second = kRouted && in.second;
+    const int n = kRouted ? in.n : a.num_leaves;
     const int64_t b = ok ? gid / a.M : 0;
     float q[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) q[d] = ok ? a.queries[in.row * D + d] : 0.0f;
-    const float* root = node_aabbs + b * nr * 2 * D;
+    const float* root = second ? g2.nodes + b * g2.nr * 2 * D : node_aabbs + b * nr * 2 * D;
     float lo[D], hi[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         lo[d] = root[d];
         hi[d] = root[D + d];
     }
-    const int shift = grid_axis_bits<D>() - level;
-    const int G = 1 << level;
+    const int lv = second ? g2.level : level;
+    const int shift = grid_axis_bits<D>() - lv;
+    const int G = 1 << lv;
     uint32_t c[D];
     grid_cell<D>(q, lo, hi, shift, c);
     // Squared lower bounds of |p_d - q_d| for points in the cells at offset
@@ -1533,8 +1570,8 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
             }
         }
     }
-    const int64_t cells = int64_t(1) << (D * level);
-    const int32_t* t = table + b * (cells + 1);
+    const int64_t cells = int64_t(1) << (D * lv);
+    const int32_t* t = (second ? g2.table : table) + b * (cells + 1);
     constexpr Order kOrder{};
     // The kept cells' ids first (no loads), then their table entries in
     // batches of 8 whose loads issue together (loading under each cell's
@@ -1616,16 +1653,19 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn2_kernel(KnnArgs a, const f
 #pragma unroll
             for (int i = 0; i < K; ++i) rd[i] = od[i];
         }
+        // A routed list was written with its route's index offset.
+        const uint32_t off = static_cast<uint32_t>(in.index_offset);
 #pragma unroll
-        for (int i = 0; i < K; ++i) best[i] = ok ? candidate_key(rd[i], ri[i]) : kEmptyKey;
+        for (int i = 0; i < K; ++i) best[i] = ok ? candidate_key(rd[i], ri[i] - off) : kEmptyKey;
     }
-    grid_stream<D, K>(s_runs + lane, ok ? nruns : 0, static_cast<const float4*>(a.accel) + in.pstart, q, best);
+    grid_stream<D, K>(s_runs + lane, ok ? nruns : 0, static_cast<const float4*>(second ? a.accel2 : a.accel) + in.pstart,
+                      q, best);
     const float safe = grid_safe_margin<D>(q, root, c, shift, G, 2);
     const float worst = __uint_as_float(static_cast<uint32_t>(best[K - 1] >> 32));
     const bool done = ok && safe > 0.0f && worst < safe * safe;
     if (done) {
-        const QueryLoc out = locate<kOrdered, false, false, true>(a, gid);
-        write_results<K, D, true>(a, out.out_row, best, 0, out.pstart);
+        const QueryLoc out = locate<kOrdered, false, kRouted, true>(a, gid);
+        write_results<K, D, true>(a, out.out_row, best, out.index_offset, out.pstart);
     }
     grid_append(list2, counts2, seg, __ballot(valid && !done), gid);
     if (ok && !done) bounds[gid] = worst;
@@ -1740,26 +1780,29 @@ int grid_level(int64_t n, int D, int K) {
 }
 
 namespace {
-// Workspace: the cells' first-point tables, the clouds' flags, the two
-// failure lists' counts (kGridCounts each, kCountStride words apart), the
-// two lists (kGridCounts sub-lists of `seg` entries: the launch positions
-// of one XCD share's tiles of one residue mod kGridSubLists), the k-th
-// distance bounds.
+// Workspace: the cells' first-point tables (a routed search's second
+// structure's after the first's), the clouds' flags (B, or 2B routed), the
+// two failure lists' counts (kGridCounts each, kCountStride words apart),
+// the two lists (kGridCounts sub-lists of `seg` entries: the launch
+// positions of one XCD share's tiles of one residue mod kGridSubLists), the
+// k-th distance bounds.  level2 = 0: not routed.
 struct GridLayout {
-    size_t table, flags, counts, list, list2, bounds, total;
+    size_t table, table2, flags, counts, list, list2, bounds, total;
     int64_t seg;
 };
-GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
+GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D, int level2) {
     auto up = [](size_t x) { return (x + 255) / 256 * 256; };
     const size_t cells = size_t(1) << (D * level);
+    const size_t cells2 = level2 > 0 ? size_t(1) << (D * level2) : 0;
     const int64_t tiles = (total_q + kKnnBlock - 1) / kKnnBlock;
     const int64_t per_xcd = (tiles + kXcds - 1) / kXcds;
     GridLayout g;
     g.seg = (per_xcd + kGridSubLists - 1) / kGridSubLists * kKnnBlock;
     const size_t list_bytes = static_cast<size_t>(kGridCounts * g.seg) * 4;
     g.table = 0;
-    g.flags = up(g.table + static_cast<size_t>(B) * (cells + 1) * 4);
-    g.counts = up(g.flags + static_cast<size_t>(B) * 4);
+    g.table2 = up(g.table + static_cast<size_t>(B) * (cells + 1) * 4);
+    g.flags = up(g.table2 + (level2 > 0 ? static_cast<size_t>(B) * (cells2 + 1) * 4 : 0));
+    g.counts = up(g.flags + static_cast<size_t>(B) * (level2 > 0 ? 2 : 1) * 4);
     g.list = up(g.counts + static_cast<size_t>(2 * kGridCounts * kCountStride) * 4);
     g.list2 = up(g.list + list_bytes);
     g.bounds = up(g.list2 + list_bytes);
@@ -1768,43 +1811,65 @@ GridLayout grid_layout(int64_t B, int64_t total_q, int level, int D) {
 }
 
 // Pass 1 (pass == 1: failures to `list`) or pass 2 (over `list`, failures
-// to `list2`).
+// to `list2`).  Routed launches are ordered (the routed sort).
 template <int D, int K>
 void launch_grid_dk(const KnnArgs& a, int pass, const float* node_aabbs, int64_t nr, int level, int32_t* table,
                     uint32_t* flags, int32_t* list, uint32_t* counts, int32_t* list2, uint32_t* counts2, int64_t seg,
-                    float* bounds, hipStream_t stream) {
+                    float* bounds, const GridSecond& g2, hipStream_t stream) {
     const int64_t tiles = (a.total_q + kKnnBlock - 1) / kKnnBlock;
     const unsigned grid = static_cast<unsigned>((tiles + kXcds - 1) / kXcds * kXcds);
     const bool ordered = a.order != nullptr;
+    const bool routed = a.routes != nullptr;
     if (pass == 1) {
-        if (ordered) {
-            grid_knn_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, list,
-                                                                         counts, seg, bounds);
+        if (routed) {
+            grid_knn_kernel<D, K, true, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags,
+                                                                             list, counts, seg, bounds, g2);
+        } else if (ordered) {
+            grid_knn_kernel<D, K, true, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags,
+                                                                              list, counts, seg, bounds, g2);
         } else {
-            grid_knn_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags, list,
-                                                                          counts, seg, bounds);
+            grid_knn_kernel<D, K, false, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, flags,
+                                                                               list, counts, seg, bounds, g2);
         }
+    } else if (routed) {
+        grid_knn2_kernel<D, K, true, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list,
+                                                                          counts, list2, counts2, seg, bounds, g2);
     } else if (ordered) {
-        grid_knn2_kernel<D, K, true><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, counts,
-                                                                      list2, counts2, seg, bounds);
+        grid_knn2_kernel<D, K, true, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list,
+                                                                           counts, list2, counts2, seg, bounds, g2);
     } else {
-        grid_knn2_kernel<D, K, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list, counts,
-                                                                       list2, counts2, seg, bounds);
+        grid_knn2_kernel<D, K, false, false><<<grid, kKnnBlock, 0, stream>>>(a, node_aabbs, nr, level, table, list,
+                                                                            counts, list2, counts2, seg, bounds, g2);
     }
+}
+
+template <int D>
+void launch_grid_table(const KnnArgs& a, const void* accel, int n, const float* node_aabbs, int64_t nr, int level,
+                       int32_t* table, uint32_t* flags, hipStream_t stream) {
+    const int64_t pts = a.B * static_cast<int64_t>(n);
+    const unsigned tgrid = static_cast<unsigned>((pts + kBlock - 1) / kBlock);
+    grid_table_kernel<D><<<tgrid, kBlock, 0, stream>>>(static_cast<const float4*>(accel), node_aabbs, nr, a.B, n,
+                                                       level, table, flags);
 }
 }  // namespace
 
-size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D) {
-    return grid_layout(B, total_q, level, D).total;
+size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D, int level2) {
+    return grid_layout(B, total_q, level, D, level2).total;
 }
 
 hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t nr, int level, int D, int K,
-                           void* ws, hipStream_t stream) {
+                           void* ws, hipStream_t stream, const float* node_aabbs2, int64_t nr2, int level2) {
     if (args.total_q == 0) return hipSuccess;
-    if (level < 2 || args.routes != nullptr || args.total_q >= (int64_t(1) << 31) || args.M <= 0) {
+    if (level < 2 || args.total_q >= (int64_t(1) << 31) || args.M <= 0) return hipErrorInvalidValue;
+    const bool routed = args.routes != nullptr;
+    // A routed search is ordered with spatial output (the routed binding's)
+    // and has both structures' grids; a plain one has no second structure.
+    if (routed && (args.order == nullptr || !args.spatial_output || args.out_positions != nullptr ||
+                   level2 < 2 || node_aabbs2 == nullptr || args.accel2 == nullptr)) {
         return hipErrorInvalidValue;
     }
-    const GridLayout g = grid_layout(args.B, args.total_q, level, D);
+    if (!routed && level2 != 0) return hipErrorInvalidValue;
+    const GridLayout g = grid_layout(args.B, args.total_q, level, D, level2);
     char* base = static_cast<char*>(ws);
     int32_t* table = reinterpret_cast<int32_t*>(base + g.table);
     uint32_t* flags = reinterpret_cast<uint32_t*>(base + g.flags);
@@ -1813,19 +1878,25 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
     int32_t* list = reinterpret_cast<int32_t*>(base + g.list);
     int32_t* list2 = reinterpret_cast<int32_t*>(base + g.list2);
     float* bounds = reinterpret_cast<float*>(base + g.bounds);
-    const int n = args.num_leaves;
-    const int64_t init = std::max<int64_t>(args.B, 2 * kGridCounts);
-    grid_init_kernel<<<static_cast<unsigned>((init + kBlock - 1) / kBlock), kBlock, 0, stream>>>(flags, args.B, counts,
+    const GridSecond g2{node_aabbs2, nr2, level2, reinterpret_cast<const int32_t*>(base + g.table2)};
+    const int64_t nflags = args.B * (routed ? 2 : 1);
+    const int64_t init = std::max<int64_t>(nflags, 2 * kGridCounts);
+    grid_init_kernel<<<static_cast<unsigned>((init + kBlock - 1) / kBlock), kBlock, 0, stream>>>(flags, nflags, counts,
                                                                                                 2 * kGridCounts);
-    const int64_t pts = args.B * static_cast<int64_t>(n);
-    const unsigned tgrid = static_cast<unsigned>((pts + kBlock - 1) / kBlock);
-    const float4* p4 = static_cast<const float4*>(args.accel);
-    if (D == 3) grid_table_kernel<3><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
-    else grid_table_kernel<2><<<tgrid, kBlock, 0, stream>>>(p4, node_aabbs, nr, args.B, n, level, table, flags);
+    auto tables = [&](auto tab) {
+        tab(args, args.accel, args.num_leaves, node_aabbs, nr, level, table, flags, stream);
+        if (routed) {
+            tab(args, args.accel2, args.num_leaves2, node_aabbs2, nr2, level2,
+                reinterpret_cast<int32_t*>(base + g.table2), flags + args.B, stream);
+        }
+    };
+    if (D == 3) tables(launch_grid_table<3>);
+    else tables(launch_grid_table<2>);
     const int passes = grid_second_pass(D, K) ? 2 : 1;
     for (int pass = 1; pass <= passes; ++pass) {
         auto run = [&](auto dk) {
-            dk(args, pass, node_aabbs, nr, level, table, flags, list, counts, list2, counts2, g.seg, bounds, stream);
+            dk(args, pass, node_aabbs, nr, level, table, flags, list, counts, list2, counts2, g.seg, bounds, g2,
+               stream);
         };
         // k in {4, 8, 16, 32} (supported_k).
         if (D == 3) {
@@ -1850,7 +1921,7 @@ hipError_t launch_grid_knn(const KnnArgs& args, const float* node_aabbs, int64_t
     if (e != hipSuccess) return e;
     // The fallback: the accel traversal over the last list (its grid sized
     // for every query; work-groups past their segment's length exit at
-    // once).
+    // once), routed where the search is.
     KnnArgs f = args;
     f.fb_list = passes == 2 ? list2 : list;
     f.fb_bound = bounds;

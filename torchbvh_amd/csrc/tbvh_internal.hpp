@@ -442,17 +442,22 @@ struct KnnArgs {
 hipError_t launch_knn(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 hipError_t launch_knn_accel(const KnnArgs& a, int D, int K, bool ragged, hipStream_t stream);
 
-// Cell-block k-NN (batched accel, `a` as for launch_knn_accel without
-// routes; spatial output and neighbour rows as there): every cloud's accel points are
-// cut into the level-`level` Morton cells against its root box (row 0 of
-// its node_aabbs, `nr` rows per cloud); each query scans the 3^D cells
-// around its own and keeps the result when its k-th distance is inside the
+// Cell-block k-NN (batched accel, `a` as for launch_knn_accel; spatial
+// output and neighbour rows as there): every cloud's accel points are cut
+// into the level-`level` Morton cells against its root box (row 0 of its
+// node_aabbs, `nr` rows per cloud); each query scans the 3^D cells around
+// its own and keeps the result when its k-th distance is inside the
 // block's margin; the others run the accel traversal seeded with that
-// distance.  `ws` holds grid_workspace_bytes(B, total_q, level, D).
+// distance.  Routed (a.routes set: ordered, spatial output, no neighbour
+// rows): the false route's structure has its own boxes (node_aabbs2, nr2
+// rows per cloud) and level (level2 >= 2), and each query searches its
+// route's; level2 = 0 otherwise.  `ws` holds grid_workspace_bytes(B,
+// total_q, level, D, level2).
 int grid_level(int64_t n, int D, int K);
-size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D);
+size_t grid_workspace_bytes(int64_t B, int64_t total_q, int level, int D, int level2 = 0);
 hipError_t launch_grid_knn(const KnnArgs& a, const float* node_aabbs, int64_t nr, int level, int D, int K,
-                           void* ws, hipStream_t stream);
+                           void* ws, hipStream_t stream, const float* node_aabbs2 = nullptr, int64_t nr2 = 0,
+                           int level2 = 0);
 
 // Tile-count bound for S segments holding `total` rows in kSortTile tiles.
 inline int64_t tiles_bound(int64_t total, int64_t S) {
