@@ -1365,6 +1365,25 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
     constexpr int kGroup = 9;
     static_assert(kCells % kGroup == 0, "whole groups of cells");
     const bool searching = ok;
+    // Per axis, the block's three columns: inside the grid or not, and their
+    // Morton bits in the axis's place, so that a cell's id is the OR of its
+    // columns' bits (grid_cell_id) and its test two ANDs.  Deriving each
+    // cell's id from its coordinates took about 18 instructions per cell,
+    // two of them quarter-rate multiplies, under a branch per cell (this
+    // pass at cfg2 239.6 -> 228.4 us, 3-D k = 32 258.5 -> 241.6 us, cfg4
+    // 556.9 -> 546.5 us).
+    uint32_t col_bits[D][3];
+    bool col_in[D][3];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int x = static_cast<int>(c[d]) + k - 1;
+            col_in[d][k] = x >= 0 && x < G;
+            const uint32_t ux = static_cast<uint32_t>(x);
+            col_bits[d][k] = (D == 3 ? morton::spread3(ux) : morton::spread2(ux)) << d;
+        }
+    }
 #pragma unroll
     for (int g0 = 0; g0 < kCells; g0 += kGroup) {
         int32_t raw_s[kGroup], raw_e[kGroup];
@@ -1372,16 +1391,12 @@ __global__ __launch_bounds__(kKnnBlock) void grid_knn_kernel(KnnArgs a, const fl
 #pragma unroll
         for (int u = 0; u < kGroup; ++u) {
             const int o = kOrder.off[g0 + u];
-            const int x = static_cast<int>(c[0]) + Order::dx(o), y = static_cast<int>(c[1]) + Order::dy(o);
-            const int z = D == 3 ? static_cast<int>(c[D - 1]) + Order::dz(o) : 0;
-            in[u] = searching && x >= 0 && x < G && y >= 0 && y < G && z >= 0 && z < G;
-            uint32_t cell[D];
-            cell[0] = static_cast<uint32_t>(x);
-            cell[1] = static_cast<uint32_t>(y);
-            if constexpr (D == 3) cell[D - 1] = static_cast<uint32_t>(z);
-            const uint32_t id = in[u] ? grid_cell_id<D>(cell) : 0u;
-            raw_s[u] = t[id];
-            raw_e[u] = t[id + 1];
+            const int kx = Order::dx(o) + 1, ky = Order::dy(o) + 1, kz = D == 3 ? Order::dz(o) + 1 : 1;
+            in[u] = searching && col_in[0][kx] && col_in[1][ky] && (D == 2 || col_in[D - 1][kz]);
+            const uint32_t id = col_bits[0][kx] | col_bits[1][ky] | (D == 3 ? col_bits[D - 1][kz] : 0u);
+            const uint32_t at = in[u] ? id : 0u;
+            raw_s[u] = t[at];
+            raw_e[u] = t[at + 1];
         }
 #pragma unroll
         for (int u = 0; u < kGroup; ++u) {
